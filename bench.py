@@ -1,0 +1,335 @@
+"""Benchmark of the W8A16 decode GEMM on one MI355X.
+
+Default workload (one "step"): the four per-layer GEMMs of a dense GQA 27B-class transformer at M = 5
+tokens (1 verified + 4 draft): qkv K=5120 N=10240, o_proj K=8192 N=5120, gate_up K=5120 N=34816,
+down K=17408 N=5120; int8 [N, K] weights with fp32 per-channel scales |N(0,1)|*0.002+1e-4, bf16
+N(0,1) activations, synthetic and seeded.  Each step runs one layer's GEMMs from a hipGraph; the
+weights rotate over several distinct layers (more bytes than the 256 MB MALL), so every step streams
+its weights from HBM.  Output: one JSON line on stdout.
+
+  value        algorithmic bytes of all timed steps / wall time of the timed steps (GB/s)
+  roofline     the dominant kernel (gate_up): algorithmic bytes per launch / its mean duration from
+               HIP events on the launch stream; peak 8 TB/s; traffic from the committed rocprofv3
+               FETCH_SIZE / WRITE_SIZE summary when one exists for this workload
+  cpu_baseline the oracle's fp32-dequant restatement of the reference CPU path
+               (F.linear(x.float(), W.float() * s[:, None])) on a bounded sample, host cores
+
+Other modes: --workload stack64 (64 distinct layers, one hipGraph per decode step, activations
+re-normalised between layers); --profile-gemm NAME --iters N (only that GEMM, for rocprofv3);
+--copy-probe (a plain device copy of known size, for counter calibration).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "qwen-a100-fastpath_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "W8A16 GEMM HBM GB/s (% of 8 TB/s) + µs/layer at M=5, 27B shapes"
+PEAK_GBS = 8000.0
+M_TOKENS = 5
+GEMMS = {  # name: (N, K)
+    "qkv": (10240, 5120),
+    "o_proj": (5120, 8192),
+    "gate_up": (34816, 5120),
+    "down": (5120, 17408),
+}
+DOMINANT = "gate_up"
+PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "w8a16_gate_up_m5_pmc.txt")
+
+
+def algo_bytes(M: int, N: int, K: int) -> int:
+    """Compulsory bytes: int8 weights + fp32 scales + bf16 activations + bf16 outputs."""
+    return N * K + 4 * N + 2 * M * K + 2 * M * N
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Layer:
+    """One layer's four weight sets plus fixed activations."""
+
+    def __init__(self, torch, dev, seed: int, M: int):
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        self.w, self.s, self.x = {}, {}, {}
+        for name, (N, K) in GEMMS.items():
+            w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+            self.w[name] = w.t()  # [K, N] view with stride (1, K), as vLLM holds it
+            self.s[name] = (torch.randn(N, device=dev, generator=g).abs() * 0.002 + 1e-4).float()
+            self.x[name] = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+
+
+def capture(torch, fn):
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn()
+    torch.cuda.synchronize()
+    return g, out
+
+
+def read_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 summary, if any."""
+    try:
+        text = open(PROFILE_SUMMARY).read()
+    except OSError:
+        return None
+    f = re.search(r"^fetch_bytes_per_launch:\s*([0-9.eE+]+)", text, re.M)
+    w = re.search(r"^write_bytes_per_launch:\s*([0-9.eE+]+)", text, re.M)
+    if not (f and w):
+        return None
+    return float(f.group(1)) + float(w.group(1))
+
+
+def cpu_baseline(M: int, seed: int = 0):
+    """Time the oracle's fp32-dequant restatement of the reference CPU path on one layer's GEMMs."""
+    import numpy as np
+    from oracle import oracle as O
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, 16))
+    try:
+        from threadpoolctl import threadpool_limits
+        limiter = threadpool_limits(limits=cores)
+    except Exception:  # noqa: BLE001 - threadpoolctl optional
+        limiter = None
+    inputs = [O.gen_inputs(M, N, K, seed=seed + i) for i, (N, K) in enumerate(GEMMS.values())]
+    total_bytes = sum(algo_bytes(M, N, K) for (N, K) in GEMMS.values())
+    best = float("inf")
+    for rep in range(3):
+        t0 = time.perf_counter()
+        for inp in inputs:
+            O.fp32_dequant_linear(inp.x, inp.w, inp.s)
+        best = min(best, time.perf_counter() - t0)
+    if limiter is not None:
+        limiter.unregister() if hasattr(limiter, "unregister") else None
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(total_bytes / best / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"one layer's 4 GEMMs at M={M} (qkv, o_proj, gate_up, down; {total_bytes / 1e6:.1f} MB), "
+                   f"best of 3, numpy fp32 BLAS over {cores} threads: {best * 1e3:.1f} ms/layer"
+                   + (f"; {cpu_model}" if cpu_model else "")),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--workload", choices=["layer", "stack64"], default="layer")
+    ap.add_argument("--layers", type=int, default=4, help="distinct layers rotated through (layer workload)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--profile-gemm", choices=list(GEMMS), default=None)
+    ap.add_argument("--iters", type=int, default=200)
+    ap.add_argument("--copy-probe", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        log("bench.py: this build measures one GPU only (the op is single-GPU; see DESIGN.md for how it "
+            "would shard); run with --gpus 1")
+        sys.exit(2)
+
+    import torch
+    import qwen_fastpath as qf
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    if args.copy_probe:
+        n = 1 << 30
+        a = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        b = torch.empty_like(a)
+        for _ in range(args.iters):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log(f"copy probe: {args.iters} copies of {n} bytes")
+        return
+
+    if args.profile_gemm:
+        N, K = GEMMS[args.profile_gemm]
+        sets = [Layer(torch, dev, 1000 + i, M_TOKENS) for i in range(args.layers)]
+        for i in range(args.iters):
+            L_ = sets[i % len(sets)]
+            qf.w8a16_mm(L_.x[args.profile_gemm], L_.w[args.profile_gemm], L_.s[args.profile_gemm], None,
+                        torch.bfloat16)
+        torch.cuda.synchronize()
+        log(f"profile: {args.iters} launches of {args.profile_gemm} M={M_TOKENS} N={N} K={K} "
+            f"cfg={tuple(qf.resolve_config(M_TOKENS, N, K))}")
+        return
+
+    if args.workload == "stack64":
+        run_stack64(torch, qf, dev, args)
+        return
+
+    M = M_TOKENS
+    R = max(1, args.layers)
+    log(f"bench: allocating {R} layers ({R * sum(N * K for N, K in GEMMS.values()) / 1e9:.2f} GB of int8 weights)")
+    layers = [Layer(torch, dev, 1000 + i, M) for i in range(R)]
+    bytes_per_step = sum(algo_bytes(M, N, K) for (N, K) in GEMMS.values())
+
+    def step_fn(L_):
+        return lambda: [qf.w8a16_mm(L_.x[n], L_.w[n], L_.s[n], None, torch.bfloat16) for n in GEMMS]
+
+    graphs = [capture(torch, step_fn(L_))[0] for L_ in layers]
+
+    for i in range(args.warmup):
+        graphs[i % R].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        graphs[i % R].replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    value = args.steps * bytes_per_step / elapsed / 1e9
+    ms_per_step = elapsed / args.steps * 1e3
+    log(f"bench: {args.steps} steps in {elapsed * 1e3:.1f} ms: {ms_per_step * 1e3:.2f} us/layer, {value:.0f} GB/s "
+        f"({100 * value / PEAK_GBS:.1f}% of 8 TB/s)")
+
+    # per-GEMM times: a graph of 8 x R launches of one GEMM, weights rotating; HIP events on the
+    # current stream around each replay
+    per_gemm = {}
+    dominant_us = None
+    for name, (N, K) in GEMMS.items():
+        reps = 8
+        g, _ = capture(torch, lambda n=name: [qf.w8a16_mm(L_.x[n], L_.w[n], L_.s[n], None, torch.bfloat16)
+                                              for _ in range(reps) for L_ in layers])
+        launches = reps * R
+        g.replay()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(10):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g.replay()
+            e1.record()
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3 / launches)
+        us = sorted(times)[len(times) // 2]
+        b = algo_bytes(M, N, K)
+        cfg = qf.resolve_config(M, N, K)
+        per_gemm[name] = {"N": N, "K": K, "us": round(us, 2), "GB_s": round(b / us / 1e3, 1),
+                          "pct_peak": round(100 * b / us / 1e3 / PEAK_GBS, 1), "config": list(cfg)}
+        log(f"  {name:8s} N={N:6d} K={K:6d}: {us:7.2f} us  {b / us / 1e3:7.0f} GB/s  "
+            f"{100 * b / us / 1e3 / PEAK_GBS:5.1f}%  cfg={tuple(cfg)}")
+        if name == DOMINANT:
+            dominant_us = us
+        del g
+
+    dom_bytes = algo_bytes(M, *GEMMS[DOMINANT])
+    achieved = dom_bytes / dominant_us / 1e3
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_GBS, 4), "traffic": read_traffic(),
+                "kernel": f"{DOMINANT} M={M} N={GEMMS[DOMINANT][0]} K={GEMMS[DOMINANT][1]}",
+                "algorithmic_bytes_per_launch": dom_bytes, "mean_launch_us": round(dominant_us, 2)}
+
+    cpu = None if args.no_cpu else cpu_baseline(M)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded int8 weights, fp32 scales, bf16 N(0,1) activations)",
+        "config": {"workload": "dense GQA 27B-class layer GEMMs at M=5: qkv 10240x5120, o_proj 5120x8192, "
+                               "gate_up 34816x5120, down 5120x17408 (N x K int8)",
+                   "M": M, "layers_rotated": R, "bytes_per_step": bytes_per_step,
+                   "timing": "one hipGraph per layer, replayed; weights rotate over distinct layers"},
+        "us_per_layer": round(ms_per_step * 1e3, 2),
+        "pct_of_peak": round(100 * value / PEAK_GBS, 2),
+        "per_gemm": per_gemm,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def run_stack64(torch, qf, dev, args):
+    """64 layers x 4 GEMMs at M=5 with distinct weights, one hipGraph per decode step.  Glue between
+    GEMMs: o_proj reads the first 8192 qkv outputs, down reads silu(gate) * up; each GEMM input is
+    re-normalised to unit RMS per row."""
+    M = M_TOKENS
+    nl = 64
+    log(f"stack64: allocating {nl} layers ({nl * sum(N * K for N, K in GEMMS.values()) / 1e9:.1f} GB)")
+    layers = [Layer(torch, dev, 5000 + i, M) for i in range(nl)]
+    x0 = torch.randn(M, 5120, device=dev).to(torch.bfloat16)
+
+    def rms(t):
+        t = t.float()
+        return (t * torch.rsqrt(t.pow(2).mean(dim=-1, keepdim=True))).to(torch.bfloat16)
+
+    def step():
+        h = x0
+        for L_ in layers:
+            qkv = qf.w8a16_mm(h, L_.w["qkv"], L_.s["qkv"], None, torch.bfloat16)
+            o = qf.w8a16_mm(rms(qkv[:, :8192]), L_.w["o_proj"], L_.s["o_proj"], None, torch.bfloat16)
+            gu = qf.w8a16_mm(rms(o), L_.w["gate_up"], L_.s["gate_up"], None, torch.bfloat16)
+            g, u = gu[:, :17408].float(), gu[:, 17408:].float()
+            d = qf.w8a16_mm(rms(torch.nn.functional.silu(g) * u), L_.w["down"], L_.s["down"], None,
+                            torch.bfloat16)
+            h = rms(d)
+        return h
+
+    g, _ = capture(torch, step)
+    bytes_per_step = nl * sum(algo_bytes(M, N, K) for (N, K) in GEMMS.values())
+    for _ in range(max(1, args.warmup // 10)):
+        g.replay()
+    torch.cuda.synchronize()
+    steps = max(1, args.steps // 50)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.replay()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    value = steps * bytes_per_step / el / 1e9
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps,
+        "warmup": max(1, args.warmup // 10), "ms_per_step": round(el / steps * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded int8 weights, fp32 scales, bf16 activations)",
+        "config": {"workload": "64-layer decode-step linear stack at M=5 (4 GEMMs/layer, distinct weights, "
+                               "unit-RMS glue), one hipGraph per step", "M": M, "layers": nl,
+                   "bytes_per_step": bytes_per_step},
+        "us_per_layer": round(el / steps / nl * 1e6, 2),
+        "pct_of_peak": round(100 * value / PEAK_GBS, 2),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,134 @@
+/*
+ * qf_w8a16.h — C ABI of the MI355X (gfx950) W8A16 decode GEMM.
+ *
+ *   y[m, n] = bf16_rne( scale[n] * sum_k x[m, k] * w[n, k] )      m < M <= 16
+ *
+ * x is bf16 [M, K] (row stride ldx elements, unit column stride), w is int8 [N, K] row-major
+ * (the W8A8 checkpoint layout; the [K, N] column-major view vLLM keeps for CUTLASS is the same
+ * memory), scale is fp32 per output channel [N], y is bf16 (or fp32) [M, N] with row stride ldy.
+ * Accumulation is fp32; the scale is applied after the K reduction; split-K partial sums are
+ * reduced in a fixed order by a second pass, so results are bitwise reproducible run to run.
+ *
+ * The ABI uses only plain pointers and sizes.  `stream` is a hipStream_t (NULL = the null stream).
+ * No entry point allocates, frees, synchronises or retains a pointer after it returns, so every
+ * launch entry point may be recorded into a HIP graph.  Errors are returned as qf_status codes;
+ * QF_ERR_UNSUPPORTED means "this shape/layout is not handled here, use the fallback path", which
+ * is how the reference's `pick_config(...) is None` branch is expressed.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   qf_w8a16_gemm            <- w8a16_mm + _w8a16_kernel   plugin/qwen_fastpath/w8a16.py:15-44,71-83
+ *   qf_w8a16_pick_config     <- pick_config / TUNED / SMALL_M   plugin/qwen_fastpath/w8a16.py:12,47-68
+ *   qf_w8a16_workspace_bytes <- the fp32 split-K buffer torch.zeros   plugin/qwen_fastpath/w8a16.py:78-79
+ *   qf_quantize_rows_int8    <- draft-head per-row quantizer   plugin/qwen_fastpath/patches.py:139-147
+ *   qf_argmax_rows_bf16      <- pad mask + argmax of draft logits   plugin/qwen_fastpath/patches.py:182-185
+ *   qf_w8a16_repack / qf_w8a16_unpack: load-time weight layout change (no reference counterpart;
+ *                              the reference streams the checkpoint layout as is, w8a16.py:1-7)
+ */
+#ifndef QF_W8A16_H
+#define QF_W8A16_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QF_W8A16_ABI_VERSION 1
+
+/* Largest M handled (the reference's SMALL_M, plugin/qwen_fastpath/w8a16.py:12). */
+#define QF_W8A16_MAX_M 16
+/* K must be a multiple of this (the reference's smallest BLOCK_K, w8a16.py:63-68). */
+#define QF_W8A16_K_ALIGN 64
+
+typedef enum qf_status {
+  QF_OK = 0,
+  QF_ERR_INVALID_ARG = 1,  /* null pointer, negative size, bad enum */
+  QF_ERR_UNSUPPORTED = 2,  /* valid request this library does not serve: caller falls back */
+  QF_ERR_WORKSPACE = 3,    /* workspace missing or smaller than qf_w8a16_workspace_bytes() */
+  QF_ERR_HIP = 4           /* a HIP runtime call failed (launch error) */
+} qf_status;
+
+/* Weight layouts. */
+typedef enum qf_layout {
+  QF_LAYOUT_ROWMAJOR = 0,  /* int8 [N, K], row stride ldw bytes: the checkpoint / CUTLASS layout */
+  QF_LAYOUT_TILED = 1      /* pre-permuted 1 KiB tiles (16 rows x 64 k), see qf_w8a16_repack */
+} qf_layout;
+
+typedef enum qf_dtype { QF_DTYPE_BF16 = 0, QF_DTYPE_F32 = 1 } qf_dtype;
+
+typedef enum qf_kernel {
+  QF_KERNEL_AUTO = 0,  /* pick by shape and M */
+  QF_KERNEL_GEMV = 1,  /* wavefront-reduction GEMV, M <= 4, row-major layout only */
+  QF_KERNEL_MFMA = 2   /* v_mfma_f32_16x16x32_bf16 tiles, M <= 16, both layouts */
+} qf_kernel;
+
+/* Launch configuration.  A zero field means "choose automatically". */
+typedef struct qf_w8a16_config {
+  int32_t kernel;          /* qf_kernel */
+  int32_t split_k;         /* K splits across workgroups (deterministic second-pass reduction) */
+  int32_t tiles_per_wave;  /* MFMA: 16-row n-tiles per wavefront; GEMV: rows per wavefront */
+  int32_t waves;           /* wavefronts per workgroup */
+  int32_t depth;           /* weight prefetch depth in k-steps (MFMA) */
+  int32_t load_hint;       /* 0: default weight loads, 1: non-temporal (streaming) loads */
+  int32_t reserved[2];
+} qf_w8a16_config;
+
+/* ABI version of the loaded library (QF_W8A16_ABI_VERSION). */
+int qf_abi_version(void);
+
+/* Static text for a qf_status value. */
+const char* qf_status_string(int status);
+
+/* Fill *cfg with the configuration used for (M, N, K, layout).  Returns QF_ERR_UNSUPPORTED when the
+ * shape is not served (M outside 1..16, K % 64 != 0, TILED with N % 16 != 0), mirroring
+ * pick_config() returning None.  Host-only; touches no device. */
+int qf_w8a16_pick_config(int M, int N, int K, int layout, qf_w8a16_config* cfg);
+
+/* Bytes of device workspace qf_w8a16_gemm needs for this call (0 when split_k == 1).
+ * cfg may be NULL (automatic configuration).  Host-only. */
+size_t qf_w8a16_workspace_bytes(int M, int N, int K, int layout, const qf_w8a16_config* cfg);
+
+/* y = bf16/fp32( scale * (x . w^T) ).  cfg may be NULL.  Alignment contract: x, w, scale 16-byte
+ * aligned, ldx % 8 == 0, ldw % 16 == 0 (row-major layout) and y 16-byte aligned; otherwise
+ * QF_ERR_UNSUPPORTED.  Any ldy >= N works (vector stores when ldy % 4 == 0).  The workspace (if
+ * any) is fully overwritten before it is read, so it needs no clearing. */
+int qf_w8a16_gemm(const uint16_t* x, int64_t ldx,
+                  const int8_t* w, int64_t ldw, int layout,
+                  const float* scale,
+                  void* y, int64_t ldy, int out_dtype,
+                  int M, int N, int K,
+                  const qf_w8a16_config* cfg,
+                  void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/* Size in bytes of the TILED image of an [N, K] weight (N rounded up to 16). */
+size_t qf_w8a16_tiled_bytes(int N, int K);
+
+/* Row-major int8 [N, K] (row stride ldw) -> TILED image (qf_w8a16_tiled_bytes bytes, pad rows 0).
+ * Out of place; K % 64 == 0. */
+int qf_w8a16_repack(const int8_t* w_rowmajor, int64_t ldw, int8_t* w_tiled,
+                    int N, int K, void* stream);
+
+/* Inverse of qf_w8a16_repack (drops pad rows). */
+int qf_w8a16_unpack(const int8_t* w_tiled, int8_t* w_rowmajor, int64_t ldw,
+                    int N, int K, void* stream);
+
+/* Per-row symmetric int8 quantisation of a bf16 [V, H] matrix (row stride ldw elements):
+ *   s[v] = max(max_h |w[v,h]|, 1e-8) / 127   (fp32, IEEE division)
+ *   q[v,h] = clamp(round_half_even(w[v,h] / s[v]), -127, 127)
+ * q is int8 [V, H] row-major (row stride H).  Reference: plugin/qwen_fastpath/patches.py:139-147. */
+int qf_quantize_rows_int8(const uint16_t* w, int64_t ldw, int8_t* q, float* s,
+                          int V, int H, void* stream);
+
+/* Row argmax of bf16 logits [M, N] (row stride ld): columns >= n_valid count as -inf (the padded
+ * vocabulary), ties go to the lowest index, NaN counts as the maximum (torch.argmax semantics).
+ * out[m] = index + index_offset (int64).  Reference: plugin/qwen_fastpath/patches.py:182-185. */
+int qf_argmax_rows_bf16(const uint16_t* logits, int64_t ld, int M, int N, int n_valid,
+                        int64_t index_offset, int64_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QF_W8A16_H */

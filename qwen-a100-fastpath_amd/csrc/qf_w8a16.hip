@@ -1,0 +1,798 @@
+// qf_w8a16.hip — gfx950 (MI355X) kernels and C ABI of the W8A16 decode GEMM.
+//
+//   y[m, n] = bf16_rne( s[n] * sum_k x[m, k] * w[n, k] ),   x bf16 [M, K], w int8 [N, K], s fp32 [N]
+//
+// The arithmetic follows the reference Triton kernel (plugin/qwen_fastpath/w8a16.py:15-44): int8
+// weights are widened to bf16 exactly (|w| <= 128 needs 8 significant bits), products are
+// accumulated in fp32, the per-channel scale is applied once after the K reduction, and the result
+// is rounded to bf16 with round-to-nearest-even.  Where the reference reduces split-K partials with
+// fp32 atomics (w8a16.py:43-44, order-dependent), this file writes the partials to a workspace and
+// sums them in split order in a second kernel, so every result is bitwise reproducible.
+//
+// Two kernels compute the product:
+//   * mfma: v_mfma_f32_16x16x32_bf16 over 1 KiB weight fragments (16 output channels x 64 k).  The
+//     weight fragment is the A operand (rows = output channels), the activation fragment the B
+//     operand (columns = tokens, padded to 16), so one lane ends with 4 consecutive output
+//     channels of one token and stores them as one 8-byte write.  Serves M = 1..16.
+//   * gemv: wavefront reduction.  Each wavefront streams RPW weight rows with 16 bytes per lane
+//     (1 KiB per row per step), multiplies on the VALU in fp32 and reduces across the 64 lanes at
+//     the end.  Serves M = 1..4 on the row-major layout.
+// Both stage the workgroup's slice of x in LDS once and read it from there; weights are loaded
+// with 128-bit global loads, dequantised in registers and never written anywhere.
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "qf_w8a16.h"
+
+namespace qf {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+constexpr int kTileN = 16;     // output channels per MFMA tile
+constexpr int kStepK = 64;     // k covered by one 16-byte-per-lane weight fragment of a tile
+constexpr size_t kMaxLds = 65536;
+
+struct GemmArgs {
+  const uint16_t* x;
+  const int8_t* w;
+  const float* scale;
+  void* y;
+  float* partial;  // [split_k][M][n_pad] fp32 when split_k > 1
+  int64_t ldx;
+  int64_t ldw;
+  int64_t ldy;
+  int M, N, K;
+  int n_pad;       // N rounded up to a multiple of 16
+  int ksteps;      // K / 64
+  int split_k;
+  int out_f32;
+  int vec_out;     // rows of y are 8-byte (bf16) / 16-byte (fp32) aligned: vector stores allowed
+};
+
+// ---------------------------------------------------------------------------------------------
+// small device helpers
+// ---------------------------------------------------------------------------------------------
+
+// Upper halves of two fp32 patterns -> one dword of two bf16 (lo in bits 0..15).  Exact when the
+// low 16 bits are zero, which holds for every integer of magnitude <= 256.
+__device__ __forceinline__ uint32_t pack_upper16(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// 4 int8 (one dword, little endian) -> 4 bf16 in two dwords.  Each byte is sign-extended and
+// converted by one v_cvt_f32_i32 with a byte-select source operand.
+__device__ __forceinline__ void i8x4_to_bf16x4(uint32_t d, uint32_t& lo, uint32_t& hi) {
+  const int32_t s = (int32_t)d;
+  const float f0 = (float)(int8_t)(s & 0xff);
+  const float f1 = (float)(int8_t)((s >> 8) & 0xff);
+  const float f2 = (float)(int8_t)((s >> 16) & 0xff);
+  const float f3 = (float)(s >> 24);
+  lo = pack_upper16(f0, f1);
+  hi = pack_upper16(f2, f3);
+}
+
+// 16 int8 weights (k..k+15 of one row) -> two bf16x8 MFMA operands (k..k+7, k+8..k+15).
+__device__ __forceinline__ void dequant16(const u32x4_t v, bf16x8_t& a0, bf16x8_t& a1) {
+  u32x4_t o0, o1;
+  uint32_t t0, t1;
+  i8x4_to_bf16x4(v.x, t0, t1); o0.x = t0; o0.y = t1;
+  i8x4_to_bf16x4(v.y, t0, t1); o0.z = t0; o0.w = t1;
+  i8x4_to_bf16x4(v.z, t0, t1); o1.x = t0; o1.y = t1;
+  i8x4_to_bf16x4(v.w, t0, t1); o1.z = t0; o1.w = t1;
+  a0 = __builtin_bit_cast(bf16x8_t, o0);
+  a1 = __builtin_bit_cast(bf16x8_t, o1);
+}
+
+// Two fp32 -> two bf16 (round to nearest even) packed in a dword.
+__device__ __forceinline__ uint32_t pack_bf16_rne(float a, float b) {
+  bf16x2_t v;
+  v.x = (__bf16)a;
+  v.y = (__bf16)b;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ uint16_t bf16_rne(float a) {
+  return __builtin_bit_cast(uint16_t, (__bf16)a);
+}
+
+template <bool kNonTemporal>
+__device__ __forceinline__ u32x4_t load16(const int8_t* p) {
+  const u32x4_t* q = reinterpret_cast<const u32x4_t*>(p);
+  if constexpr (kNonTemporal) {
+    return __builtin_nontemporal_load(q);
+  } else {
+    return *q;
+  }
+}
+
+// Store 4 consecutive outputs n..n+3 of one token row; `cnt` < 4 only at a ragged N tail.  Without
+// `vec` (a row stride that breaks vector alignment) every element is stored on its own.
+__device__ __forceinline__ void store_out4(void* y, int64_t ldy, int out_f32, int vec, int m, int n, int cnt,
+                                           f32x4_t v) {
+  const bool full = vec && cnt == 4;
+  if (out_f32) {
+    float* row = reinterpret_cast<float*>(y) + (int64_t)m * ldy + n;
+    if (full) {
+      *reinterpret_cast<f32x4_t*>(row) = v;
+    } else {
+      for (int i = 0; i < cnt; ++i) row[i] = v[i];
+    }
+  } else {
+    uint16_t* row = reinterpret_cast<uint16_t*>(y) + (int64_t)m * ldy + n;
+    if (full) {
+      u32x2_t p;
+      p.x = pack_bf16_rne(v.x, v.y);
+      p.y = pack_bf16_rne(v.z, v.w);
+      *reinterpret_cast<u32x2_t*>(row) = p;
+    } else {
+      for (int i = 0; i < cnt; ++i) row[i] = bf16_rne(v[i]);
+    }
+  }
+}
+
+__device__ __forceinline__ f32x4_t load_scale4(const float* scale, int N, int n) {
+  f32x4_t s = {0.f, 0.f, 0.f, 0.f};
+  if (n + 4 <= N) {
+    s = *reinterpret_cast<const f32x4_t*>(scale + n);
+  } else {
+    for (int i = 0; i < 4; ++i)
+      if (n + i < N) s[i] = scale[n + i];
+  }
+  return s;
+}
+
+// k-steps [begin, end) of split `split` out of `splits` over `ksteps` (balanced, deterministic).
+__device__ __forceinline__ void split_range(int split, int splits, int ksteps, int& begin, int& end) {
+  begin = (int)(((int64_t)split * ksteps) / splits);
+  end = (int)(((int64_t)(split + 1) * ksteps) / splits);
+}
+
+// ---------------------------------------------------------------------------------------------
+// MFMA kernel
+//
+// Workgroup = WAVES wavefronts; wavefront w owns NT consecutive 16-row n-tiles; blockIdx.y is the
+// K split.  Lane l (group g = l / 16, r = l % 16) loads, for every 64-k step s of the split:
+//   rowmajor: w[tile*16 + r][s*64 + 16g .. +15]
+//   tiled:    bytes [16 l, 16 l + 16) of the 1 KiB tile (tile, s), which hold the same values
+// and the activation chunk x[r][s*64 + 16g .. +15] from LDS (zero when r >= M).  Both MFMA operands
+// index k identically per lane, so the k order inside a step is immaterial to the product.
+// LDS holds x as [chunk c of 16 k][m][16 bf16] so that the 16 lanes of a group read 16
+// consecutive 32-byte pieces.
+// ---------------------------------------------------------------------------------------------
+template <int LAYOUT, int NT, int WAVES, int DEPTH, bool NTH>
+__global__ void __launch_bounds__(WAVES * kWave) w8a16_mfma_kernel(const GemmArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int g = lane >> 4;
+  const int r = lane & 15;
+  const int split = blockIdx.y;
+  int s_begin, s_end;
+  split_range(split, a.split_k, a.ksteps, s_begin, s_end);
+  const int nsteps = s_end - s_begin;
+  const int ntiles = a.n_pad / kTileN;
+  const int tile0 = (blockIdx.x * WAVES + wave) * NT;
+  const bool wave_active = tile0 < ntiles;
+
+  // Weight fragment pointers at step s_begin, and the byte stride between steps.
+  const int8_t* wp[NT];
+  constexpr int64_t step_bytes = (LAYOUT == QF_LAYOUT_ROWMAJOR) ? kStepK : kTileN * kStepK;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int tile = min(tile0 + t, ntiles - 1);
+    if constexpr (LAYOUT == QF_LAYOUT_ROWMAJOR) {
+      const int row = min(tile * kTileN + r, a.N - 1);
+      wp[t] = a.w + (int64_t)row * a.ldw + (int64_t)s_begin * kStepK + g * 16;
+    } else {
+      wp[t] = a.w + (((int64_t)tile * a.ksteps + s_begin) * kWave + lane) * 16;
+    }
+  }
+
+  // Issue the first DEPTH steps of weight loads before staging x, so the LDS fill overlaps them.
+  // Every load in this kernel is unconditional: step indices past the split are clamped to its
+  // last step (an in-bounds re-read), and the matching activation fragment is the zero step, so
+  // those extra MFMAs add exactly 0.  This keeps the loop free of branches around loads, which
+  // lets the compiler keep DEPTH steps of loads in flight.
+  // The ring has DEPTH + 1 slots: at step s the load for step s + DEPTH goes into the slot freed at
+  // step s - 1, so it can be issued before step s's fragment is consumed.
+  constexpr int RING = DEPTH + 1;
+  u32x4_t buf[RING][NT];
+  if (wave_active) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      const int sd = min(d, nsteps - 1);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) buf[d][t] = load16<NTH>(wp[t] + sd * step_bytes);
+    }
+  }
+
+  // Stage x[0:M][kb:kb + 64*nsteps] into LDS: piece (m, c) = 32 bytes = k kb+16c .. +15 of row m,
+  // stored at ((c * M) + m) * 32.  One more step of zeros follows (the zero step).
+  {
+    const int nchunks = nsteps * 4;
+    const int total = a.M * nchunks;
+    const int64_t kb = (int64_t)s_begin * kStepK;
+    for (int i = threadIdx.x; i < total; i += WAVES * kWave) {
+      const int m = i / nchunks;
+      const int c = i - m * nchunks;
+      const u32x4_t* src = reinterpret_cast<const u32x4_t*>(a.x + (int64_t)m * a.ldx + kb + c * 16);
+      const u32x4_t v0 = src[0];
+      const u32x4_t v1 = src[1];
+      u32x4_t* dst = reinterpret_cast<u32x4_t*>(smem + ((size_t)c * a.M + m) * 32);
+      dst[0] = v0;
+      dst[1] = v1;
+    }
+    const u32x4_t z = {0u, 0u, 0u, 0u};
+    u32x4_t* zs = reinterpret_cast<u32x4_t*>(smem + (size_t)nchunks * a.M * 32);
+    for (int i = threadIdx.x; i < 4 * a.M * 2; i += WAVES * kWave) zs[i] = z;
+  }
+  __syncthreads();
+  if (!wave_active) return;
+
+  f32x4_t acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+
+  // Lanes with r >= M read the zero step at every step (stride 0).
+  const size_t xs_step = (size_t)4 * a.M * 32;  // 4 chunks per step
+  const bool xrow = r < a.M;
+  const uint8_t* xs = xrow ? smem + ((size_t)g * a.M + r) * 32 : smem + (size_t)nsteps * xs_step;
+  const size_t xs_stride = xrow ? xs_step : 0;
+
+  for (int base = 0; base < nsteps; base += RING) {
+#pragma unroll
+    for (int d = 0; d < RING; ++d) {
+      const int s = base + d;
+      const int sn = min(s + DEPTH, nsteps - 1);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) buf[(d + DEPTH) % RING][t] = load16<NTH>(wp[t] + (int64_t)sn * step_bytes);
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch issue ahead of this step's math
+      const int sx = min(s, nsteps);      // nsteps -> zero step
+      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(xs + (size_t)sx * xs_stride);
+      const bf16x8_t xb0 = __builtin_bit_cast(bf16x8_t, p[0]);
+      const bf16x8_t xb1 = __builtin_bit_cast(bf16x8_t, p[1]);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        bf16x8_t w0, w1;
+        dequant16(buf[d][t], w0, w1);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, xb0, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, xb1, acc[t], 0, 0, 0);
+      }
+    }
+  }
+
+  // Lane (g, r) holds C[n = tile*16 + 4g + i][m = r], i = 0..3.
+  if (r >= a.M) return;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int tile = tile0 + t;
+    if (tile >= ntiles) break;
+    const int n = tile * kTileN + 4 * g;
+    if (a.split_k == 1) {
+      if (n < a.N) {
+        const f32x4_t sc = load_scale4(a.scale, a.N, n);
+        store_out4(a.y, a.ldy, a.out_f32, a.vec_out, r, n, min(4, a.N - n), acc[t] * sc);
+      }
+    } else {
+      float* dst = a.partial + ((int64_t)split * a.M + r) * a.n_pad + n;
+      *reinterpret_cast<f32x4_t*>(dst) = acc[t];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// GEMV kernel (wavefront reduction), row-major layout, M = MM <= 4.
+//
+// Workgroup = WAVES wavefronts; wavefront w owns RPW consecutive rows; blockIdx.y is the K split.
+// x[0:MM][k-range] is staged in LDS row-major (bf16).  Each step covers 1024 k: lane l loads
+// k0 + 16 l .. +15 of each of its RPW rows and reads the matching 32 bytes of each x row.
+// ---------------------------------------------------------------------------------------------
+template <int MM, int RPW, int WAVES, bool NTH>
+__global__ void __launch_bounds__(WAVES * kWave) w8a16_gemv_kernel(const GemmArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int split = blockIdx.y;
+  int s_begin, s_end;
+  split_range(split, a.split_k, a.ksteps, s_begin, s_end);
+  const int klen = (s_end - s_begin) * kStepK;
+  const int64_t kb = (int64_t)s_begin * kStepK;
+  const int row0 = (blockIdx.x * WAVES + wave) * RPW;
+  const bool wave_active = row0 < a.N;
+
+  // Stage x rows (klen bf16 each) into LDS, 16 bytes per thread per iteration.
+  {
+    const int per_row = klen / 8;
+    const int total = MM * per_row;
+    for (int i = threadIdx.x; i < total; i += WAVES * kWave) {
+      const int m = i / per_row;
+      const int c = i - m * per_row;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(a.x + (int64_t)m * a.ldx + kb + c * 8);
+      *reinterpret_cast<u32x4_t*>(smem + ((size_t)m * klen + c * 8) * 2) = v;
+    }
+  }
+  __syncthreads();
+  if (!wave_active) return;
+
+  const int8_t* wrow[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int row = min(row0 + i, a.N - 1);
+    wrow[i] = a.w + (int64_t)row * a.ldw + kb + lane * 16;
+  }
+
+  float acc[RPW][MM];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i)
+#pragma unroll
+    for (int m = 0; m < MM; ++m) acc[i][m] = 0.f;
+
+  const int nq = (klen + 1023) / 1024;
+  u32x4_t cur[RPW];
+  if (lane * 16 < klen) {
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) cur[i] = load16<NTH>(wrow[i]);
+  }
+  for (int q = 0; q < nq; ++q) {
+    const int kofs = q * 1024 + lane * 16;
+    if (kofs >= klen) break;
+    u32x4_t nxt[RPW];
+    const bool more = kofs + 1024 < klen;
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < RPW; ++i) nxt[i] = load16<NTH>(wrow[i] + (int64_t)(q + 1) * 1024);
+    }
+    // activations for k = kofs .. kofs+15 as fp32
+    float xf[MM][16];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(smem + ((size_t)m * klen + kofs) * 2);
+      const u32x4_t h0 = p[0], h1 = p[1];
+      const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        xf[m][2 * j] = __uint_as_float(hw[j] << 16);
+        xf[m][2 * j + 1] = __uint_as_float(hw[j] & 0xffff0000u);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const uint32_t wd[4] = {cur[i].x, cur[i].y, cur[i].z, cur[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int32_t s = (int32_t)wd[j];
+        const float wf[4] = {(float)(int8_t)(s & 0xff), (float)(int8_t)((s >> 8) & 0xff),
+                             (float)(int8_t)((s >> 16) & 0xff), (float)(s >> 24)};
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+          for (int m = 0; m < MM; ++m) acc[i][m] = __builtin_fmaf(wf[b], xf[m][4 * j + b], acc[i][m]);
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < RPW; ++i) cur[i] = nxt[i];
+    }
+  }
+
+  // Butterfly reduction across the 64 lanes (fixed pattern: deterministic).
+#pragma unroll
+  for (int i = 0; i < RPW; ++i)
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      float v = acc[i][m];
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+      acc[i][m] = v;
+    }
+
+  // Lane i*MM + m writes row row0+i, token m.
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      if (lane == i * MM + m) {
+        const int n = row0 + i;
+        if (n < a.N) {
+          if (a.split_k == 1) {
+            const float v = acc[i][m] * a.scale[n];
+            if (a.out_f32)
+              reinterpret_cast<float*>(a.y)[(int64_t)m * a.ldy + n] = v;
+            else
+              reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.ldy + n] = bf16_rne(v);
+          } else {
+            a.partial[((int64_t)split * MM + m) * a.n_pad + n] = acc[i][m];
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Split-K second pass: y[m, n..n+3] = round(s[n] * sum_{j=0..SK-1} P[j][m][n]), summed in j order.
+// ---------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmArgs a) {
+  const int groups = a.n_pad / 4;
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= a.M * groups) return;
+  const int m = idx / groups;
+  const int n = (idx - m * groups) * 4;
+  if (n >= a.N) return;
+  const int64_t plane = (int64_t)a.M * a.n_pad;
+  const float* p = a.partial + (int64_t)m * a.n_pad + n;
+  f32x4_t sum = *reinterpret_cast<const f32x4_t*>(p);
+  for (int j = 1; j < a.split_k; ++j) sum += *reinterpret_cast<const f32x4_t*>(p + j * plane);
+  const f32x4_t sc = load_scale4(a.scale, a.N, n);
+  store_out4(a.y, a.ldy, a.out_f32, a.vec_out, m, n, min(4, a.N - n), sum * sc);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Layout change: row-major [N, K] <-> TILED.  One thread per 16-byte piece of the tiled image:
+// piece p = (tile * ksteps + s) * 64 + l holds row tile*16 + (l % 16), k = s*64 + 16*(l / 16).
+// ---------------------------------------------------------------------------------------------
+template <bool kUnpack>
+__global__ void __launch_bounds__(256) repack_kernel(const int8_t* src, int8_t* dst, int64_t ldw, int N,
+                                                     int ksteps, int64_t pieces) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= pieces) return;
+  const int l = (int)(p & 63);
+  const int64_t ts = p >> 6;
+  const int s = (int)(ts % ksteps);
+  const int64_t tile = ts / ksteps;
+  const int64_t row = tile * kTileN + (l & 15);
+  const int64_t col = (int64_t)s * kStepK + 16 * (l >> 4);
+  if constexpr (!kUnpack) {
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    if (row < N) v = *reinterpret_cast<const u32x4_t*>(src + row * ldw + col);
+    *reinterpret_cast<u32x4_t*>(dst + p * 16) = v;
+  } else {
+    if (row < N) {
+      *reinterpret_cast<u32x4_t*>(dst + row * ldw + col) = *reinterpret_cast<const u32x4_t*>(src + p * 16);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Draft-head per-row int8 quantiser (plugin/qwen_fastpath/patches.py:139-147).  One workgroup per
+// row.  s = max(amax, 1e-8) * fl(1/127): the reference divides a CUDA tensor by the Python scalar
+// 127.0, which PyTorch evaluates as a multiply by the fp32 reciprocal; w / s is an IEEE division.
+// ---------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* w, int64_t ldw, int8_t* q,
+                                                            float* s_out, int H) {
+  __shared__ float red[256 / kWave];
+  const int64_t v = blockIdx.x;
+  const uint16_t* row = w + v * ldw;
+  float amax = 0.f;
+  for (int h = threadIdx.x; h < H; h += 256) amax = fmaxf(amax, fabsf(__uint_as_float((uint32_t)row[h] << 16)));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = amax;
+  __syncthreads();
+  amax = red[0];
+#pragma unroll
+  for (int i = 1; i < 256 / kWave; ++i) amax = fmaxf(amax, red[i]);
+  const float inv127 = 1.0f / 127.0f;  // constant-folded: the fp32 reciprocal of 127
+  const float s = fmaxf(amax, 1e-8f) * inv127;
+  if (threadIdx.x == 0) s_out[v] = s;
+  int8_t* qrow = q + v * (int64_t)H;
+  for (int h = threadIdx.x; h < H; h += 256) {
+    const float x = __uint_as_float((uint32_t)row[h] << 16);
+    float t = rintf(__fdiv_rn(x, s));
+    t = fminf(fmaxf(t, -127.f), 127.f);
+    qrow[h] = (int8_t)(int)t;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Row argmax over bf16 logits (torch.argmax semantics: NaN is the maximum, first index on ties).
+// One workgroup per row.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ bool argmax_better(float av, int ai, float bv, int bi) {
+  const bool an = av != av, bn = bv != bv;
+  if (an != bn) return an;
+  if (an) return ai < bi;
+  if (av != bv) return av > bv;
+  return ai < bi;
+}
+
+__global__ void __launch_bounds__(256) argmax_rows_kernel(const uint16_t* logits, int64_t ld, int n_valid,
+                                                          int64_t index_offset, int64_t* out) {
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  const uint16_t* row = logits + (int64_t)blockIdx.x * ld;
+  float bv = -__builtin_inff();
+  int bi = 0x7fffffff;
+  for (int n = threadIdx.x; n < n_valid; n += 256) {
+    const float v = __uint_as_float((uint32_t)row[n] << 16);
+    if (argmax_better(v, n, bv, bi)) {
+      bv = v;
+      bi = n;
+    }
+  }
+  sv[threadIdx.x] = bv;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int stride = 128; stride >= 1; stride >>= 1) {
+    if ((int)threadIdx.x < stride) {
+      const float ov = sv[threadIdx.x + stride];
+      const int oi = si[threadIdx.x + stride];
+      if (argmax_better(ov, oi, sv[threadIdx.x], si[threadIdx.x])) {
+        sv[threadIdx.x] = ov;
+        si[threadIdx.x] = oi;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    // every column -inf (or no valid column): torch.argmax returns the first index
+    const int idx = (si[0] == 0x7fffffff) ? 0 : si[0];
+    out[blockIdx.x] = (int64_t)idx + index_offset;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------------------------
+using KernelFn = void (*)(GemmArgs);
+
+template <int L, int NT, int W, int D>
+KernelFn mfma_fn(int hint) {
+  return hint ? &w8a16_mfma_kernel<L, NT, W, D, true> : &w8a16_mfma_kernel<L, NT, W, D, false>;
+}
+
+template <int L, int NT, int W>
+KernelFn mfma_by_depth(int depth, int hint) {
+  switch (depth) {
+    case 2: return mfma_fn<L, NT, W, 2>(hint);
+    case 4: return mfma_fn<L, NT, W, 4>(hint);
+    case 8: return mfma_fn<L, NT, W, 8>(hint);
+    default: return nullptr;
+  }
+}
+
+template <int L, int W>
+KernelFn mfma_by_nt(int nt, int depth, int hint) {
+  switch (nt) {
+    case 1: return mfma_by_depth<L, 1, W>(depth, hint);
+    case 2: return mfma_by_depth<L, 2, W>(depth, hint);
+    case 4: return mfma_by_depth<L, 4, W>(depth, hint);
+    default: return nullptr;
+  }
+}
+
+KernelFn select_mfma(int layout, int nt, int waves, int depth, int hint) {
+  if (waves != 4) return nullptr;
+  return layout == QF_LAYOUT_ROWMAJOR ? mfma_by_nt<QF_LAYOUT_ROWMAJOR, 4>(nt, depth, hint)
+                                      : mfma_by_nt<QF_LAYOUT_TILED, 4>(nt, depth, hint);
+}
+
+template <int MM, int RPW>
+KernelFn gemv_fn(int hint) {
+  return hint ? &w8a16_gemv_kernel<MM, RPW, 4, true> : &w8a16_gemv_kernel<MM, RPW, 4, false>;
+}
+
+template <int MM>
+KernelFn gemv_by_rpw(int rpw, int hint) {
+  switch (rpw) {
+    case 2: return gemv_fn<MM, 2>(hint);
+    case 4: return gemv_fn<MM, 4>(hint);
+    default: return nullptr;
+  }
+}
+
+KernelFn select_gemv(int M, int rpw, int waves, int hint) {
+  if (waves != 4) return nullptr;
+  switch (M) {
+    case 1: return gemv_by_rpw<1>(rpw, hint);
+    case 2: return gemv_by_rpw<2>(rpw, hint);
+    case 3: return gemv_by_rpw<3>(rpw, hint);
+    case 4: return gemv_by_rpw<4>(rpw, hint);
+    default: return nullptr;
+  }
+}
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+inline int round_up16(int n) { return (n + 15) / 16 * 16; }
+
+// LDS bytes one workgroup stages for split_k splits of ksteps (the largest split).
+size_t lds_bytes(int kernel, int M, int ksteps, int split_k) {
+  const size_t klen = (size_t)ceil_div(ksteps, split_k) * kStepK;
+  // the MFMA kernel stages one extra step of zeros after the activations
+  return (size_t)M * (klen + (kernel == QF_KERNEL_MFMA ? kStepK : 0)) * 2;
+}
+
+int workgroups(const qf_w8a16_config& c, int N) {
+  if (c.kernel == QF_KERNEL_GEMV) return ceil_div(N, c.waves * c.tiles_per_wave);
+  return ceil_div(round_up16(N) / kTileN, c.waves * c.tiles_per_wave);
+}
+
+// Automatic configuration (host only).  Returns false when unsupported.
+bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
+  if (M < 1 || M > QF_W8A16_MAX_M || N < 1 || K < QF_W8A16_K_ALIGN || K % QF_W8A16_K_ALIGN) return false;
+  if (layout != QF_LAYOUT_ROWMAJOR && layout != QF_LAYOUT_TILED) return false;
+  *c = qf_w8a16_config{};
+  c->kernel = QF_KERNEL_MFMA;
+  c->tiles_per_wave = 2;
+  c->waves = 4;
+  c->depth = 4;
+  c->load_hint = 0;
+  const int ksteps = K / kStepK;
+  const int wgs = workgroups(*c, N);
+  // Aim for >= 2 workgroups per CU (256 CUs) while keeping >= 8 k-steps per split.
+  int sk = 1;
+  while (wgs * sk < 512 && ksteps / (sk * 2) >= 8) sk *= 2;
+  while (lds_bytes(c->kernel, M, ksteps, sk) > kMaxLds && sk < ksteps) ++sk;
+  c->split_k = sk;
+  return true;
+}
+
+// Validate / complete a caller configuration.
+int resolve_config(int M, int N, int K, int layout, const qf_w8a16_config* in, qf_w8a16_config* out) {
+  if (!auto_config(M, N, K, layout, out)) return QF_ERR_UNSUPPORTED;
+  if (in == nullptr || in->kernel == QF_KERNEL_AUTO) return QF_OK;
+  qf_w8a16_config c = *in;
+  if (c.kernel != QF_KERNEL_GEMV && c.kernel != QF_KERNEL_MFMA) return QF_ERR_INVALID_ARG;
+  if (c.kernel == QF_KERNEL_GEMV && (M > 4 || layout != QF_LAYOUT_ROWMAJOR)) return QF_ERR_UNSUPPORTED;
+  if (c.waves == 0) c.waves = 4;
+  if (c.tiles_per_wave == 0) c.tiles_per_wave = (c.kernel == QF_KERNEL_GEMV) ? 4 : 2;
+  if (c.depth == 0) c.depth = 4;
+  if (c.split_k == 0) {
+    c.split_k = out->split_k;
+  }
+  const int ksteps = K / kStepK;
+  if (c.split_k < 1 || c.split_k > ksteps) return QF_ERR_INVALID_ARG;
+  if (lds_bytes(c.kernel, M, ksteps, c.split_k) > kMaxLds) return QF_ERR_UNSUPPORTED;
+  if (c.kernel == QF_KERNEL_MFMA && select_mfma(layout, c.tiles_per_wave, c.waves, c.depth, c.load_hint) == nullptr)
+    return QF_ERR_UNSUPPORTED;
+  if (c.kernel == QF_KERNEL_GEMV && select_gemv(M, c.tiles_per_wave, c.waves, c.load_hint) == nullptr)
+    return QF_ERR_UNSUPPORTED;
+  *out = c;
+  return QF_OK;
+}
+
+size_t workspace_for(const qf_w8a16_config& c, int M, int N) {
+  if (c.split_k <= 1) return 0;
+  return (size_t)c.split_k * (size_t)M * (size_t)round_up16(N) * sizeof(float);
+}
+
+int launch(KernelFn fn, dim3 grid, dim3 block, size_t smem, hipStream_t stream, const GemmArgs& a) {
+  void* args[] = {const_cast<GemmArgs*>(&a)};
+  if (hipLaunchKernel(reinterpret_cast<const void*>(fn), grid, block, args, smem, stream) != hipSuccess)
+    return QF_ERR_HIP;
+  return QF_OK;
+}
+
+}  // namespace qf
+
+using namespace qf;
+
+extern "C" {
+
+int qf_abi_version(void) { return QF_W8A16_ABI_VERSION; }
+
+const char* qf_status_string(int status) {
+  switch (status) {
+    case QF_OK: return "ok";
+    case QF_ERR_INVALID_ARG: return "invalid argument";
+    case QF_ERR_UNSUPPORTED: return "unsupported shape, layout or alignment (use the fallback path)";
+    case QF_ERR_WORKSPACE: return "workspace missing or too small";
+    case QF_ERR_HIP: return "HIP runtime error";
+    default: return "unknown status";
+  }
+}
+
+int qf_w8a16_pick_config(int M, int N, int K, int layout, qf_w8a16_config* cfg) {
+  if (cfg == nullptr) return QF_ERR_INVALID_ARG;
+  return auto_config(M, N, K, layout, cfg) ? QF_OK : QF_ERR_UNSUPPORTED;
+}
+
+size_t qf_w8a16_workspace_bytes(int M, int N, int K, int layout, const qf_w8a16_config* cfg) {
+  qf_w8a16_config c;
+  if (resolve_config(M, N, K, layout, cfg, &c) != QF_OK) return 0;
+  return workspace_for(c, M, N);
+}
+
+size_t qf_w8a16_tiled_bytes(int N, int K) {
+  if (N < 1 || K < 1) return 0;
+  return (size_t)round_up16(N) * (size_t)K;
+}
+
+int qf_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int layout, const float* scale,
+                  void* y, int64_t ldy, int out_dtype, int M, int N, int K, const qf_w8a16_config* cfg,
+                  void* workspace, size_t workspace_bytes, void* stream) {
+  if (x == nullptr || w == nullptr || scale == nullptr || y == nullptr) return QF_ERR_INVALID_ARG;
+  if (M < 1 || N < 1 || K < 1) return QF_ERR_INVALID_ARG;
+  if (layout != QF_LAYOUT_ROWMAJOR && layout != QF_LAYOUT_TILED) return QF_ERR_INVALID_ARG;
+  if (out_dtype != QF_DTYPE_BF16 && out_dtype != QF_DTYPE_F32) return QF_ERR_INVALID_ARG;
+  if (ldx < K || ldy < N || (layout == QF_LAYOUT_ROWMAJOR && ldw < K)) return QF_ERR_INVALID_ARG;
+  if (M > QF_W8A16_MAX_M || K % QF_W8A16_K_ALIGN) return QF_ERR_UNSUPPORTED;
+  if (!aligned16(x) || !aligned16(w) || !aligned16(scale) || !aligned16(y)) return QF_ERR_UNSUPPORTED;
+  if (ldx % 8 || (layout == QF_LAYOUT_ROWMAJOR && ldw % 16)) return QF_ERR_UNSUPPORTED;
+
+  qf_w8a16_config c;
+  const int rc = resolve_config(M, N, K, layout, cfg, &c);
+  if (rc != QF_OK) return rc;
+  const size_t need = workspace_for(c, M, N);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))) return QF_ERR_WORKSPACE;
+
+  GemmArgs a;
+  a.x = x;
+  a.w = w;
+  a.scale = scale;
+  a.y = y;
+  a.partial = reinterpret_cast<float*>(workspace);
+  a.ldx = ldx;
+  a.ldw = ldw;
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.n_pad = round_up16(N);
+  a.ksteps = K / kStepK;
+  a.split_k = c.split_k;
+  a.out_f32 = out_dtype == QF_DTYPE_F32;
+  a.vec_out = (ldy % 4) == 0;
+
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(workgroups(c, N), c.split_k);
+  const dim3 block(c.waves * kWave);
+  const size_t smem = lds_bytes(c.kernel, M, a.ksteps, c.split_k);
+  KernelFn fn = (c.kernel == QF_KERNEL_GEMV) ? select_gemv(M, c.tiles_per_wave, c.waves, c.load_hint)
+                                              : select_mfma(layout, c.tiles_per_wave, c.waves, c.depth, c.load_hint);
+  if (fn == nullptr) return QF_ERR_UNSUPPORTED;
+  int st = launch(fn, grid, block, smem, s, a);
+  if (st != QF_OK) return st;
+  if (c.split_k > 1) {
+    const int threads = M * (a.n_pad / 4);
+    st = launch(&splitk_reduce_kernel, dim3(ceil_div(threads, 256)), dim3(256), 0, s, a);
+  }
+  return st;
+}
+
+int qf_w8a16_repack(const int8_t* w_rowmajor, int64_t ldw, int8_t* w_tiled, int N, int K, void* stream) {
+  if (w_rowmajor == nullptr || w_tiled == nullptr || N < 1 || K < 1 || ldw < K) return QF_ERR_INVALID_ARG;
+  if (K % QF_W8A16_K_ALIGN || ldw % 16 || !aligned16(w_rowmajor) || !aligned16(w_tiled)) return QF_ERR_UNSUPPORTED;
+  const int ksteps = K / kStepK;
+  const int64_t pieces = (int64_t)(round_up16(N) / kTileN) * ksteps * kWave;
+  const int64_t blocks = (pieces + 255) / 256;
+  hipLaunchKernelGGL(repack_kernel<false>, dim3((unsigned)blocks), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), w_rowmajor, w_tiled, ldw, N, ksteps, pieces);
+  return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
+}
+
+int qf_w8a16_unpack(const int8_t* w_tiled, int8_t* w_rowmajor, int64_t ldw, int N, int K, void* stream) {
+  if (w_rowmajor == nullptr || w_tiled == nullptr || N < 1 || K < 1 || ldw < K) return QF_ERR_INVALID_ARG;
+  if (K % QF_W8A16_K_ALIGN || ldw % 16 || !aligned16(w_rowmajor) || !aligned16(w_tiled)) return QF_ERR_UNSUPPORTED;
+  const int ksteps = K / kStepK;
+  const int64_t pieces = (int64_t)(round_up16(N) / kTileN) * ksteps * kWave;
+  const int64_t blocks = (pieces + 255) / 256;
+  hipLaunchKernelGGL(repack_kernel<true>, dim3((unsigned)blocks), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), w_tiled, w_rowmajor, ldw, N, ksteps, pieces);
+  return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
+}
+
+int qf_quantize_rows_int8(const uint16_t* w, int64_t ldw, int8_t* q, float* s, int V, int H, void* stream) {
+  if (w == nullptr || q == nullptr || s == nullptr || V < 1 || H < 1 || ldw < H) return QF_ERR_INVALID_ARG;
+  hipLaunchKernelGGL(quantize_rows_kernel, dim3(V), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), w, ldw,
+                     q, s, H);
+  return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
+}
+
+int qf_argmax_rows_bf16(const uint16_t* logits, int64_t ld, int M, int N, int n_valid, int64_t index_offset,
+                        int64_t* out, void* stream) {
+  if (logits == nullptr || out == nullptr || M < 1 || N < 1 || ld < N || n_valid < 0 || n_valid > N)
+    return QF_ERR_INVALID_ARG;
+  hipLaunchKernelGGL(argmax_rows_kernel, dim3(M), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), logits, ld,
+                     n_valid, index_offset, out);
+  return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
+}
+
+}  // extern "C"

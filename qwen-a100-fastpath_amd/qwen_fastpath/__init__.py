@@ -1,0 +1,46 @@
+"""qwen_fastpath on MI355X: the W8A16 decode GEMM behind QWEN_FAST_LINEAR and the int8 MTP draft head.
+
+vLLM general plugin (entry point ``qwen_fastpath:register``, as plugin/qwen_fastpath/__init__.py:17-28
+in the reference).  Each patch can be switched off with an environment variable read once at
+register():
+
+  QWEN_FAST_LINEAR=0      keep the original W8A8 path for small-batch (decode) int8 linears
+  QWEN_FAST_DRAFT_HEAD=0  keep the bf16 lm_head for MTP draft proposals
+
+QWEN_FAST_ATTN (split-KV verification attention) is not provided by this package; the switch is
+accepted and ignored.
+"""
+import logging
+import os
+
+from .w8a16 import AUTO, ROWMAJOR, SMALL_M, TILED, W8A16Config, from_tiled, pick_config, resolve_config, to_tiled, w8a16_mm  # noqa: F401
+from .patches import (  # noqa: F401
+    Int8Head,
+    W8A16LinearMethod,
+    eligible,
+    int8_logits,
+    make_int8_head,
+    patch_draft_lm_head,
+    patch_int8_linear,
+    qf_int8_linear,
+    quantize_lm_head,
+    top_tokens,
+    w8a8_reference,
+)
+
+logger = logging.getLogger("vllm.qwen_fastpath")
+_registered = False
+
+
+def register():
+    """Idempotent plugin entry point (reference: plugin/qwen_fastpath/__init__.py:17-28)."""
+    global _registered
+    if _registered:
+        return
+    _registered = True
+    if os.environ.get("QWEN_FAST_ATTN", "1") == "1":
+        logger.info("qwen_fastpath: QWEN_FAST_ATTN is not implemented by this package; attention unchanged")
+    if os.environ.get("QWEN_FAST_LINEAR", "1") == "1":
+        patch_int8_linear()
+    if os.environ.get("QWEN_FAST_DRAFT_HEAD", "1") == "1":
+        patch_draft_lm_head()

@@ -1,0 +1,147 @@
+"""ctypes binding of libqf_w8a16.so, the C ABI declared in include/qf_w8a16.h.
+
+The library is built in-tree (qwen-a100-fastpath_amd/csrc/Makefile) next to this file.  There is no
+fallback implementation: if the library is missing, every GPU entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+LIB_NAME = "libqf_w8a16.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+ABI_VERSION = 1
+
+# qf_status
+OK = 0
+ERR_INVALID_ARG = 1
+ERR_UNSUPPORTED = 2
+ERR_WORKSPACE = 3
+ERR_HIP = 4
+
+# qf_layout / qf_dtype / qf_kernel
+LAYOUT_ROWMAJOR = 0
+LAYOUT_TILED = 1
+DTYPE_BF16 = 0
+DTYPE_F32 = 1
+KERNEL_AUTO = 0
+KERNEL_GEMV = 1
+KERNEL_MFMA = 2
+
+MAX_M = 16
+K_ALIGN = 64
+
+# Every symbol include/qf_w8a16.h declares.
+EXPORTS = (
+    "qf_abi_version",
+    "qf_status_string",
+    "qf_w8a16_pick_config",
+    "qf_w8a16_workspace_bytes",
+    "qf_w8a16_gemm",
+    "qf_w8a16_tiled_bytes",
+    "qf_w8a16_repack",
+    "qf_w8a16_unpack",
+    "qf_quantize_rows_int8",
+    "qf_argmax_rows_bf16",
+)
+
+
+class Config(ctypes.Structure):
+    """struct qf_w8a16_config."""
+
+    _fields_ = [
+        ("kernel", ctypes.c_int32),
+        ("split_k", ctypes.c_int32),
+        ("tiles_per_wave", ctypes.c_int32),
+        ("waves", ctypes.c_int32),
+        ("depth", ctypes.c_int32),
+        ("load_hint", ctypes.c_int32),
+        ("reserved", ctypes.c_int32 * 2),
+    ]
+
+    FIELDS = ("kernel", "split_k", "tiles_per_wave", "waves", "depth", "load_hint")
+
+    @classmethod
+    def from_seq(cls, seq) -> "Config":
+        c = cls()
+        for name, v in zip(cls.FIELDS, seq):
+            setattr(c, name, int(v))
+        return c
+
+    def to_tuple(self):
+        return tuple(int(getattr(self, f)) for f in self.FIELDS)
+
+
+class QFError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        self.status = status
+        super().__init__(f"{what}: {status_string(status)} (status {status})")
+
+
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the library once.  Raises ImportError (never falls back) when it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `make -C qwen-a100-fastpath_amd/csrc` "
+            "(or __graft_entry__.build()); the W8A16 op has no non-HIP implementation")
+    # torch first: its HIP runtime (soname libamdhip64.so.7) must be the one this library binds to.
+    import torch  # noqa: F401
+    L = ctypes.CDLL(LIB_PATH)
+    p, i64, i32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
+    L.qf_abi_version.argtypes = []
+    L.qf_abi_version.restype = i32
+    L.qf_status_string.argtypes = [i32]
+    L.qf_status_string.restype = ctypes.c_char_p
+    L.qf_w8a16_pick_config.argtypes = [i32, i32, i32, i32, ctypes.POINTER(Config)]
+    L.qf_w8a16_pick_config.restype = i32
+    L.qf_w8a16_workspace_bytes.argtypes = [i32, i32, i32, i32, ctypes.POINTER(Config)]
+    L.qf_w8a16_workspace_bytes.restype = sz
+    L.qf_w8a16_gemm.argtypes = [p, i64, p, i64, i32, p, p, i64, i32, i32, i32, i32,
+                                ctypes.POINTER(Config), p, sz, p]
+    L.qf_w8a16_gemm.restype = i32
+    L.qf_w8a16_tiled_bytes.argtypes = [i32, i32]
+    L.qf_w8a16_tiled_bytes.restype = sz
+    L.qf_w8a16_repack.argtypes = [p, i64, p, i32, i32, p]
+    L.qf_w8a16_repack.restype = i32
+    L.qf_w8a16_unpack.argtypes = [p, p, i64, i32, i32, p]
+    L.qf_w8a16_unpack.restype = i32
+    L.qf_quantize_rows_int8.argtypes = [p, i64, p, p, i32, i32, p]
+    L.qf_quantize_rows_int8.restype = i32
+    L.qf_argmax_rows_bf16.argtypes = [p, i64, i32, i32, i32, i64, p, p]
+    L.qf_argmax_rows_bf16.restype = i32
+    v = L.qf_abi_version()
+    if v != ABI_VERSION:
+        raise ImportError(f"{LIB_PATH}: ABI version {v}, expected {ABI_VERSION}")
+    _lib = L
+    return L
+
+
+def status_string(status: int) -> str:
+    try:
+        return load().qf_status_string(status).decode()
+    except ImportError:
+        return f"status {status}"
+
+
+def check(status: int, what: str) -> None:
+    if status != OK:
+        raise QFError(status, what)
+
+
+def pick_config(M: int, N: int, K: int, layout: int = LAYOUT_ROWMAJOR) -> Config | None:
+    c = Config()
+    rc = load().qf_w8a16_pick_config(M, N, K, layout, ctypes.byref(c))
+    if rc == ERR_UNSUPPORTED:
+        return None
+    check(rc, "qf_w8a16_pick_config")
+    return c
+
+
+def workspace_bytes(M: int, N: int, K: int, layout: int, cfg: Config | None) -> int:
+    return int(load().qf_w8a16_workspace_bytes(M, N, K, layout, ctypes.byref(cfg) if cfg is not None else None))

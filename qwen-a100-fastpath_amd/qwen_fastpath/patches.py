@@ -1,0 +1,346 @@
+"""Plugin surface of the W8A16 decode path (reference: plugin/qwen_fastpath/patches.py:72-189).
+
+* ``qf_int8_linear`` -- the dispatcher op (patches.py:84-106): M <= 16 bf16 activations on an int8
+  weight with stride(0) == 1 and one fp32 scale per output channel go to the HIP W8A16 kernel;
+  anything else goes to the W8A8 path the reference falls back to.
+* ``patch_int8_linear`` -- swaps ``apply_weights(self, layer, x, bias)`` of vLLM's int8 scaled-mm
+  kernel class (patches.py:72-116); ``W8A16LinearMethod.apply(layer, x, bias)`` is the same surface
+  for callers that hold the layer directly.
+* ``patch_draft_lm_head`` / ``quantize_lm_head`` / ``int8_logits`` / ``top_tokens`` -- the int8 MTP
+  draft head (patches.py:119-189), running the same kernel form over a per-row int8 copy of the
+  lm_head.
+
+vLLM is an optional dependency: with vLLM absent the patch functions return False and log; the
+ops, ``W8A16LinearMethod`` and the draft-head helpers work on plain tensors.
+"""
+from __future__ import annotations
+
+import logging
+import os
+from typing import Callable, NamedTuple, Optional
+
+import torch
+
+from . import _lib as L
+from .w8a16 import ROWMAJOR, SMALL_M, TILED, pick_config, w8a16_mm
+
+logger = logging.getLogger("vllm.qwen_fastpath")
+
+
+def linear_switch_enabled() -> bool:
+    """QWEN_FAST_LINEAR, default "1" (plugin/qwen_fastpath/__init__.py:25)."""
+    return os.environ.get("QWEN_FAST_LINEAR", "1") == "1"
+
+
+def draft_head_switch_enabled() -> bool:
+    """QWEN_FAST_DRAFT_HEAD, default "1" (plugin/qwen_fastpath/__init__.py:27)."""
+    return os.environ.get("QWEN_FAST_DRAFT_HEAD", "1") == "1"
+
+
+# ------------------------------------------------------------------------------------------------
+# W8A8 fallback (M > 16 or ineligible inputs)
+# ------------------------------------------------------------------------------------------------
+
+def _vllm_w8a8() -> Optional[Callable]:
+    try:
+        from vllm import _custom_ops as ops  # type: ignore
+    except ImportError:
+        return None
+
+    def run(x2, w_q, w_s, bias, out_dtype):
+        x_q, x_s, _ = ops.scaled_int8_quant(x2.contiguous(), None, None, symmetric=True)
+        return ops.cutlass_scaled_mm(x_q, w_q, scale_a=x_s, scale_b=w_s, out_dtype=out_dtype, bias=bias)
+
+    return run
+
+
+def w8a8_reference(x2: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, bias: Optional[torch.Tensor],
+                   out_dtype: torch.dtype) -> torch.Tensor:
+    """Dynamic per-token symmetric int8 activations x int8 weights, exact integer accumulation, then
+    fp32 scale_a * scale_b epilogue and optional bias -- the semantics of the scaled_int8_quant +
+    cutlass_scaled_mm pair the reference falls back to (patches.py:99-100).  Used when vLLM is not
+    installed; accuracy is pinned only by the reference's published W8A8 error statistic."""
+    xf = x2.float()
+    s_a = xf.abs().amax(dim=-1, keepdim=True) / 127.0
+    x_q = torch.where(s_a > 0, torch.round(xf / torch.where(s_a > 0, s_a, torch.ones_like(s_a))),
+                      torch.zeros_like(xf)).clamp_(-128, 127)
+    acc = (x_q.double() @ w_q.double()).float()  # integer sums: exact in fp64
+    y = acc * s_a * w_s.reshape(1, -1).float()
+    if bias is not None:
+        y = y + bias.float()
+    return y.to(out_dtype)
+
+
+_fallback_impl: Optional[Callable] = None
+
+
+def _fallback(x2, w_q, w_s, bias, out_dtype, layout):
+    if layout == TILED:
+        # The permuted image is readable only by this library's kernel: run it over 16-row slices.
+        ys = [w8a16_mm(x2[i:i + SMALL_M], w_q, w_s.reshape(-1), None, out_dtype, layout)
+              for i in range(0, x2.shape[0], SMALL_M)]
+        y = torch.cat(ys, dim=0)
+        return y if bias is None else y + bias
+    global _fallback_impl
+    if _fallback_impl is None:
+        _fallback_impl = _vllm_w8a8() or w8a8_reference
+    return _fallback_impl(x2, w_q, w_s, bias, out_dtype)
+
+
+# ------------------------------------------------------------------------------------------------
+# dispatcher op (patches.py:84-106)
+# ------------------------------------------------------------------------------------------------
+
+def eligible(x2: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, layout: int = ROWMAJOR) -> bool:
+    """The reference's predicate (patches.py:90-92), plus: the tensors live on the GPU."""
+    M, K = x2.shape
+    if layout == ROWMAJOR:
+        N = w_q.shape[1]
+        layout_ok = w_q.stride(0) == 1
+    else:
+        N = w_s.numel()
+        layout_ok = True
+    return (M <= SMALL_M and x2.dtype == torch.bfloat16 and layout_ok and w_s.numel() == N
+            and x2.is_cuda and pick_config(N, K, layout) is not None)
+
+
+def _qf_int8_linear_impl(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, bias: Optional[torch.Tensor],
+                         layout: int = ROWMAJOR) -> torch.Tensor:
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    N = w_q.shape[1] if layout == ROWMAJOR else w_s.numel()
+    if eligible(x2, w_q, w_s, layout):
+        if x2.stride(-1) != 1:
+            x2 = x2.contiguous()
+        s = w_s.reshape(-1)
+        if s.dtype != torch.float32:
+            s = s.float()
+        y = w8a16_mm(x2, w_q, s, None, x.dtype, layout)
+        if bias is not None:
+            y = y + bias
+        return y.view(*lead, N)
+    y = _fallback(x2, w_q, w_s, bias, x.dtype, layout)
+    return y.view(*lead, N)
+
+
+@torch.library.custom_op("qwen_fastpath::qf_int8_linear", mutates_args=())
+def qf_int8_linear(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, bias: Optional[torch.Tensor],
+                   layout: int = 0) -> torch.Tensor:
+    """torch.ops.qwen_fastpath.qf_int8_linear(x, w_q, w_s, bias, layout=0): one opaque node under
+    torch.compile, like the reference's torch.ops.vllm.qf_int8_linear."""
+    return _qf_int8_linear_impl(x, w_q, w_s, bias, layout)
+
+
+@qf_int8_linear.register_fake
+def _qf_int8_linear_fake(x, w_q, w_s, bias, layout=0):
+    N = w_q.shape[1] if layout == ROWMAJOR else w_s.numel()
+    return x.new_empty((*x.shape[:-1], N))
+
+
+# ------------------------------------------------------------------------------------------------
+# linear-layer surfaces (patches.py:108-116)
+# ------------------------------------------------------------------------------------------------
+
+def make_apply_weights(orig_apply: Callable) -> Callable:
+    """Replacement for ``apply_weights(self, layer, x, bias=None)`` of an int8 scaled-mm kernel class
+    whose ``_get_layer_params(layer)`` returns (w_q, w_s, i_s, i_zp, azp_adj)."""
+
+    def apply_weights(self, layer, x, bias=None):
+        w_q, w_s, i_s, i_zp, azp_adj = self._get_layer_params(layer)
+        if i_s is None and i_zp is None and azp_adj is None:  # dynamic symmetric per-token
+            return torch.ops.qwen_fastpath.qf_int8_linear(x, w_q, w_s, bias, getattr(layer, "_qf_layout", ROWMAJOR))
+        return orig_apply(self, layer, x, bias)
+
+    apply_weights._qwen_fastpath = True
+    return apply_weights
+
+
+# vLLM classes whose apply_weights serve int8 W8A8 linears: the reference's CUTLASS class first,
+# then the ROCm-side implementations of the same interface.
+VLLM_INT8_KERNEL_CLASSES = (
+    "vllm.model_executor.kernels.linear.scaled_mm.cutlass:CutlassInt8ScaledMMLinearKernel",
+    "vllm.model_executor.layers.quantization.kernels.scaled_mm.cutlass:CutlassScaledMMLinearKernel",
+    "vllm.model_executor.layers.quantization.kernels.scaled_mm.triton:TritonScaledMMLinearKernel",
+    "vllm.model_executor.layers.quantization.kernels.scaled_mm.aiter:AiterScaledMMLinearKernel",
+)
+
+
+def _import_attr(path: str):
+    mod, _, attr = path.partition(":")
+    import importlib
+    return getattr(importlib.import_module(mod), attr)
+
+
+def patch_int8_linear(kernel_cls=None) -> bool:
+    """Install the W8A16 decode path on ``kernel_cls`` (default: vLLM's int8 scaled-mm kernel
+    classes).  Idempotent (patches.py:80-82).  Returns False when no class could be patched."""
+    classes = [kernel_cls] if kernel_cls is not None else []
+    if kernel_cls is None:
+        for path in VLLM_INT8_KERNEL_CLASSES:
+            try:
+                classes.append(_import_attr(path))
+            except (ImportError, AttributeError):
+                continue
+    if not classes:
+        logger.info("qwen_fastpath: vLLM int8 linear kernel classes not found; W8A16 op available as "
+                    "torch.ops.qwen_fastpath.qf_int8_linear only")
+        return False
+    for cls in classes:
+        orig = cls.apply_weights
+        if getattr(orig, "_qwen_fastpath", False):
+            continue
+        cls.apply_weights = make_apply_weights(orig)
+    logger.info("qwen_fastpath: W8A16 decode path for W8A8-int8 linears (M <= %d), W8A8 above", SMALL_M)
+    return True
+
+
+class W8A16LinearMethod:
+    """vLLM LinearMethod-style surface ``apply(layer, x, bias=None)`` over a W8A8 int8 layer.
+
+    The layer holds ``weight`` (int8 [K, N] with stride(0) == 1, or the TILED image when
+    ``layer._qf_layout == TILED``), ``weight_scale`` (fp32, N values) and optionally
+    ``input_scale`` / ``input_zero_point`` / ``azp_adj`` (static or asymmetric activation
+    quantisation, which keeps the original path).  The QWEN_FAST_LINEAR switch is read once at
+    construction; "0" routes every call to ``fallback``."""
+
+    def __init__(self, fallback: Optional[Callable] = None, enabled: Optional[bool] = None):
+        self.enabled = linear_switch_enabled() if enabled is None else bool(enabled)
+        self.fallback = fallback
+
+    def _original(self, layer, x, bias):
+        if self.fallback is not None:
+            return self.fallback(layer, x, bias)
+        x2 = x.reshape(-1, x.shape[-1])
+        y = _fallback(x2, layer.weight, layer.weight_scale, bias, x.dtype, getattr(layer, "_qf_layout", ROWMAJOR))
+        return y.view(*x.shape[:-1], y.shape[-1])
+
+    def apply(self, layer, x: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+        dynamic = all(getattr(layer, n, None) is None for n in ("input_scale", "input_zero_point", "azp_adj"))
+        if self.enabled and dynamic:
+            return torch.ops.qwen_fastpath.qf_int8_linear(x, layer.weight, layer.weight_scale, bias,
+                                                          getattr(layer, "_qf_layout", ROWMAJOR))
+        return self._original(layer, x, bias)
+
+
+# ------------------------------------------------------------------------------------------------
+# int8 MTP draft head (patches.py:119-189)
+# ------------------------------------------------------------------------------------------------
+
+class Int8Head(NamedTuple):
+    """What the reference stores as draft_model._qf_head_i8 (patches.py:149)."""
+
+    w_t: torch.Tensor      # int8 [H, V] view with stride (1, H) of the [V, H] quantised head
+    scale: torch.Tensor    # fp32 [V]
+    num_pad: int           # padded vocabulary rows at the end
+    cfg: object            # pick_config(V, H)
+
+
+def quantize_lm_head(weight: torch.Tensor):
+    """Per-row int8 copy of a bf16 [V, H] lm_head on the GPU (HIP kernel; patches.py:139-147):
+    s = max(amax|row|, 1e-8) / 127, q = clamp(round_half_even(row / s), -127, 127).
+    Returns (w8 [V, H] int8, scale [V] fp32)."""
+    if weight.dtype != torch.bfloat16 or weight.dim() != 2 or not weight.is_cuda:
+        raise TypeError("quantize_lm_head expects a 2-D bf16 CUDA tensor")
+    if weight.stride(1) != 1:
+        weight = weight.contiguous()
+    V, H = weight.shape
+    w8 = torch.empty((V, H), dtype=torch.int8, device=weight.device)
+    scale = torch.empty((V,), dtype=torch.float32, device=weight.device)
+    stream = torch.cuda.current_stream(weight.device).cuda_stream
+    L.check(L.load().qf_quantize_rows_int8(weight.data_ptr(), weight.stride(0), w8.data_ptr(), scale.data_ptr(),
+                                           V, H, stream), "qf_quantize_rows_int8")
+    return w8, scale
+
+
+def make_int8_head(weight: torch.Tensor, num_pad: int = 0) -> Int8Head:
+    w8, scale = quantize_lm_head(weight)
+    V, H = w8.shape
+    return Int8Head(w8.t(), scale, int(num_pad), pick_config(V, H))
+
+
+def int8_logits(head: Optional[Int8Head], hidden_states: torch.Tensor, logits_as_input: bool = False,
+                soft_cap=None, scale: float = 1.0, draft_id_to_target_id=None) -> Optional[torch.Tensor]:
+    """Draft logits through the W8A16 kernel, or None when the guard of patches.py:160-163 fails
+    (the caller then uses the bf16 head)."""
+    if (head is None or hidden_states.dim() != 2 or hidden_states.shape[0] > SMALL_M
+            or hidden_states.dtype != torch.bfloat16 or logits_as_input or soft_cap is not None
+            or scale != 1.0 or draft_id_to_target_id is not None or head.cfg is None):
+        return None
+    x = hidden_states if hidden_states.stride(-1) == 1 else hidden_states.contiguous()
+    return w8a16_mm(x, head.w_t, head.scale, head.cfg, torch.bfloat16)
+
+
+def top_tokens(logits: torch.Tensor, num_pad: int = 0, vocab_start: int = 0) -> torch.Tensor:
+    """argmax over the vocabulary with the last num_pad columns treated as -inf, plus the vocabulary
+    start index (patches.py:182-185); HIP kernel, torch.argmax tie/NaN semantics."""
+    if logits.dtype != torch.bfloat16 or logits.dim() != 2 or logits.stride(1) != 1:
+        raise TypeError("top_tokens expects 2-D bf16 logits with unit column stride")
+    M, N = logits.shape
+    out = torch.empty((M,), dtype=torch.int64, device=logits.device)
+    stream = torch.cuda.current_stream(logits.device).cuda_stream
+    L.check(L.load().qf_argmax_rows_bf16(logits.data_ptr(), logits.stride(0), M, N, N - int(num_pad),
+                                         int(vocab_start), out.data_ptr(), stream), "qf_argmax_rows_bf16")
+    return out
+
+
+def patch_draft_lm_head(speculator_cls=None, mtp_cls=None) -> bool:
+    """Give the MTP drafter an int8 per-row lm_head (patches.py:119-189).  With vLLM absent and no
+    classes passed, returns False.  The classes need: speculator.load_draft_model(target_model,
+    target_attn_layer_names) -> draft_model; draft_model.lm_head.weight / .tp_size /
+    .shard_indices.(num_org_vocab_padding, org_vocab_start_index); draft_model.logits_processor
+    with logits_as_input / soft_cap / scale / org_vocab_size; compute_logits / get_top_tokens."""
+    if speculator_cls is None or mtp_cls is None:
+        try:
+            from vllm.model_executor.models import qwen3_5_mtp  # type: ignore
+            from vllm.v1.worker.gpu.spec_decode.mtp.speculator import MTPSpeculator  # type: ignore
+        except ImportError:
+            logger.info("qwen_fastpath: vLLM MTP classes not found; int8 draft head helpers only")
+            return False
+        speculator_cls = speculator_cls or MTPSpeculator
+        mtp_cls = mtp_cls or qwen3_5_mtp.Qwen3_5MTP
+
+    orig_load = speculator_cls.load_draft_model
+    if getattr(orig_load, "_qwen_fastpath", False):
+        return True
+
+    def load_draft_model(self, target_model, target_attn_layer_names):
+        draft_model = orig_load(self, target_model, target_attn_layer_names)
+        lm_head = getattr(draft_model, "lm_head", None)
+        weight = getattr(lm_head, "weight", None)
+        if (isinstance(draft_model, mtp_cls) and weight is not None and weight.dim() == 2
+                and getattr(lm_head, "tp_size", 1) == 1):
+            num_pad = lm_head.shard_indices.num_org_vocab_padding
+            draft_model._qf_head_i8 = make_int8_head(weight, num_pad)
+            logger.info("qwen_fastpath: int8 draft lm_head (%d x %d, %.2f GB) for MTP proposals",
+                        weight.shape[0], weight.shape[1], weight.numel() / 1e9)
+        return draft_model
+
+    load_draft_model._qwen_fastpath = True
+    speculator_cls.load_draft_model = load_draft_model
+
+    def _logits(model, hidden_states):
+        lp = model.logits_processor
+        return int8_logits(model.__dict__.get("_qf_head_i8"), hidden_states, lp.logits_as_input, lp.soft_cap,
+                           lp.scale, getattr(model, "draft_id_to_target_id", None))
+
+    orig_logits = mtp_cls.compute_logits
+
+    def compute_logits(self, hidden_states, spec_step_idx=0):
+        logits = _logits(self, hidden_states)
+        if logits is None:
+            return orig_logits(self, hidden_states, spec_step_idx)
+        return logits[..., : self.logits_processor.org_vocab_size]
+
+    orig_top = mtp_cls.get_top_tokens
+
+    def get_top_tokens(self, hidden_states):
+        logits = _logits(self, hidden_states)
+        if logits is None:
+            return orig_top(self, hidden_states)
+        si = self.lm_head.shard_indices
+        return top_tokens(logits, si.num_org_vocab_padding, si.org_vocab_start_index)
+
+    mtp_cls.compute_logits = compute_logits
+    mtp_cls.get_top_tokens = get_top_tokens
+    logger.info("qwen_fastpath: int8 draft lm_head enabled")
+    return True

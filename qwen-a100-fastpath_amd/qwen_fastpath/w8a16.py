@@ -1,0 +1,175 @@
+"""Small-M W8A16 GEMM over the int8 weights of a W8A8 checkpoint, on MI355X.
+
+Host side of the op (reference: plugin/qwen_fastpath/w8a16.py).  The weights are the checkpoint's
+int8 [N, K] row-major matrix -- the [K, N] column-major view vLLM keeps for its int8 GEMM is the same
+memory -- with a per-output-channel fp32 scale.  Activations stay bf16; the kernels widen the int8
+weights to bf16 in registers, accumulate in fp32 and apply the scale after the K reduction.  The
+compute is hand-written HIP for gfx950 behind a C ABI (include/qf_w8a16.h); this module only
+allocates outputs and workspaces through torch and launches on torch's current stream.
+
+Public names mirror the reference module:
+  SMALL_M        w8a16.py:12     largest M routed to this op
+  pick_config    w8a16.py:58-68  None when the shape is not served (K % 64 != 0)
+  w8a16_mm       w8a16.py:71-83  y = (x @ W^T) * s as a new [M, N] tensor of out_dtype
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import NamedTuple
+
+import torch
+
+from . import _lib as L
+
+SMALL_M = L.MAX_M
+ROWMAJOR = L.LAYOUT_ROWMAJOR
+TILED = L.LAYOUT_TILED
+
+
+class W8A16Config(NamedTuple):
+    """Launch configuration; zero fields are chosen by the library for the call's M (see
+    qf_w8a16_pick_config).  kernel: 0 auto, 1 gemv (M <= 4), 2 mfma."""
+
+    kernel: int = 0
+    split_k: int = 0
+    tiles_per_wave: int = 0
+    waves: int = 0
+    depth: int = 0
+    load_hint: int = 0
+
+
+AUTO = W8A16Config()
+
+
+def pick_config(N: int, K: int, layout: int = ROWMAJOR) -> W8A16Config | None:
+    """Configuration for an [N, K] weight, or None when this op does not serve the shape (the
+    caller falls back), as the reference's pick_config does for K not a multiple of 64
+    (w8a16.py:63-68).  Kernel, split-K and tiling depend on M, so they are resolved per call."""
+    if N < 1 or K < L.K_ALIGN or K % L.K_ALIGN:
+        return None
+    if layout not in (ROWMAJOR, TILED):
+        return None
+    return AUTO
+
+
+def resolve_config(M: int, N: int, K: int, layout: int = ROWMAJOR) -> W8A16Config | None:
+    """The configuration the library picks for this M (None: unsupported)."""
+    c = L.pick_config(M, N, K, layout)
+    return None if c is None else W8A16Config(*c.to_tuple())
+
+
+_cfg_cache: dict[tuple, L.Config] = {}
+
+
+def _config_struct(cfg) -> L.Config:
+    key = tuple(int(v) for v in cfg)
+    c = _cfg_cache.get(key)
+    if c is None:
+        c = L.Config.from_seq(key)
+        _cfg_cache[key] = c
+    return c
+
+
+def _weight_geometry(w: torch.Tensor, N: int, K: int, layout: int) -> int:
+    """Validate the weight tensor and return its row stride (bytes between output channels)."""
+    if w.dtype != torch.int8:
+        raise TypeError(f"weight must be int8, got {w.dtype}")
+    if layout == ROWMAJOR:
+        # [K, N] with stride (1, ldw): the reference's w_t (w8a16.py:72)
+        if w.dim() != 2 or tuple(w.shape) != (K, N) or (w.stride(0) != 1 and K > 1):
+            raise ValueError(f"row-major weight must be a [K, N] = [{K}, {N}] view with stride(0) == 1, "
+                             f"got shape {tuple(w.shape)} stride {w.stride()}")
+        return w.stride(1) if N > 1 else K
+    if layout == TILED:
+        if not w.is_contiguous() or w.numel() != tiled_numel(N, K):
+            raise ValueError(f"TILED weight must be a contiguous image of {tiled_numel(N, K)} bytes")
+        return K
+    raise ValueError(f"unknown layout {layout}")
+
+
+def _launch(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, layout: int, out_dtype: torch.dtype,
+            config) -> torch.Tensor:
+    lib = L.load()
+    if x.dim() != 2 or x.dtype != torch.bfloat16:
+        raise TypeError(f"x must be a 2-D bf16 tensor, got {x.dtype} {tuple(x.shape)}")
+    if w_scale.dtype != torch.float32:
+        raise TypeError(f"w_scale must be fp32, got {w_scale.dtype}")
+    M, K = x.shape
+    N = w_scale.numel()
+    ldw = _weight_geometry(w, N, K, layout)
+    if x.stride(1) != 1 and K > 1:
+        x = x.contiguous()
+    ldx = x.stride(0) if M > 1 else K
+    if x.data_ptr() % 16 or ldx % 8:
+        x = x.clone(memory_format=torch.contiguous_format)
+        ldx = K
+    s = w_scale.reshape(-1)
+    if not s.is_contiguous() or s.data_ptr() % 16:
+        s = s.clone(memory_format=torch.contiguous_format)
+    if out_dtype == torch.bfloat16:
+        dt = L.DTYPE_BF16
+    elif out_dtype == torch.float32:
+        dt = L.DTYPE_F32
+    else:
+        raise TypeError(f"out_dtype must be bf16 or fp32, got {out_dtype}")
+    y = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    c = _config_struct(config)
+    ws_bytes = int(lib.qf_w8a16_workspace_bytes(M, N, K, layout, ctypes.byref(c)))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    rc = lib.qf_w8a16_gemm(x.data_ptr(), ldx, w.data_ptr(), ldw, layout, s.data_ptr(), y.data_ptr(), N, dt,
+                           M, N, K, ctypes.byref(c), ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+    L.check(rc, f"qf_w8a16_gemm(M={M}, N={N}, K={K}, layout={layout})")
+    return y
+
+
+@torch.library.custom_op("qwen_fastpath::w8a16_mm", mutates_args=(), device_types="cuda")
+def _w8a16_mm_op(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, layout: int, out_dtype: torch.dtype,
+                 config: list[int]) -> torch.Tensor:
+    return _launch(x, w, w_scale, layout, out_dtype, config)
+
+
+@_w8a16_mm_op.register_fake
+def _w8a16_mm_fake(x, w, w_scale, layout, out_dtype, config):
+    return x.new_empty((x.shape[0], w_scale.numel()), dtype=out_dtype)
+
+
+def w8a16_mm(x: torch.Tensor, w_t: torch.Tensor, w_scale: torch.Tensor, cfg, out_dtype: torch.dtype,
+             layout: int = ROWMAJOR) -> torch.Tensor:
+    """y[M, N] = (x @ W^T) * w_scale in out_dtype (reference: w8a16.py:71-83).
+
+    x [M, K] bf16 (row stride arbitrary, unit column stride); w_t [K, N] int8 with stride (1, K) --
+    the checkpoint's [N, K] row-major matrix -- or, with layout=TILED, the image made by to_tiled();
+    w_scale [N] fp32.  Runs on torch's current stream; graph-capturable (no host synchronisation,
+    allocations through torch's caching allocator only)."""
+    cfg = AUTO if cfg is None else cfg
+    return torch.ops.qwen_fastpath.w8a16_mm(x, w_t, w_scale, int(layout), out_dtype, [int(v) for v in cfg])
+
+
+# ------------------------------------------------------------------------------------------------
+# weight layout
+# ------------------------------------------------------------------------------------------------
+
+def tiled_numel(N: int, K: int) -> int:
+    return (N + 15) // 16 * 16 * K
+
+
+def to_tiled(w_t: torch.Tensor) -> torch.Tensor:
+    """Pre-permuted image of a [K, N] stride-(1, K) int8 weight: 1 KiB tiles of 16 output channels
+    x 64 k, tile (t, s) at byte ((t * K/64) + s) * 1024, lane l of the tile holding channel
+    16 t + l % 16, k = 64 s + 16 (l // 16) .. +15.  Every 64-lane 16-byte load of the kernel then
+    reads one contiguous KiB."""
+    K, N = w_t.shape
+    ldw = _weight_geometry(w_t, N, K, ROWMAJOR)
+    out = torch.empty(tiled_numel(N, K), dtype=torch.int8, device=w_t.device)
+    stream = torch.cuda.current_stream(w_t.device).cuda_stream
+    L.check(L.load().qf_w8a16_repack(w_t.data_ptr(), ldw, out.data_ptr(), N, K, stream), "qf_w8a16_repack")
+    return out
+
+
+def from_tiled(w_tiled: torch.Tensor, N: int, K: int) -> torch.Tensor:
+    """Inverse of to_tiled: returns the [K, N] stride-(1, K) view of a fresh [N, K] matrix."""
+    out = torch.empty((N, K), dtype=torch.int8, device=w_tiled.device)
+    stream = torch.cuda.current_stream(w_tiled.device).cuda_stream
+    L.check(L.load().qf_w8a16_unpack(w_tiled.data_ptr(), out.data_ptr(), K, N, K, stream), "qf_w8a16_unpack")
+    return out.t()

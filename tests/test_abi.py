@@ -1,0 +1,110 @@
+"""The C ABI library loads, exports every symbol include/qf_w8a16.h declares, and its host-only entry
+points behave as documented.  No call here reaches the GPU: every qf_w8a16_gemm call is rejected by
+argument validation before any HIP call."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from qwen_fastpath import _lib as L
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "qf_w8a16.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(qf_\w+)\(", text, flags=re.M)))
+
+
+def test_header_declares_the_python_export_list():
+    assert header_symbols() == sorted(L.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.load()
+    for name in header_symbols():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_matches_header():
+    m = re.search(r"#define QF_W8A16_ABI_VERSION (\d+)", open(HEADER).read())
+    assert L.load().qf_abi_version() == int(m.group(1)) == L.ABI_VERSION
+
+
+def test_status_strings():
+    for st in (L.OK, L.ERR_INVALID_ARG, L.ERR_UNSUPPORTED, L.ERR_WORKSPACE, L.ERR_HIP):
+        assert L.status_string(st) and L.status_string(st) != "unknown status"
+    assert L.status_string(99) == "unknown status"
+
+
+@pytest.mark.parametrize("M,N,K,layout", [(0, 64, 64, 0), (17, 64, 64, 0), (5, 64, 100, 0), (5, 64, 0, 0),
+                                          (5, 0, 64, 0), (5, 64, 64, 7)])
+def test_pick_config_unsupported(M, N, K, layout):
+    assert L.pick_config(M, N, K, layout) is None
+
+
+@pytest.mark.parametrize("M", range(1, 17))
+def test_pick_config_supported_and_lds_bounded(M):
+    for (N, K) in ((10240, 5120), (5120, 8192), (34816, 5120), (5120, 17408), (151936, 5120), (100, 64)):
+        c = L.pick_config(M, N, K)
+        assert c is not None
+        assert c.kernel in (L.KERNEL_GEMV, L.KERNEL_MFMA)
+        ksteps = K // 64
+        assert 1 <= c.split_k <= ksteps
+        klen = -(-ksteps // c.split_k) * 64
+        assert M * (klen + 64) * 2 <= 65536
+        ws = L.workspace_bytes(M, N, K, 0, None)
+        n_pad = (N + 15) // 16 * 16
+        assert ws == (0 if c.split_k == 1 else c.split_k * M * n_pad * 4)
+
+
+def test_workspace_for_explicit_config():
+    c = L.Config.from_seq((2, 4, 2, 4, 4, 0))
+    assert L.workspace_bytes(5, 1000, 1024, 0, c) == 4 * 5 * 1008 * 4
+    c1 = L.Config.from_seq((2, 1, 2, 4, 4, 0))
+    assert L.workspace_bytes(5, 1000, 1024, 0, c1) == 0
+
+
+def _gemm(x=16, ldx=64, w=16, ldw=64, layout=0, s=16, y=16, ldy=64, dt=0, M=5, N=64, K=64, cfg=None,
+          ws=None, wsb=0):
+    lib = L.load()
+    return lib.qf_w8a16_gemm(x, ldx, w, ldw, layout, s, y, ldy, dt, M, N, K,
+                             ctypes.byref(cfg) if cfg is not None else None, ws, wsb, None)
+
+
+def test_gemm_argument_validation_host_only():
+    fake = 1 << 20  # never dereferenced: every call below is rejected before launch
+    assert _gemm(x=None) == L.ERR_INVALID_ARG
+    assert _gemm(x=fake, w=fake, s=fake, y=fake, M=0) == L.ERR_INVALID_ARG
+    assert _gemm(x=fake, w=fake, s=fake, y=fake, layout=5) == L.ERR_INVALID_ARG
+    assert _gemm(x=fake, w=fake, s=fake, y=fake, dt=9) == L.ERR_INVALID_ARG
+    assert _gemm(x=fake, w=fake, s=fake, y=fake, ldx=32) == L.ERR_INVALID_ARG       # ldx < K
+    assert _gemm(x=fake, w=fake, s=fake, y=fake, M=17) == L.ERR_UNSUPPORTED         # > SMALL_M
+    assert _gemm(x=fake, w=fake, s=fake, y=fake, K=96, ldx=96, ldw=96) == L.ERR_UNSUPPORTED  # K % 64
+    assert _gemm(x=fake + 2, w=fake, s=fake, y=fake) == L.ERR_UNSUPPORTED           # misaligned x
+    assert _gemm(x=fake, w=fake, s=fake, y=fake, ldx=68) == L.ERR_UNSUPPORTED       # ldx % 8
+    gemv_big_m = L.Config.from_seq((L.KERNEL_GEMV, 1, 4, 4, 4, 0))
+    assert _gemm(x=fake, w=fake, s=fake, y=fake, cfg=gemv_big_m) == L.ERR_UNSUPPORTED  # gemv needs M <= 4
+    bad_tiles = L.Config.from_seq((L.KERNEL_MFMA, 1, 3, 4, 4, 0))
+    assert _gemm(x=fake, w=fake, s=fake, y=fake, cfg=bad_tiles) == L.ERR_UNSUPPORTED
+    split = L.Config.from_seq((L.KERNEL_MFMA, 4, 2, 4, 4, 0))
+    assert _gemm(x=fake, w=fake, s=fake, y=fake, K=1024, ldx=1024, ldw=1024, cfg=split) == L.ERR_WORKSPACE
+    too_many = L.Config.from_seq((L.KERNEL_MFMA, 99, 2, 4, 4, 0))
+    assert _gemm(x=fake, w=fake, s=fake, y=fake, cfg=too_many) == L.ERR_INVALID_ARG
+
+
+def test_tiled_bytes():
+    lib = L.load()
+    assert lib.qf_w8a16_tiled_bytes(34816, 5120) == 34816 * 5120
+    assert lib.qf_w8a16_tiled_bytes(100, 64) == 112 * 64
+    assert lib.qf_w8a16_tiled_bytes(0, 64) == 0
+
+
+def test_other_entry_points_validate_host_only():
+    lib = L.load()
+    assert lib.qf_w8a16_repack(None, 64, None, 16, 64, None) == L.ERR_INVALID_ARG
+    assert lib.qf_w8a16_repack(1 << 20, 64, 1 << 21, 16, 96, None) == L.ERR_INVALID_ARG  # ldw < K
+    assert lib.qf_w8a16_unpack(1 << 20, 1 << 21, 96, 16, 96, None) == L.ERR_UNSUPPORTED  # K % 64
+    assert lib.qf_quantize_rows_int8(None, 8, None, None, 1, 8, None) == L.ERR_INVALID_ARG
+    assert lib.qf_argmax_rows_bf16(1 << 20, 8, 1, 8, 9, 0, 1 << 21, None) == L.ERR_INVALID_ARG  # n_valid > N

@@ -1,0 +1,304 @@
+"""Pins the oracle (oracle/oracle.py, oracle/qf_oracle.c) before anything is checked against it.
+
+Each oracle function is checked against something independent of its own code: exact rational
+arithmetic (fractions.Fraction), torch's fp32->bf16 rounding, closed forms, the reference's own tile
+table (plugin/qwen_fastpath/w8a16.py:47-68) and its published error statistic
+(data/measurements.json:429-436), and planted mistakes that the checker must reject.
+"""
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+
+# ------------------------------------------------------------------------------------------------
+# independent exact rounding (pure Python rationals)
+# ------------------------------------------------------------------------------------------------
+
+def rne_bf16_fraction(v: Fraction) -> float:
+    """Round a rational to bf16, nearest-even, by exact arithmetic; returns the value as float."""
+    if v == 0:
+        return 0.0
+    a = abs(v)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    q_exp = max(e, -126) - 7
+    q = round(a / (Fraction(2) ** q_exp))  # Fraction round(): half to even
+    r = q * Fraction(2) ** q_exp
+    if r >= Fraction(2) ** 128 - Fraction(2) ** 120:  # beyond bf16 max after rounding
+        return float("inf") if v > 0 else float("-inf")
+    f = float(r)
+    return f if v > 0 else -f
+
+
+def bits_to_fraction(b: int) -> Fraction:
+    f = np.array([b], dtype=np.uint16)
+    from oracle import oracle as O
+    return Fraction(float(O.bf16_to_f32(f)[0]))
+
+
+def test_bf16_rounding_matches_torch(oracle):
+    rng = np.random.default_rng(1)
+    v = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32),
+        (rng.standard_normal(20000) * 1e-39).astype(np.float32),   # bf16 subnormal range
+        np.clip(rng.standard_normal(20000) * 1e38, -3.4e38, 3.4e38).astype(np.float32),  # near overflow
+        np.array([3.3895e38, 3.39e38, -3.4e38, 1e-45, 0.0, -0.0, np.inf, -np.inf], dtype=np.float32),
+    ])
+    got = oracle.bf16_from_f64(v.astype(np.float64))
+    want = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_bf16_rounding_from_f64_matches_fractions(oracle):
+    # fp64 values that are not fp32 values, including exact bf16 ties and ties +- 1 fp64 ulp
+    rng = np.random.default_rng(2)
+    base = oracle.bf16_to_f32(rng.integers(0, 0x7F00, 3000).astype(np.uint16)).astype(np.float64)
+    ulp = oracle.bf16_ulp(base)
+    ties = base + ulp / 2
+    vals = np.concatenate([ties, np.nextafter(ties, np.inf), np.nextafter(ties, -np.inf),
+                           rng.standard_normal(3000) * np.exp2(rng.integers(-140, 120, 3000))])
+    vals = vals[np.isfinite(vals)]
+    got = oracle.bf16_to_f32(oracle.bf16_from_f64(vals)).astype(np.float64)
+    want = np.array([rne_bf16_fraction(Fraction(float(v))) for v in vals])
+    assert np.array_equal(got, want)
+
+
+def _fraction_product(x, w, s):
+    xs = oracle_x_fracs(x)
+    M, K = x.shape
+    N = w.shape[0]
+    out = np.empty((M, N))
+    for m in range(M):
+        for n in range(N):
+            acc = sum(xs[m][k] * int(w[n, k]) for k in range(K))
+            out[m, n] = rne_bf16_fraction(acc * Fraction(float(s[n])))
+    return out
+
+
+def oracle_x_fracs(x):
+    from oracle import oracle as O
+    xf = O.bf16_to_f32(x).astype(np.float64)
+    return [[Fraction(float(v)) for v in row] for row in xf]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_exact_product_matches_fractions(oracle, seed):
+    rng = np.random.default_rng(100 + seed)
+    M, N, K = 3, 7, 64 * (1 + seed % 3)
+    # activations spread over ~60 binades, including bf16 subnormals and zeros
+    lo, hi = ((-140, -80) if seed == 0 else (-70, 20))  # within the accumulator's ~100 binades
+    mag = rng.standard_normal((M, K)) * np.exp2(rng.integers(lo, hi, (M, K)))
+    mag[:, ::9] = 0.0
+    x = oracle.bf16_from_f64(mag)
+    w = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    s = (rng.standard_normal(N) * np.exp2(rng.integers(-20, 5, N))).astype(np.float32)
+    bits, y64 = oracle.w8a16_exact(x, w, s)
+    got = oracle.bf16_to_f32(bits).astype(np.float64)
+    want = _fraction_product(x, w, s)
+    assert np.array_equal(got, want)
+
+
+def test_exact_product_rejects_out_of_range_rows(oracle):
+    x = oracle.bf16_from_f64(np.array([[1e30, 1e-30] + [0.0] * 62]))
+    w = np.ones((2, 64), dtype=np.int8)
+    s = np.ones(2, dtype=np.float32)
+    with pytest.raises(ValueError):
+        oracle.w8a16_exact(x, w, s)
+
+
+def test_exact_matches_f64_blas_on_benchmark_inputs(oracle):
+    inp = oracle.gen_inputs(5, 2048, 8192, seed=3)
+    bits, y64 = oracle.w8a16_exact(inp.x, inp.w, inp.s)
+    f = oracle.w8a16_f64(inp.x, inp.w, inp.s)
+    assert np.array_equal(y64, f)
+    assert np.array_equal(oracle.bf16_from_f64(f), bits)
+
+
+def test_one_hot_closed_form(oracle):
+    rng = np.random.default_rng(5)
+    N, K = 96, 192
+    w = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    s = (np.abs(rng.standard_normal(N)) * 0.002 + 1e-4).astype(np.float32)
+    ks = [0, 1, 63, 64, 191]
+    x = np.zeros((len(ks), K), dtype=np.uint16)
+    for m, k in enumerate(ks):
+        x[m, k] = 0x3F80  # 1.0
+    bits, _ = oracle.w8a16_exact(x, w, s)
+    for m, k in enumerate(ks):
+        want = [rne_bf16_fraction(Fraction(float(s[n])) * int(w[n, k])) for n in range(N)]
+        assert np.array_equal(oracle.bf16_to_f32(bits[m]).astype(np.float64), np.array(want))
+
+
+def test_invariants(oracle):
+    inp = oracle.gen_inputs(4, 64, 256, seed=7)
+    x = inp.x.copy()
+    x[1] = x[0]
+    x[3] = 0
+    bits, _ = oracle.w8a16_exact(x, inp.w, inp.s)
+    assert np.array_equal(bits[0], bits[1])
+    assert np.all(oracle.bf16_to_f32(bits[3]) == 0)
+    # scaling by a power of two is exact
+    b2, _ = oracle.w8a16_exact(x, inp.w, (inp.s * 2).astype(np.float32))
+    assert np.array_equal(oracle.bf16_to_f32(b2), 2 * oracle.bf16_to_f32(bits))
+    # linearity in x for disjoint supports: x = a + b with a, b on alternating k
+    a = inp.x[:1].copy(); a[:, 1::2] = 0
+    b = inp.x[:1].copy(); b[:, ::2] = 0
+    _, ya = oracle.w8a16_exact(a, inp.w, inp.s)
+    _, yb = oracle.w8a16_exact(b, inp.w, inp.s)
+    _, yab = oracle.w8a16_exact(inp.x[:1], inp.w, inp.s)
+    assert np.allclose(ya + yb, yab, rtol=1e-12, atol=0)
+
+
+# ------------------------------------------------------------------------------------------------
+# the checker and planted mistakes
+# ------------------------------------------------------------------------------------------------
+
+@pytest.fixture(scope="module")
+def mid(oracle):
+    inp = oracle.gen_inputs(5, 1024, 5120, seed=0)
+    return inp, oracle.w8a16_exact(inp.x, inp.w, inp.s)
+
+
+def test_checker_accepts_exact_and_fp32_paths(oracle, mid):
+    inp, ex = mid
+    assert oracle.check_w8a16(ex[0], inp.x, inp.w, inp.s, exact=ex).ok
+    y32 = oracle.fp32_dequant_linear(inp.x, inp.w, inp.s)
+    assert oracle.check_w8a16(oracle.bf16_from_f64(y32), inp.x, inp.w, inp.s, exact=ex).ok
+    rb, _ = oracle.w8a16_refkernel(inp.x, inp.w, inp.s, 256, 4)
+    rep = oracle.check_w8a16(rb, inp.x, inp.w, inp.s, exact=ex, ref_bits=rb)
+    assert rep.ok and rep.n_over_ref == 0
+
+
+@pytest.mark.parametrize("mistake", ["transpose_k", "no_scale", "shift_k", "flip_row", "truncate", "scale_before_round_to_bf16_x"])
+def test_checker_rejects_planted_mistakes(oracle, mid, mistake):
+    inp, ex = mid
+    x, w, s = inp.x, inp.w, inp.s
+    if mistake == "transpose_k":      # weight k order reversed within each 64-block
+        wk = w.reshape(w.shape[0], -1, 64)[:, :, ::-1].reshape(w.shape)
+        y = oracle.w8a16_exact(x, np.ascontiguousarray(wk), s)[0]
+    elif mistake == "no_scale":
+        y = oracle.bf16_from_f64(oracle.w8a16_f64(x, w, np.ones_like(s)))
+    elif mistake == "shift_k":        # activations shifted by one k
+        y = oracle.w8a16_exact(np.ascontiguousarray(np.roll(x, 1, axis=1)), w, s)[0]
+    elif mistake == "flip_row":       # one output channel with the wrong sign
+        y = ex[0].copy()
+        y[:, 17] ^= 0x8000
+    elif mistake == "truncate":       # round toward zero instead of nearest-even
+        y = (ex[1].astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    else:                             # x rounded to 4 mantissa bits before the product
+        xr = (x & 0xFFF8).astype(np.uint16)
+        y = oracle.w8a16_exact(xr, w, s)[0]
+    assert not oracle.check_w8a16(y, x, w, s, exact=ex).ok
+
+
+def test_literal_bound_is_unreachable_for_bf16_outputs(oracle):
+    """max|err|/RMS <= 1e-2 read against the unrounded product fails for the correctly rounded bf16
+    result itself (outputs reach ~11x RMS, where one bf16 quantum is ~4e-2 RMS); the checker therefore
+    applies the bound beyond the output's own quantum, and at fp32 precision for fp32 outputs."""
+    inp = oracle.gen_inputs(5, 34816, 5120, seed=0)
+    ex = oracle.w8a16_exact(inp.x, inp.w, inp.s)
+    rep = oracle.check_w8a16(ex[0], inp.x, inp.w, inp.s, exact=ex)
+    assert rep.ok and rep.n_diff_exact == 0 and rep.rel_excess == 0.0
+    assert rep.rel_max_f32 > 1e-2
+    assert oracle.check_w8a16_f32(ex[1], inp.x, inp.w, inp.s, exact=ex) == 0.0
+
+
+def test_reference_published_rel_l2_statistic(oracle):
+    """data/measurements.json:429-436: W8A16 rel-L2 vs the exact product is 0.0016-0.0017 at M=1 on
+    the reference's shapes with its test distribution (bench/test_w8a16.py:10-13).  That error is
+    the bf16 rounding of the result: the bf16-rounded exact product must reproduce it."""
+    for (N, K) in ((34816, 5120), (5120, 17408), (16384, 5120), (5120, 6144), (14336, 5120)):
+        inp = oracle.gen_inputs(1, N, K, seed=0, dist="reftest")
+        f = oracle.w8a16_f64(inp.x, inp.w, inp.s)
+        yb = oracle.bf16_to_f32(oracle.bf16_from_f64(f)).astype(np.float64)
+        rel = np.linalg.norm(yb - f) / np.linalg.norm(f)
+        assert 0.0015 <= rel <= 0.00175, (N, K, rel)
+
+
+# ------------------------------------------------------------------------------------------------
+# reference-kernel arithmetic and tile table
+# ------------------------------------------------------------------------------------------------
+
+def test_refkernel_split_semantics(oracle):
+    inp = oracle.gen_inputs(3, 256, 2048, seed=11)
+    ex = oracle.w8a16_exact(inp.x, inp.w, inp.s)
+    for bk, sk in ((256, 1), (256, 2), (128, 4), (64, 8), (256, 8)):
+        rb, r32 = oracle.w8a16_refkernel(inp.x, inp.w, inp.s, bk, sk)
+        rep = oracle.check_w8a16(rb, inp.x, inp.w, inp.s, exact=ex)
+        assert rep.ok, (bk, sk, rep)
+        # fp32 partials summed over splits are within a few fp32 ulps of the exact value
+        assert np.max(np.abs(r32 - ex[1]) / (np.abs(ex[1]) + 1e-3)) < 1e-4
+    with pytest.raises(ValueError):
+        oracle.w8a16_refkernel(inp.x, inp.w, inp.s, 256, 3)
+
+
+def test_ref_pick_config_table(oracle):
+    """Values of plugin/qwen_fastpath/w8a16.py:58-68 at the benchmark shapes."""
+    pc = oracle.ref_pick_config
+    assert pc(5120, 5120) == (16, 32, 256, 4, 4, 3)
+    assert pc(10240, 5120) == (16, 32, 256, 1, 4, 3)
+    assert pc(5120, 8192) == (16, 32, 256, 4, 4, 3)
+    assert pc(34816, 5120) == (16, 32, 256, 1, 4, 3)
+    assert pc(5120, 17408) == (16, 32, 256, 2, 4, 3)
+    assert pc(151936, 5120) == (16, 32, 256, 1, 4, 3)
+    assert pc(248320, 5120) == (16, 64, 256, 1, 8, 3)
+    assert pc(100, 64) == (16, 32, 64, 1, 4, 3)
+    assert pc(5120, 5000) is None
+
+
+# ------------------------------------------------------------------------------------------------
+# draft head
+# ------------------------------------------------------------------------------------------------
+
+def test_quantize_rows_closed_form(oracle):
+    rng = np.random.default_rng(3)
+    V, H = 64, 300
+    wf = rng.standard_normal((V, H)) * np.exp2(rng.integers(-10, 10, (V, 1)))
+    wf[0] = 0.0                   # amax floor 1e-8
+    wf[1, :] = 0.5; wf[1, 7] = -2.0
+    wb = oracle.bf16_from_f64(wf)
+    q, s = oracle.quantize_rows(wb)
+    vals = oracle.bf16_to_f32(wb)
+    inv = np.float32(1.0) / np.float32(127.0)
+    amax = np.maximum(np.abs(vals).max(axis=1), np.float32(1e-8)).astype(np.float32)
+    s_want = (amax * inv).astype(np.float32)
+    assert np.array_equal(s, s_want)
+    q_want = np.clip(np.rint(vals / s_want[:, None]), -127, 127).astype(np.int8)  # float32 IEEE division
+    assert np.array_equal(q, q_want)
+    assert np.all(q[0] == 0)
+    assert q[1, 7] == -127 and np.all(np.abs(q).max(axis=1)[1:] == 127)
+
+
+def test_quantize_rows_vs_torch_reference_form(oracle):
+    """Against the reference's torch expressions (patches.py:144-146) evaluated on the CPU, with the
+    divide-by-127 written as the multiply by fl32(1/127) that PyTorch's CUDA kernel performs."""
+    rng = np.random.default_rng(4)
+    wf = torch.from_numpy(rng.standard_normal((128, 512)).astype(np.float32)).to(torch.bfloat16)
+    blk = wf.float()
+    s = blk.abs().amax(dim=1).clamp_(min=1e-8) * torch.tensor(1.0 / 127.0, dtype=torch.float32)
+    w8 = torch.round(blk / s[:, None]).clamp_(-127, 127).to(torch.int8)
+    q, so = oracle.quantize_rows(wf.view(torch.int16).numpy().view(np.uint16))
+    assert np.array_equal(so, s.numpy())
+    assert np.array_equal(q, w8.numpy())
+
+
+def test_argmax_semantics(oracle):
+    v = np.full((5, 10), -1.0)
+    v[0, 3] = v[0, 6] = 2.0                    # tie -> first
+    v[1, 8] = 5.0                              # max in the pad region -> ignored
+    v[1, 2] = 1.0
+    v[2, 4] = np.nan; v[2, 5] = 9.0            # NaN is the max
+    v[3, :] = -np.inf                          # all -inf -> 0
+    v[4, 9] = 3.0; v[4, 0] = 3.0
+    bits = oracle.bf16_from_f64(v)
+    got = oracle.argmax_rows(bits, n_valid=8, index_offset=100)
+    assert list(got) == [103, 102, 104, 100, 100]
+    # agrees with torch.argmax on the masked row
+    t = torch.from_numpy(oracle.bf16_to_f32(bits).copy())
+    t[:, 8:] = -float("inf")
+    assert list(got - 100) == t.argmax(dim=-1).tolist()
