@@ -55,17 +55,24 @@ def log(*a):
 
 
 class Layer:
-    """One layer's four weight sets plus fixed activations."""
+    """One layer's four weight sets plus fixed activations.  With layout TILED the weights are
+    converted once at set-up (the load-time repack) and only the tiled image is kept."""
 
-    def __init__(self, torch, dev, seed: int, M: int):
+    def __init__(self, torch, qf, dev, seed: int, M: int, layout: int):
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
+        self.layout = layout
         self.w, self.s, self.x = {}, {}, {}
         for name, (N, K) in GEMMS.items():
             w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
-            self.w[name] = w.t()  # [K, N] view with stride (1, K), as vLLM holds it
+            w_t = w.t()  # [K, N] view with stride (1, K), as vLLM holds it
+            self.w[name] = qf.to_tiled(w_t) if layout == qf.TILED else w_t
+            del w, w_t
             self.s[name] = (torch.randn(N, device=dev, generator=g).abs() * 0.002 + 1e-4).float()
             self.x[name] = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+
+    def gemm(self, qf, torch, name, cfg=None):
+        return qf.w8a16_mm(self.x[name], self.w[name], self.s[name], cfg, torch.bfloat16, self.layout)
 
 
 def capture(torch, fn):
@@ -150,11 +157,14 @@ def main():
     ap.add_argument("--profile-gemm", choices=list(GEMMS), default=None)
     ap.add_argument("--iters", type=int, default=200)
     ap.add_argument("--copy-probe", action="store_true")
+    ap.add_argument("--layout", choices=["tiled", "rowmajor"], default="tiled",
+                    help="weight layout: tiled = pre-permuted at load (default), rowmajor = checkpoint layout")
+    ap.add_argument("--cfg", default=None, help="explicit config kernel,split_k,tiles,waves,depth,hint (profile mode)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        log("bench.py: this build measures one GPU only (the op is single-GPU; see DESIGN.md for how it "
-            "would shard); run with --gpus 1")
+        log("bench.py: this build measures one GPU only (the W8A16 op runs on a single GPU); "
+            "run with --gpus 1")
         sys.exit(2)
 
     import torch
@@ -162,6 +172,7 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    layout = qf.TILED if args.layout == "tiled" else qf.ROWMAJOR
 
     if args.copy_probe:
         n = 1 << 30
@@ -175,14 +186,13 @@ def main():
 
     if args.profile_gemm:
         N, K = GEMMS[args.profile_gemm]
-        sets = [Layer(torch, dev, 1000 + i, M_TOKENS) for i in range(args.layers)]
+        cfg = qf.W8A16Config(*[int(v) for v in args.cfg.split(",")]) if args.cfg else None
+        sets = [Layer(torch, qf, dev, 1000 + i, M_TOKENS, layout) for i in range(args.layers)]
         for i in range(args.iters):
-            L_ = sets[i % len(sets)]
-            qf.w8a16_mm(L_.x[args.profile_gemm], L_.w[args.profile_gemm], L_.s[args.profile_gemm], None,
-                        torch.bfloat16)
+            sets[i % len(sets)].gemm(qf, torch, args.profile_gemm, cfg)
         torch.cuda.synchronize()
-        log(f"profile: {args.iters} launches of {args.profile_gemm} M={M_TOKENS} N={N} K={K} "
-            f"cfg={tuple(qf.resolve_config(M_TOKENS, N, K))}")
+        log(f"profile: {args.iters} launches of {args.profile_gemm} M={M_TOKENS} N={N} K={K} layout={args.layout} "
+            f"cfg={tuple(cfg) if cfg else tuple(qf.resolve_config(M_TOKENS, N, K, layout))}")
         return
 
     if args.workload == "stack64":
@@ -192,11 +202,11 @@ def main():
     M = M_TOKENS
     R = max(1, args.layers)
     log(f"bench: allocating {R} layers ({R * sum(N * K for N, K in GEMMS.values()) / 1e9:.2f} GB of int8 weights)")
-    layers = [Layer(torch, dev, 1000 + i, M) for i in range(R)]
+    layers = [Layer(torch, qf, dev, 1000 + i, M, layout) for i in range(R)]
     bytes_per_step = sum(algo_bytes(M, N, K) for (N, K) in GEMMS.values())
 
     def step_fn(L_):
-        return lambda: [qf.w8a16_mm(L_.x[n], L_.w[n], L_.s[n], None, torch.bfloat16) for n in GEMMS]
+        return lambda: [L_.gemm(qf, torch, n) for n in GEMMS]
 
     graphs = [capture(torch, step_fn(L_))[0] for L_ in layers]
 
@@ -219,8 +229,7 @@ def main():
     dominant_us = None
     for name, (N, K) in GEMMS.items():
         reps = 8
-        g, _ = capture(torch, lambda n=name: [qf.w8a16_mm(L_.x[n], L_.w[n], L_.s[n], None, torch.bfloat16)
-                                              for _ in range(reps) for L_ in layers])
+        g, _ = capture(torch, lambda n=name: [L_.gemm(qf, torch, n) for _ in range(reps) for L_ in layers])
         launches = reps * R
         g.replay()
         torch.cuda.synchronize()
@@ -235,7 +244,7 @@ def main():
             times.append(e0.elapsed_time(e1) * 1e3 / launches)
         us = sorted(times)[len(times) // 2]
         b = algo_bytes(M, N, K)
-        cfg = qf.resolve_config(M, N, K)
+        cfg = qf.resolve_config(M, N, K, layout)
         per_gemm[name] = {"N": N, "K": K, "us": round(us, 2), "GB_s": round(b / us / 1e3, 1),
                           "pct_peak": round(100 * b / us / 1e3 / PEAK_GBS, 1), "config": list(cfg)}
         log(f"  {name:8s} N={N:6d} K={K:6d}: {us:7.2f} us  {b / us / 1e3:7.0f} GB/s  "
@@ -250,6 +259,10 @@ def main():
                 "frac": round(achieved / PEAK_GBS, 4), "traffic": read_traffic(),
                 "kernel": f"{DOMINANT} M={M} N={GEMMS[DOMINANT][0]} K={GEMMS[DOMINANT][1]}",
                 "algorithmic_bytes_per_launch": dom_bytes, "mean_launch_us": round(dominant_us, 2)}
+
+    ceiling = read_ceiling(torch, qf, dev, algo_bytes(M, *GEMMS[DOMINANT]))
+    log(f"  read probe ({algo_bytes(M, *GEMMS[DOMINANT]) / 1e6:.0f} MB windows): {ceiling:.0f} GB/s")
+    roofline["read_probe_GB_s"] = round(ceiling, 1)
 
     cpu = None if args.no_cpu else cpu_baseline(M)
 
@@ -268,7 +281,7 @@ def main():
         "data": "synthetic (seeded int8 weights, fp32 scales, bf16 N(0,1) activations)",
         "config": {"workload": "dense GQA 27B-class layer GEMMs at M=5: qkv 10240x5120, o_proj 5120x8192, "
                                "gate_up 34816x5120, down 5120x17408 (N x K int8)",
-                   "M": M, "layers_rotated": R, "bytes_per_step": bytes_per_step,
+                   "M": M, "layers_rotated": R, "bytes_per_step": bytes_per_step, "weight_layout": args.layout,
                    "timing": "one hipGraph per layer, replayed; weights rotate over distinct layers"},
         "us_per_layer": round(ms_per_step * 1e3, 2),
         "pct_of_peak": round(100 * value / PEAK_GBS, 2),
@@ -279,6 +292,39 @@ def main():
     print(json.dumps(line), flush=True)
 
 
+def read_ceiling(torch, qf, dev, window: int) -> float:
+    """GB/s of the library's read probe over rotating windows of `window` bytes in a 2 GB buffer
+    (the practical HBM read ceiling at the dominant GEMM's size), timed like the GEMMs."""
+    from qwen_fastpath import _lib as L
+    window = window // 4096 * 4096
+    nwin = 8
+    buf = torch.empty(nwin * window, dtype=torch.uint8, device=dev)
+    buf.fill_(1)
+    blocks = 256 * 8
+    sink = torch.empty(blocks, dtype=torch.int32, device=dev)
+    lib = L.load()
+
+    def fn():
+        st = torch.cuda.current_stream().cuda_stream
+        for i in range(nwin):
+            L.check(lib.qf_read_probe(buf.data_ptr() + i * window, window, sink.data_ptr(), blocks, st), "probe")
+
+    g, _ = capture(torch, fn)
+    g.replay()
+    times = []
+    for _ in range(10):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e3 / nwin)
+    us = sorted(times)[len(times) // 2]
+    del buf
+    return window / us / 1e3
+
+
 def run_stack64(torch, qf, dev, args):
     """64 layers x 4 GEMMs at M=5 with distinct weights, one hipGraph per decode step.  Glue between
     GEMMs: o_proj reads the first 8192 qkv outputs, down reads silu(gate) * up; each GEMM input is
@@ -286,7 +332,8 @@ def run_stack64(torch, qf, dev, args):
     M = M_TOKENS
     nl = 64
     log(f"stack64: allocating {nl} layers ({nl * sum(N * K for N, K in GEMMS.values()) / 1e9:.1f} GB)")
-    layers = [Layer(torch, dev, 5000 + i, M) for i in range(nl)]
+    layout = qf.TILED if args.layout == "tiled" else qf.ROWMAJOR
+    layers = [Layer(torch, qf, dev, 5000 + i, M, layout) for i in range(nl)]
     x0 = torch.randn(M, 5120, device=dev).to(torch.bfloat16)
 
     def rms(t):
@@ -296,12 +343,12 @@ def run_stack64(torch, qf, dev, args):
     def step():
         h = x0
         for L_ in layers:
-            qkv = qf.w8a16_mm(h, L_.w["qkv"], L_.s["qkv"], None, torch.bfloat16)
-            o = qf.w8a16_mm(rms(qkv[:, :8192]), L_.w["o_proj"], L_.s["o_proj"], None, torch.bfloat16)
-            gu = qf.w8a16_mm(rms(o), L_.w["gate_up"], L_.s["gate_up"], None, torch.bfloat16)
+            mm = lambda a, n: qf.w8a16_mm(a, L_.w[n], L_.s[n], None, torch.bfloat16, layout)  # noqa: E731
+            qkv = mm(h, "qkv")
+            o = mm(rms(qkv[:, :8192]), "o_proj")
+            gu = mm(rms(o), "gate_up")
             g, u = gu[:, :17408].float(), gu[:, 17408:].float()
-            d = qf.w8a16_mm(rms(torch.nn.functional.silu(g) * u), L_.w["down"], L_.s["down"], None,
-                            torch.bfloat16)
+            d = mm(rms(torch.nn.functional.silu(g) * u), "down")
             h = rms(d)
         return h
 

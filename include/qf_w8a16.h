@@ -40,6 +40,8 @@ extern "C" {
 #define QF_W8A16_MAX_M 16
 /* K must be a multiple of this (the reference's smallest BLOCK_K, w8a16.py:63-68). */
 #define QF_W8A16_K_ALIGN 64
+/* Bytes at the front of a split-K workspace that hold arrival counters (one per workgroup column). */
+#define QF_W8A16_COUNTER_BYTES 65536
 
 typedef enum qf_status {
   QF_OK = 0,
@@ -71,7 +73,9 @@ typedef struct qf_w8a16_config {
   int32_t waves;           /* wavefronts per workgroup */
   int32_t depth;           /* weight prefetch depth in k-steps (MFMA) */
   int32_t load_hint;       /* 0: default weight loads, 1: non-temporal (streaming) loads */
-  int32_t reserved[2];
+  int32_t k_waves;         /* MFMA: wavefronts per workgroup that split K (waves % k_waves == 0) */
+  int32_t reduce;          /* MFMA, split_k > 1: 0 = the last workgroup of an n-block sums the
+                              splits, 1 = a second kernel does */
 } qf_w8a16_config;
 
 /* ABI version of the loaded library (QF_W8A16_ABI_VERSION). */
@@ -85,14 +89,19 @@ const char* qf_status_string(int status);
  * pick_config() returning None.  Host-only; touches no device. */
 int qf_w8a16_pick_config(int M, int N, int K, int layout, qf_w8a16_config* cfg);
 
-/* Bytes of device workspace qf_w8a16_gemm needs for this call (0 when split_k == 1).
- * cfg may be NULL (automatic configuration).  Host-only. */
+/* Bytes of device workspace qf_w8a16_gemm needs for this call (0 when split_k == 1): arrival
+ * counters followed by the split partial sums.  cfg may be NULL (automatic configuration).
+ * Host-only. */
 size_t qf_w8a16_workspace_bytes(int M, int N, int K, int layout, const qf_w8a16_config* cfg);
 
 /* y = bf16/fp32( scale * (x . w^T) ).  cfg may be NULL.  Alignment contract: x, w, scale 16-byte
  * aligned, ldx % 8 == 0, ldw % 16 == 0 (row-major layout) and y 16-byte aligned; otherwise
- * QF_ERR_UNSUPPORTED.  Any ldy >= N works (vector stores when ldy % 4 == 0).  The workspace (if
- * any) is fully overwritten before it is read, so it needs no clearing. */
+ * QF_ERR_UNSUPPORTED.  Any ldy >= N works (vector stores when ldy % 4 == 0).
+ * Workspace contract (split_k > 1): its first QF_W8A16_COUNTER_BYTES bytes are arrival counters
+ * that must be zero when a call starts; every call leaves them zero again, so a workspace zeroed
+ * once can be reused by any number of calls issued in order on one stream (and by graph replays).
+ * Calls that may run at the same time need distinct workspaces.  The partial sums that follow need
+ * no clearing. */
 int qf_w8a16_gemm(const uint16_t* x, int64_t ldx,
                   const int8_t* w, int64_t ldw, int layout,
                   const float* scale,
@@ -126,6 +135,12 @@ int qf_quantize_rows_int8(const uint16_t* w, int64_t ldw, int8_t* q, float* s,
  * out[m] = index + index_offset (int64).  Reference: plugin/qwen_fastpath/patches.py:182-185. */
 int qf_argmax_rows_bf16(const uint16_t* logits, int64_t ld, int M, int N, int n_valid,
                         int64_t index_offset, int64_t* out, void* stream);
+
+/* Diagnostic: read every byte of [buf, buf + bytes) once with 16-byte non-temporal loads across
+ * `blocks` workgroups of 256 threads, writing one xor per workgroup to sink[blocks].  The practical
+ * HBM read ceiling the GEMM is compared with; the analogue of the reference's device-copy probe
+ * (bench/kernels/linear_kernels.py:87-89).  bytes % 16 == 0, buf 16-byte aligned. */
+int qf_read_probe(const void* buf, size_t bytes, uint32_t* sink, int blocks, void* stream);
 
 #ifdef __cplusplus
 }

@@ -23,6 +23,9 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <mutex>
+#include <unordered_set>
+
 #include "qf_w8a16.h"
 
 namespace qf {
@@ -36,14 +39,16 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 constexpr int kWave = 64;
 constexpr int kTileN = 16;     // output channels per MFMA tile
 constexpr int kStepK = 64;     // k covered by one 16-byte-per-lane weight fragment of a tile
-constexpr size_t kMaxLds = 65536;
+constexpr size_t kMaxLds = 160 * 1024 - 256;  // gfx950 LDS per workgroup; static __shared__ uses the rest
+constexpr size_t kDefaultLds = 64 * 1024;      // above this a kernel needs the dynamic-LDS attribute raised
 
 struct GemmArgs {
   const uint16_t* x;
   const int8_t* w;
   const float* scale;
   void* y;
-  float* partial;  // [split_k][M][n_pad] fp32 when split_k > 1
+  float* partial;      // [split_k][M][n_pad] fp32 when split_k > 1
+  unsigned* counters;  // [grid.x] arrival counters (MFMA, split_k > 1): zero on entry and on exit
   int64_t ldx;
   int64_t ldw;
   int64_t ldy;
@@ -53,6 +58,7 @@ struct GemmArgs {
   int split_k;
   int out_f32;
   int vec_out;     // rows of y are 8-byte (bf16) / 16-byte (fp32) aligned: vector stores allowed
+  int fused_reduce;  // MFMA, split_k > 1: the last workgroup of an n-block reduces (else a second kernel)
 };
 
 // ---------------------------------------------------------------------------------------------
@@ -147,6 +153,61 @@ __device__ __forceinline__ f32x4_t load_scale4(const float* scale, int N, int n)
   return s;
 }
 
+// LDS row pitch (bytes) of a staged x slice of `steps` k-steps: the row bytes plus 32, so the rows
+// that the 16 lanes of an MFMA fragment read start in distinct 32-byte bank groups.
+__host__ __device__ __forceinline__ int x_pitch(int steps) { return steps * kStepK * 2 + 32; }
+
+// Copy of x[0:M][64*s_begin : 64*(s_begin + steps)] into LDS (row m at byte m * x_pitch(steps)) in
+// 16-byte pieces, in two phases so that the caller can issue its weight requests in between:
+// load() requests the first kBatch pieces of every thread into registers, store() writes them to
+// LDS (waiting only for these loads, which were issued first) and copies any remaining pieces.
+// Pieces are indexed (row << shift) | column, the column space padded to a power of two, so row and
+// column come from a shift and a mask.
+template <int THREADS>
+struct XStage {
+  static constexpr int kBatch = 8;
+  u32x4_t v[kBatch];
+  const uint16_t* src0;
+  int row_pieces, shift, mask, span, pitch;
+
+  __device__ __forceinline__ XStage(const GemmArgs& a, int s_begin, int steps) {
+    row_pieces = steps * (kStepK / 8);
+    shift = 32 - __builtin_clz((row_pieces - 1) | 1);  // ceil(log2(row_pieces)), >= 1
+    mask = (1 << shift) - 1;
+    span = a.M << shift;
+    pitch = x_pitch(steps);
+    src0 = a.x + (int64_t)s_begin * kStepK;
+  }
+
+  __device__ __forceinline__ void load_batch(const GemmArgs& a, int base) {
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int f = base + b * THREADS + (int)threadIdx.x;
+      const int m = f >> shift, j = f & mask;
+      if (f < span && j < row_pieces) v[b] = *reinterpret_cast<const u32x4_t*>(src0 + (int64_t)m * a.ldx + j * 8);
+    }
+  }
+
+  __device__ __forceinline__ void store_batch(uint8_t* smem, int base) {
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int f = base + b * THREADS + (int)threadIdx.x;
+      const int m = f >> shift, j = f & mask;
+      if (f < span && j < row_pieces) *reinterpret_cast<u32x4_t*>(smem + m * pitch + j * 16) = v[b];
+    }
+  }
+
+  __device__ __forceinline__ void load(const GemmArgs& a) { load_batch(a, 0); }
+
+  __device__ __forceinline__ void store(const GemmArgs& a, uint8_t* smem) {
+    store_batch(smem, 0);
+    for (int base = THREADS * kBatch; base < span; base += THREADS * kBatch) {
+      load_batch(a, base);
+      store_batch(smem, base);
+    }
+  }
+};
+
 // k-steps [begin, end) of split `split` out of `splits` over `ksteps` (balanced, deterministic).
 __device__ __forceinline__ void split_range(int split, int splits, int ksteps, int& begin, int& end) {
   begin = (int)(((int64_t)split * ksteps) / splits);
@@ -156,134 +217,212 @@ __device__ __forceinline__ void split_range(int split, int splits, int ksteps, i
 // ---------------------------------------------------------------------------------------------
 // MFMA kernel
 //
-// Workgroup = WAVES wavefronts; wavefront w owns NT consecutive 16-row n-tiles; blockIdx.y is the
-// K split.  Lane l (group g = l / 16, r = l % 16) loads, for every 64-k step s of the split:
+// Workgroup = WN x WK wavefronts over NT-tile groups: wavefront (wn, wk) owns the NT consecutive
+// 16-row n-tiles of group wn and slice wk of the workgroup's k-steps; blockIdx.y is the split of K
+// across workgroups.  Lane l (group g = l / 16, r = l % 16) loads, for every 64-k step s:
 //   rowmajor: w[tile*16 + r][s*64 + 16g .. +15]
 //   tiled:    bytes [16 l, 16 l + 16) of the 1 KiB tile (tile, s), which hold the same values
-// and the activation chunk x[r][s*64 + 16g .. +15] from LDS (zero when r >= M).  Both MFMA operands
+// and the activation chunk x[r][s*64 + 16g .. +15] from LDS (row M - 1 when r >= M).  Both MFMA operands
 // index k identically per lane, so the k order inside a step is immaterial to the product.
-// LDS holds x as [chunk c of 16 k][m][16 bf16] so that the 16 lanes of a group read 16
-// consecutive 32-byte pieces.
+// LDS holds the workgroup's x slice row-major with a pitch of (row bytes + 32), so the 16 rows a
+// fragment read touches start in distinct 32-byte bank groups.
+//
+// Reductions, all in a fixed order: the WK slices of a tile are summed through LDS in slice order;
+// with split_k > 1 each workgroup writes its partial tile to the workspace, and the last workgroup
+// of an n-block to finish (a per-n-block arrival counter in the workspace) sums the split_k partials
+// in split order, applies the scale and writes y, then resets the counter to zero.
 // ---------------------------------------------------------------------------------------------
-template <int LAYOUT, int NT, int WAVES, int DEPTH, bool NTH>
-__global__ void __launch_bounds__(WAVES * kWave) w8a16_mfma_kernel(const GemmArgs a) {
+template <int LAYOUT, int NT, int WN, int WK, int DEPTH, bool NTH>
+__global__ void __launch_bounds__(WN * WK * kWave) w8a16_mfma_kernel(const GemmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ int last_arrival;
+  constexpr int WAVES = WN * WK;
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // uniform: scalar registers
+  const int wn = wave % WN;
+  const int wk = wave / WN;
   const int g = lane >> 4;
   const int r = lane & 15;
   const int split = blockIdx.y;
   int s_begin, s_end;
   split_range(split, a.split_k, a.ksteps, s_begin, s_end);
-  const int nsteps = s_end - s_begin;
+  const int wg_steps = s_end - s_begin;  // k-steps staged by this workgroup
+  int k_lo, k_hi;
+  split_range(wk, WK, wg_steps, k_lo, k_hi);  // this wavefront's slice, relative to s_begin
   const int ntiles = a.n_pad / kTileN;
-  const int tile0 = (blockIdx.x * WAVES + wave) * NT;
-  const bool wave_active = tile0 < ntiles;
+  const int tile0 = (blockIdx.x * WN + wn) * NT;
+  // >= 1: the host keeps wg_steps >= WK.  A wavefront whose tiles lie past N (only in the last
+  // workgroup column) runs one clamped step instead of skipping the loop, so no branch surrounds
+  // the loads; its results are never stored.
+  const int nsteps = tile0 < ntiles ? k_hi - k_lo : 1;
 
-  // Weight fragment pointers at step s_begin, and the byte stride between steps.
+  // Weight fragment pointers at this wavefront's first step, and the byte stride between steps.
   const int8_t* wp[NT];
   constexpr int64_t step_bytes = (LAYOUT == QF_LAYOUT_ROWMAJOR) ? kStepK : kTileN * kStepK;
+  const int s0 = s_begin + k_lo;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int tile = min(tile0 + t, ntiles - 1);
     if constexpr (LAYOUT == QF_LAYOUT_ROWMAJOR) {
       const int row = min(tile * kTileN + r, a.N - 1);
-      wp[t] = a.w + (int64_t)row * a.ldw + (int64_t)s_begin * kStepK + g * 16;
+      wp[t] = a.w + (int64_t)row * a.ldw + (int64_t)s0 * kStepK + g * 16;
     } else {
-      wp[t] = a.w + (((int64_t)tile * a.ksteps + s_begin) * kWave + lane) * 16;
+      wp[t] = a.w + (((int64_t)tile * a.ksteps + s0) * kWave + lane) * 16;
     }
   }
 
-  // Issue the first DEPTH steps of weight loads before staging x, so the LDS fill overlaps them.
-  // Every load in this kernel is unconditional: step indices past the split are clamped to its
-  // last step (an in-bounds re-read), and the matching activation fragment is the zero step, so
-  // those extra MFMAs add exactly 0.  This keeps the loop free of branches around loads, which
-  // lets the compiler keep DEPTH steps of loads in flight.
+  // Prologue: the x slice of the workgroup (all WK k-slices) is requested first, then the first
+  // DEPTH steps of weights; writing x to LDS waits only for the x requests (vmcnt retires in issue
+  // order), so the weight requests stay in flight across the barrier.
+  // Every weight load in this kernel is unconditional: step indices past the slice are clamped to its
+  // last step (an in-bounds re-read of a line just fetched) and their math is skipped.  Keeping
+  // branches away from the loads lets the compiler keep DEPTH steps of loads in flight.
   // The ring has DEPTH + 1 slots: at step s the load for step s + DEPTH goes into the slot freed at
   // step s - 1, so it can be issued before step s's fragment is consumed.
+  const int pitch = x_pitch(wg_steps);
+  XStage<WAVES * kWave> xst(a, s_begin, wg_steps);
+  xst.load(a);
+  __builtin_amdgcn_sched_barrier(0);  // the x requests go out before the weight requests
   constexpr int RING = DEPTH + 1;
   u32x4_t buf[RING][NT];
-  if (wave_active) {
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-      const int sd = min(d, nsteps - 1);
+  for (int d = 0; d < DEPTH; ++d) {
+    const int sd = min(d, nsteps - 1);
 #pragma unroll
-      for (int t = 0; t < NT; ++t) buf[d][t] = load16<NTH>(wp[t] + sd * step_bytes);
-    }
+    for (int t = 0; t < NT; ++t) buf[d][t] = load16<NTH>(wp[t] + sd * step_bytes);
   }
-
-  // Stage x[0:M][kb:kb + 64*nsteps] into LDS: piece (m, c) = 32 bytes = k kb+16c .. +15 of row m,
-  // stored at ((c * M) + m) * 32.  One more step of zeros follows (the zero step).
-  {
-    const int nchunks = nsteps * 4;
-    const int total = a.M * nchunks;
-    const int64_t kb = (int64_t)s_begin * kStepK;
-    for (int i = threadIdx.x; i < total; i += WAVES * kWave) {
-      const int m = i / nchunks;
-      const int c = i - m * nchunks;
-      const u32x4_t* src = reinterpret_cast<const u32x4_t*>(a.x + (int64_t)m * a.ldx + kb + c * 16);
-      const u32x4_t v0 = src[0];
-      const u32x4_t v1 = src[1];
-      u32x4_t* dst = reinterpret_cast<u32x4_t*>(smem + ((size_t)c * a.M + m) * 32);
-      dst[0] = v0;
-      dst[1] = v1;
-    }
-    const u32x4_t z = {0u, 0u, 0u, 0u};
-    u32x4_t* zs = reinterpret_cast<u32x4_t*>(smem + (size_t)nchunks * a.M * 32);
-    for (int i = threadIdx.x; i < 4 * a.M * 2; i += WAVES * kWave) zs[i] = z;
-  }
+  __builtin_amdgcn_sched_barrier(0);
+  xst.store(a, smem);
   __syncthreads();
-  if (!wave_active) return;
 
   f32x4_t acc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
 
-  // Lanes with r >= M read the zero step at every step (stride 0).
-  const size_t xs_step = (size_t)4 * a.M * 32;  // 4 chunks per step
-  const bool xrow = r < a.M;
-  const uint8_t* xs = xrow ? smem + ((size_t)g * a.M + r) * 32 : smem + (size_t)nsteps * xs_step;
-  const size_t xs_stride = xrow ? xs_step : 0;
+  {
+    // Lane (g, r) reads x[r][k + 16g .. +15] of each step.  Lanes of token rows r >= M read row M - 1
+    // instead: MFMA column r only feeds output column r, which is never stored.
+    const int xr = min(r, a.M - 1);
+    const uint8_t* xs = smem + xr * pitch + (k_lo * kStepK + 16 * g) * 2;
+    constexpr int xs_stride = kStepK * 2;
 
-  for (int base = 0; base < nsteps; base += RING) {
+    for (int base = 0; base < nsteps; base += RING) {
 #pragma unroll
-    for (int d = 0; d < RING; ++d) {
-      const int s = base + d;
-      const int sn = min(s + DEPTH, nsteps - 1);
+      for (int d = 0; d < RING; ++d) {
+        const int s = base + d;
+        const int sn = min(s + DEPTH, nsteps - 1);
 #pragma unroll
-      for (int t = 0; t < NT; ++t) buf[(d + DEPTH) % RING][t] = load16<NTH>(wp[t] + (int64_t)sn * step_bytes);
-      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch issue ahead of this step's math
-      const int sx = min(s, nsteps);      // nsteps -> zero step
-      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(xs + (size_t)sx * xs_stride);
-      const bf16x8_t xb0 = __builtin_bit_cast(bf16x8_t, p[0]);
-      const bf16x8_t xb1 = __builtin_bit_cast(bf16x8_t, p[1]);
+        for (int t = 0; t < NT; ++t) buf[(d + DEPTH) % RING][t] = load16<NTH>(wp[t] + (int64_t)sn * step_bytes);
+        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch issue ahead of this step's math
+        if (s < nsteps) {                   // uniform: steps past the slice only keep loads in flight
+          const u32x4_t* p = reinterpret_cast<const u32x4_t*>(xs + (size_t)s * xs_stride);
+          const bf16x8_t xb0 = __builtin_bit_cast(bf16x8_t, p[0]);
+          const bf16x8_t xb1 = __builtin_bit_cast(bf16x8_t, p[1]);
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            bf16x8_t w0, w1;
+            dequant16(buf[d][t], w0, w1);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, xb0, acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, xb1, acc[t], 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+
+  // Sum the WK slices through LDS (the x slice is no longer read): slice 0 adds slices 1.. WK-1.
+  if constexpr (WK > 1) {
+    __syncthreads();
+    f32x4_t* red = reinterpret_cast<f32x4_t*>(smem);
+    if (wk > 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) red[((wk * WN + wn) * NT + t) * kWave + lane] = acc[t];
+    }
+    __syncthreads();
+    if (wk == 0) {
+      for (int j = 1; j < WK; ++j) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] += red[((j * WN + wn) * NT + t) * kWave + lane];
+      }
+    }
+  }
+
+  // Lane (g, r) of slice 0 holds C[n = tile*16 + 4g + i][m = r], i = 0..3.
+  const bool holder = wk == 0 && tile0 < ntiles && r < a.M;
+  if (a.split_k == 1) {
+    if (holder) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        bf16x8_t w0, w1;
-        dequant16(buf[d][t], w0, w1);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, xb0, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, xb1, acc[t], 0, 0, 0);
+        const int tile = tile0 + t;
+        const int n = tile * kTileN + 4 * g;
+        if (tile < ntiles && n < a.N) {
+          const f32x4_t sc = load_scale4(a.scale, a.N, n);
+          store_out4(a.y, a.ldy, a.out_f32, a.vec_out, r, n, min(4, a.N - n), acc[t] * sc);
+        }
       }
     }
+    return;
   }
 
-  // Lane (g, r) holds C[n = tile*16 + 4g + i][m = r], i = 0..3.
-  if (r >= a.M) return;
+  // split_k > 1: publish this workgroup's partial tiles, then count arrivals for the n-block.
+  const int64_t plane = (int64_t)a.M * a.n_pad;
+  if (!a.fused_reduce) {  // the second-pass kernel reduces
+    if (holder) {
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const int tile = tile0 + t;
-    if (tile >= ntiles) break;
-    const int n = tile * kTileN + 4 * g;
-    if (a.split_k == 1) {
-      if (n < a.N) {
-        const f32x4_t sc = load_scale4(a.scale, a.N, n);
-        store_out4(a.y, a.ldy, a.out_f32, a.vec_out, r, n, min(4, a.N - n), acc[t] * sc);
+      for (int t = 0; t < NT; ++t) {
+        const int tile = tile0 + t;
+        if (tile < ntiles) {
+          float* dst = a.partial + (int64_t)split * plane + (int64_t)r * a.n_pad + tile * kTileN + 4 * g;
+          *reinterpret_cast<f32x4_t*>(dst) = acc[t];
+        }
       }
-    } else {
-      float* dst = a.partial + ((int64_t)split * a.M + r) * a.n_pad + n;
-      *reinterpret_cast<f32x4_t*>(dst) = acc[t];
+    }
+    return;
+  }
+  if (holder) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int tile = tile0 + t;
+      if (tile < ntiles) {
+        float* dst = a.partial + (int64_t)split * plane + (int64_t)r * a.n_pad + tile * kTileN + 4 * g;
+        *reinterpret_cast<f32x4_t*>(dst) = acc[t];
+      }
     }
   }
+  // Arrival count.  The barrier orders every wavefront's partial stores before thread 0's
+  // device-scope release increment (which writes the XCD's L2 back).  The last arrival reads the
+  // partials with device-coherent loads, which fetch from the coherence point rather than a stale
+  // L2 line, so no cache-wide invalidate is needed; they are issued only once the increment has
+  // returned and selected this workgroup.
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(a.counters + blockIdx.x, 1u, __ATOMIC_RELEASE,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    last_arrival = prev == (unsigned)(a.split_k - 1);
+  }
+  __syncthreads();
+  if (!last_arrival) return;
+  if (holder) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int tile = tile0 + t;
+      const int n = tile * kTileN + 4 * g;
+      if (tile < ntiles && n < a.N) {
+        float* src = a.partial + (int64_t)r * a.n_pad + n;
+        f32x4_t sum = {0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < a.split_k; ++j) {
+          f32x4_t v;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            v[i] = __hip_atomic_load(src + j * plane + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          sum = j == 0 ? v : sum + v;
+        }
+        const f32x4_t sc = load_scale4(a.scale, a.N, n);
+        store_out4(a.y, a.ldy, a.out_f32, a.vec_out, r, n, min(4, a.N - n), sum * sc);
+      }
+    }
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(a.counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -297,7 +436,7 @@ template <int MM, int RPW, int WAVES, bool NTH>
 __global__ void __launch_bounds__(WAVES * kWave) w8a16_gemv_kernel(const GemmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int split = blockIdx.y;
   int s_begin, s_end;
   split_range(split, a.split_k, a.ksteps, s_begin, s_end);
@@ -306,15 +445,14 @@ __global__ void __launch_bounds__(WAVES * kWave) w8a16_gemv_kernel(const GemmArg
   const int row0 = (blockIdx.x * WAVES + wave) * RPW;
   const bool wave_active = row0 < a.N;
 
-  // Stage x rows (klen bf16 each) into LDS, 16 bytes per thread per iteration.
+  // Stage x rows (klen bf16 each) into LDS, row m at byte m * klen * 2.
   {
     const int per_row = klen / 8;
-    const int total = MM * per_row;
-    for (int i = threadIdx.x; i < total; i += WAVES * kWave) {
-      const int m = i / per_row;
-      const int c = i - m * per_row;
-      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(a.x + (int64_t)m * a.ldx + kb + c * 8);
-      *reinterpret_cast<u32x4_t*>(smem + ((size_t)m * klen + c * 8) * 2) = v;
+    for (int m = 0; m < MM; ++m) {
+      for (int c = threadIdx.x; c < per_row; c += WAVES * kWave) {
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(a.x + (int64_t)m * a.ldx + kb + c * 8);
+        *reinterpret_cast<u32x4_t*>(smem + ((size_t)m * klen + c * 8) * 2) = v;
+      }
     }
   }
   __syncthreads();
@@ -538,39 +676,66 @@ __global__ void __launch_bounds__(256) argmax_rows_kernel(const uint16_t* logits
 }
 
 // ---------------------------------------------------------------------------------------------
+// Read-bandwidth probe: every byte of [buf, buf + bytes) read once with 16-byte loads, grid-stride.
+// One 32-bit xor per workgroup is written to sink so the loads cannot be dropped.
+// ---------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) read_probe_kernel(const u32x4_t* buf, int64_t n16, uint32_t* sink) {
+  __shared__ uint32_t red[256 / kWave];
+  uint32_t acc = 0;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const u32x4_t a = __builtin_nontemporal_load(buf + i);
+    const u32x4_t b = __builtin_nontemporal_load(buf + i + stride);
+    const u32x4_t c = __builtin_nontemporal_load(buf + i + 2 * stride);
+    const u32x4_t d = __builtin_nontemporal_load(buf + i + 3 * stride);
+    acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+  }
+  for (; i < n16; i += stride) {
+    const u32x4_t a = __builtin_nontemporal_load(buf + i);
+    acc ^= a.x ^ a.y ^ a.z ^ a.w;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) acc ^= __shfl_xor(acc, off, kWave);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) sink[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
+// ---------------------------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------------------------
 using KernelFn = void (*)(GemmArgs);
 
-template <int L, int NT, int W, int D>
-KernelFn mfma_fn(int hint) {
-  return hint ? &w8a16_mfma_kernel<L, NT, W, D, true> : &w8a16_mfma_kernel<L, NT, W, D, false>;
+// MFMA instantiations: layout x NT {1, 2} x (WN, WK) x DEPTH {4, 8} x load hint.
+template <int L, int NT, int WN, int WK>
+KernelFn mfma_fn(int depth, int hint) {
+  if (depth == 4) return hint ? &w8a16_mfma_kernel<L, NT, WN, WK, 4, true> : &w8a16_mfma_kernel<L, NT, WN, WK, 4, false>;
+  if (depth == 8) return hint ? &w8a16_mfma_kernel<L, NT, WN, WK, 8, true> : &w8a16_mfma_kernel<L, NT, WN, WK, 8, false>;
+  return nullptr;
 }
 
-template <int L, int NT, int W>
-KernelFn mfma_by_depth(int depth, int hint) {
-  switch (depth) {
-    case 2: return mfma_fn<L, NT, W, 2>(hint);
-    case 4: return mfma_fn<L, NT, W, 4>(hint);
-    case 8: return mfma_fn<L, NT, W, 8>(hint);
-    default: return nullptr;
+template <int L, int NT>
+KernelFn mfma_by_shape(int wn, int wk, int depth, int hint) {
+#define QF_WNWK(A, B) \
+  if (wn == A && wk == B) return mfma_fn<L, NT, A, B>(depth, hint);
+  QF_WNWK(4, 1) QF_WNWK(8, 1) QF_WNWK(2, 2) QF_WNWK(4, 2) QF_WNWK(8, 2)
+  QF_WNWK(1, 4) QF_WNWK(2, 4) QF_WNWK(4, 4) QF_WNWK(1, 8) QF_WNWK(2, 8)
+#undef QF_WNWK
+  return nullptr;
+}
+
+KernelFn select_mfma(int layout, int nt, int waves, int k_waves, int depth, int hint) {
+  if (k_waves < 1 || waves % k_waves) return nullptr;
+  const int wn = waves / k_waves;
+  if (layout == QF_LAYOUT_ROWMAJOR) {
+    if (nt == 1) return mfma_by_shape<QF_LAYOUT_ROWMAJOR, 1>(wn, k_waves, depth, hint);
+    if (nt == 2) return mfma_by_shape<QF_LAYOUT_ROWMAJOR, 2>(wn, k_waves, depth, hint);
+  } else {
+    if (nt == 1) return mfma_by_shape<QF_LAYOUT_TILED, 1>(wn, k_waves, depth, hint);
+    if (nt == 2) return mfma_by_shape<QF_LAYOUT_TILED, 2>(wn, k_waves, depth, hint);
   }
-}
-
-template <int L, int W>
-KernelFn mfma_by_nt(int nt, int depth, int hint) {
-  switch (nt) {
-    case 1: return mfma_by_depth<L, 1, W>(depth, hint);
-    case 2: return mfma_by_depth<L, 2, W>(depth, hint);
-    case 4: return mfma_by_depth<L, 4, W>(depth, hint);
-    default: return nullptr;
-  }
-}
-
-KernelFn select_mfma(int layout, int nt, int waves, int depth, int hint) {
-  if (waves != 4) return nullptr;
-  return layout == QF_LAYOUT_ROWMAJOR ? mfma_by_nt<QF_LAYOUT_ROWMAJOR, 4>(nt, depth, hint)
-                                      : mfma_by_nt<QF_LAYOUT_TILED, 4>(nt, depth, hint);
+  return nullptr;
 }
 
 template <int MM, int RPW>
@@ -602,36 +767,87 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 inline int round_up16(int n) { return (n + 15) / 16 * 16; }
 
-// LDS bytes one workgroup stages for split_k splits of ksteps (the largest split).
-size_t lds_bytes(int kernel, int M, int ksteps, int split_k) {
-  const size_t klen = (size_t)ceil_div(ksteps, split_k) * kStepK;
-  // the MFMA kernel stages one extra step of zeros after the activations
-  return (size_t)M * (klen + (kernel == QF_KERNEL_MFMA ? kStepK : 0)) * 2;
+// LDS bytes of one workgroup: the largest split's x slice, or, for MFMA with k_waves > 1, the
+// slice-reduction buffer if that is larger.
+size_t lds_bytes(const qf_w8a16_config& c, int M, int ksteps) {
+  const int steps = ceil_div(ksteps, c.split_k);
+  if (c.kernel == QF_KERNEL_GEMV) return (size_t)M * steps * kStepK * 2;
+  const size_t xs = (size_t)M * x_pitch(steps);
+  const size_t red = c.k_waves > 1 ? (size_t)c.waves * c.tiles_per_wave * kWave * sizeof(f32x4_t) : 0;
+  return xs > red ? xs : red;
 }
 
 int workgroups(const qf_w8a16_config& c, int N) {
   if (c.kernel == QF_KERNEL_GEMV) return ceil_div(N, c.waves * c.tiles_per_wave);
-  return ceil_div(round_up16(N) / kTileN, c.waves * c.tiles_per_wave);
+  const int wn = c.waves / c.k_waves;
+  return ceil_div(round_up16(N) / kTileN, wn * c.tiles_per_wave);
 }
 
-// Automatic configuration (host only).  Returns false when unsupported.
+// Workspace: a fixed prefix of arrival counters (the same bytes for every call, so counters never
+// land on memory an earlier call used for partial sums), then the split partials.
+size_t workspace_for(const qf_w8a16_config& c, int M, int N) {
+  if (c.split_k <= 1) return 0;
+  return QF_W8A16_COUNTER_BYTES + (size_t)c.split_k * (size_t)M * (size_t)round_up16(N) * sizeof(float);
+}
+
+// Checks a complete configuration against the instantiated kernels and the LDS budget.
+int validate_config(int M, int N, int K, int layout, const qf_w8a16_config& c) {
+  const int ksteps = K / kStepK;
+  if (c.kernel != QF_KERNEL_GEMV && c.kernel != QF_KERNEL_MFMA) return QF_ERR_INVALID_ARG;
+  if (c.split_k < 1 || c.split_k > ksteps || c.waves < 1 || c.k_waves < 1 || c.tiles_per_wave < 1)
+    return QF_ERR_INVALID_ARG;
+  if (c.kernel == QF_KERNEL_GEMV && (M > 4 || layout != QF_LAYOUT_ROWMAJOR || c.k_waves != 1))
+    return QF_ERR_UNSUPPORTED;
+  if (ksteps / c.split_k < c.k_waves) return QF_ERR_UNSUPPORTED;  // every k-slice needs a step
+  if (c.kernel == QF_KERNEL_MFMA && c.split_k > 1 && c.reduce == 0 &&
+      (size_t)workgroups(c, N) * 4 > QF_W8A16_COUNTER_BYTES)
+    return QF_ERR_UNSUPPORTED;  // one arrival counter per workgroup column
+  if (lds_bytes(c, M, ksteps) > kMaxLds) return QF_ERR_UNSUPPORTED;
+  if (c.kernel == QF_KERNEL_MFMA &&
+      select_mfma(layout, c.tiles_per_wave, c.waves, c.k_waves, c.depth, c.load_hint) == nullptr)
+    return QF_ERR_UNSUPPORTED;
+  if (c.kernel == QF_KERNEL_GEMV && select_gemv(M, c.tiles_per_wave, c.waves, c.load_hint) == nullptr)
+    return QF_ERR_UNSUPPORTED;
+  return QF_OK;
+}
+
+// Automatic configuration (host only).  Returns false when unsupported.  Chosen from measured
+// sweeps at M = 5 on MI355X (TILED layout): one 16-row tile per wavefront, 8 wavefronts per
+// workgroup, a 4-step weight prefetch ring; the K range is split inside the workgroup (k_waves,
+// reduced through LDS) so that a wavefront streams ~20-40 KiB, and across workgroups only when
+// K > 128 k-steps or the staged activation slice would not fit in LDS; such splits are reduced by
+// the second-pass kernel, which measured faster than the last-arrival reduction.
 bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
   if (M < 1 || M > QF_W8A16_MAX_M || N < 1 || K < QF_W8A16_K_ALIGN || K % QF_W8A16_K_ALIGN) return false;
   if (layout != QF_LAYOUT_ROWMAJOR && layout != QF_LAYOUT_TILED) return false;
   *c = qf_w8a16_config{};
   c->kernel = QF_KERNEL_MFMA;
-  c->tiles_per_wave = 2;
-  c->waves = 4;
+  c->tiles_per_wave = 1;
   c->depth = 4;
-  c->load_hint = 0;
+  c->load_hint = layout == QF_LAYOUT_TILED ? 1 : 0;
+  c->waves = 8;
+  c->reduce = 1;
   const int ksteps = K / kStepK;
-  const int wgs = workgroups(*c, N);
-  // Aim for >= 2 workgroups per CU (256 CUs) while keeping >= 8 k-steps per split.
-  int sk = 1;
-  while (wgs * sk < 512 && ksteps / (sk * 2) >= 8) sk *= 2;
-  while (lds_bytes(c->kernel, M, ksteps, sk) > kMaxLds && sk < ksteps) ++sk;
-  c->split_k = sk;
-  return true;
+  if (layout == QF_LAYOUT_ROWMAJOR && M <= 2) {
+    // Row-major weights at M <= 2: the GEMV kernel's contiguous 1 KiB row reads win over the
+    // MFMA tiles' 64-byte row pieces (gate_up, M = 1: 30.5 us against 46 us).
+    c->kernel = QF_KERNEL_GEMV;
+    c->waves = 4;
+    c->k_waves = 1;
+    c->tiles_per_wave = 4;
+    c->load_hint = 1;
+    c->split_k = 1;
+    while (lds_bytes(*c, M, ksteps) > kMaxLds && c->split_k < ksteps) ++c->split_k;
+    return validate_config(M, N, K, layout, *c) == QF_OK;
+  }
+  c->split_k = ceil_div(ksteps, 128);
+  for (;;) {
+    const int per_split = ksteps / c->split_k;
+    c->k_waves = per_split >= 64 ? 4 : (per_split >= 16 ? 2 : 1);
+    if (lds_bytes(*c, M, ksteps) <= kMaxLds || c->split_k >= ksteps) break;
+    ++c->split_k;
+  }
+  return validate_config(M, N, K, layout, *c) == QF_OK;
 }
 
 // Validate / complete a caller configuration.
@@ -639,32 +855,32 @@ int resolve_config(int M, int N, int K, int layout, const qf_w8a16_config* in, q
   if (!auto_config(M, N, K, layout, out)) return QF_ERR_UNSUPPORTED;
   if (in == nullptr || in->kernel == QF_KERNEL_AUTO) return QF_OK;
   qf_w8a16_config c = *in;
-  if (c.kernel != QF_KERNEL_GEMV && c.kernel != QF_KERNEL_MFMA) return QF_ERR_INVALID_ARG;
-  if (c.kernel == QF_KERNEL_GEMV && (M > 4 || layout != QF_LAYOUT_ROWMAJOR)) return QF_ERR_UNSUPPORTED;
   if (c.waves == 0) c.waves = 4;
-  if (c.tiles_per_wave == 0) c.tiles_per_wave = (c.kernel == QF_KERNEL_GEMV) ? 4 : 2;
-  if (c.depth == 0) c.depth = 4;
-  if (c.split_k == 0) {
-    c.split_k = out->split_k;
-  }
-  const int ksteps = K / kStepK;
-  if (c.split_k < 1 || c.split_k > ksteps) return QF_ERR_INVALID_ARG;
-  if (lds_bytes(c.kernel, M, ksteps, c.split_k) > kMaxLds) return QF_ERR_UNSUPPORTED;
-  if (c.kernel == QF_KERNEL_MFMA && select_mfma(layout, c.tiles_per_wave, c.waves, c.depth, c.load_hint) == nullptr)
-    return QF_ERR_UNSUPPORTED;
-  if (c.kernel == QF_KERNEL_GEMV && select_gemv(M, c.tiles_per_wave, c.waves, c.load_hint) == nullptr)
-    return QF_ERR_UNSUPPORTED;
+  if (c.k_waves == 0) c.k_waves = 1;
+  if (c.tiles_per_wave == 0) c.tiles_per_wave = (c.kernel == QF_KERNEL_GEMV) ? 4 : 1;
+  if (c.depth == 0) c.depth = 8;
+  if (c.split_k == 0) c.split_k = out->split_k;
+  const int rc = validate_config(M, N, K, layout, c);
+  if (rc != QF_OK) return rc;
   *out = c;
   return QF_OK;
 }
 
-size_t workspace_for(const qf_w8a16_config& c, int M, int N) {
-  if (c.split_k <= 1) return 0;
-  return (size_t)c.split_k * (size_t)M * (size_t)round_up16(N) * sizeof(float);
-}
+// Kernels that were allowed more than the default dynamic LDS (hipFuncSetAttribute is per kernel).
+std::mutex g_lds_mutex;
+std::unordered_set<const void*> g_lds_raised;
 
 int launch(KernelFn fn, dim3 grid, dim3 block, size_t smem, hipStream_t stream, const GemmArgs& a) {
   void* args[] = {const_cast<GemmArgs*>(&a)};
+  if (smem > kDefaultLds) {
+    std::lock_guard<std::mutex> lock(g_lds_mutex);
+    const void* key = reinterpret_cast<const void*>(fn);
+    if (g_lds_raised.find(key) == g_lds_raised.end()) {
+      if (hipFuncSetAttribute(key, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds) != hipSuccess)
+        return QF_ERR_HIP;
+      g_lds_raised.insert(key);
+    }
+  }
   if (hipLaunchKernel(reinterpret_cast<const void*>(fn), grid, block, args, smem, stream) != hipSuccess)
     return QF_ERR_HIP;
   return QF_OK;
@@ -728,7 +944,9 @@ int qf_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, 
   a.w = w;
   a.scale = scale;
   a.y = y;
-  a.partial = reinterpret_cast<float*>(workspace);
+  a.counters = reinterpret_cast<unsigned*>(workspace);
+  a.partial = need > 0 ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + QF_W8A16_COUNTER_BYTES)
+                       : nullptr;
   a.ldx = ldx;
   a.ldw = ldw;
   a.ldy = ldy;
@@ -740,17 +958,19 @@ int qf_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, 
   a.split_k = c.split_k;
   a.out_f32 = out_dtype == QF_DTYPE_F32;
   a.vec_out = (ldy % 4) == 0;
+  a.fused_reduce = c.kernel == QF_KERNEL_MFMA && c.reduce == 0;
 
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(workgroups(c, N), c.split_k);
   const dim3 block(c.waves * kWave);
-  const size_t smem = lds_bytes(c.kernel, M, a.ksteps, c.split_k);
-  KernelFn fn = (c.kernel == QF_KERNEL_GEMV) ? select_gemv(M, c.tiles_per_wave, c.waves, c.load_hint)
-                                              : select_mfma(layout, c.tiles_per_wave, c.waves, c.depth, c.load_hint);
+  const size_t smem = lds_bytes(c, M, a.ksteps);
+  KernelFn fn = (c.kernel == QF_KERNEL_GEMV)
+                    ? select_gemv(M, c.tiles_per_wave, c.waves, c.load_hint)
+                    : select_mfma(layout, c.tiles_per_wave, c.waves, c.k_waves, c.depth, c.load_hint);
   if (fn == nullptr) return QF_ERR_UNSUPPORTED;
   int st = launch(fn, grid, block, smem, s, a);
   if (st != QF_OK) return st;
-  if (c.split_k > 1) {
+  if (c.split_k > 1 && (c.kernel == QF_KERNEL_GEMV || !a.fused_reduce)) {
     const int threads = M * (a.n_pad / 4);
     st = launch(&splitk_reduce_kernel, dim3(ceil_div(threads, 256)), dim3(256), 0, s, a);
   }
@@ -783,6 +1003,13 @@ int qf_quantize_rows_int8(const uint16_t* w, int64_t ldw, int8_t* q, float* s, i
   if (w == nullptr || q == nullptr || s == nullptr || V < 1 || H < 1 || ldw < H) return QF_ERR_INVALID_ARG;
   hipLaunchKernelGGL(quantize_rows_kernel, dim3(V), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), w, ldw,
                      q, s, H);
+  return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
+}
+
+int qf_read_probe(const void* buf, size_t bytes, uint32_t* sink, int blocks, void* stream) {
+  if (buf == nullptr || sink == nullptr || blocks < 1 || bytes % 16 || !aligned16(buf)) return QF_ERR_INVALID_ARG;
+  hipLaunchKernelGGL(read_probe_kernel, dim3(blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     reinterpret_cast<const u32x4_t*>(buf), (int64_t)(bytes / 16), sink);
   return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
 }
 

@@ -43,6 +43,7 @@ EXPORTS = (
     "qf_w8a16_unpack",
     "qf_quantize_rows_int8",
     "qf_argmax_rows_bf16",
+    "qf_read_probe",
 )
 
 
@@ -56,10 +57,11 @@ class Config(ctypes.Structure):
         ("waves", ctypes.c_int32),
         ("depth", ctypes.c_int32),
         ("load_hint", ctypes.c_int32),
-        ("reserved", ctypes.c_int32 * 2),
+        ("k_waves", ctypes.c_int32),
+        ("reduce", ctypes.c_int32),
     ]
 
-    FIELDS = ("kernel", "split_k", "tiles_per_wave", "waves", "depth", "load_hint")
+    FIELDS = ("kernel", "split_k", "tiles_per_wave", "waves", "depth", "load_hint", "k_waves", "reduce")
 
     @classmethod
     def from_seq(cls, seq) -> "Config":
@@ -115,6 +117,8 @@ def load() -> ctypes.CDLL:
     L.qf_quantize_rows_int8.restype = i32
     L.qf_argmax_rows_bf16.argtypes = [p, i64, i32, i32, i32, i64, p, p]
     L.qf_argmax_rows_bf16.restype = i32
+    L.qf_read_probe.argtypes = [p, sz, p, i32, p]
+    L.qf_read_probe.restype = i32
     v = L.qf_abi_version()
     if v != ABI_VERSION:
         raise ImportError(f"{LIB_PATH}: ABI version {v}, expected {ABI_VERSION}")

@@ -28,7 +28,9 @@ TILED = L.LAYOUT_TILED
 
 class W8A16Config(NamedTuple):
     """Launch configuration; zero fields are chosen by the library for the call's M (see
-    qf_w8a16_pick_config).  kernel: 0 auto, 1 gemv (M <= 4), 2 mfma."""
+    qf_w8a16_pick_config).  kernel: 0 auto, 1 gemv (M <= 4), 2 mfma.  waves = wavefronts per
+    workgroup, of which k_waves split K inside the workgroup (MFMA); reduce (MFMA, split_k > 1):
+    0 = the last workgroup of each n-block sums the splits, 1 = a second kernel does."""
 
     kernel: int = 0
     split_k: int = 0
@@ -36,6 +38,8 @@ class W8A16Config(NamedTuple):
     waves: int = 0
     depth: int = 0
     load_hint: int = 0
+    k_waves: int = 0
+    reduce: int = 0
 
 
 AUTO = W8A16Config()
@@ -87,6 +91,33 @@ def _weight_geometry(w: torch.Tensor, N: int, K: int, layout: int) -> int:
     raise ValueError(f"unknown layout {layout}")
 
 
+# Split-K workspace, one per device: allocated zeroed outside graph capture and reused.  The
+# library's arrival counters at the front of it are zero before every call and are returned to zero
+# by it, so every call issued in order on the device -- eager, or replayed from a graph, whichever
+# stream captured it -- can share the buffer; the partial sums behind the counters need no
+# clearing.  Two split-K calls running at the same time on different streams of one device would
+# share it too, which is not supported.
+_workspaces: dict[int, torch.Tensor] = {}
+_retired: list[torch.Tensor] = []  # superseded workspaces stay allocated: captured graphs may hold them
+_WS_MIN = 8 << 20
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                f"W8A16 split-K workspace of {nbytes} bytes is not allocated on this device; run the op "
+                "once outside graph capture (a warm-up) before capturing it")
+        size = max(nbytes, _WS_MIN, 0 if ws is None else 2 * ws.numel())
+        if ws is not None:
+            _retired.append(ws)
+        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
 def _launch(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, layout: int, out_dtype: torch.dtype,
             config) -> torch.Tensor:
     lib = L.load()
@@ -115,10 +146,11 @@ def _launch(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, layout: int
     y = torch.empty((M, N), dtype=out_dtype, device=x.device)
     c = _config_struct(config)
     ws_bytes = int(lib.qf_w8a16_workspace_bytes(M, N, K, layout, ctypes.byref(c)))
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
     stream = torch.cuda.current_stream(x.device).cuda_stream
+    ws = _workspace(x.device, ws_bytes) if ws_bytes else None
     rc = lib.qf_w8a16_gemm(x.data_ptr(), ldx, w.data_ptr(), ldw, layout, s.data_ptr(), y.data_ptr(), N, dt,
-                           M, N, K, ctypes.byref(c), ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+                           M, N, K, ctypes.byref(c), ws.data_ptr() if ws is not None else None,
+                           ws.numel() if ws is not None else 0, stream)
     L.check(rc, f"qf_w8a16_gemm(M={M}, N={N}, K={K}, layout={layout})")
     return y
 

@@ -52,18 +52,38 @@ def test_pick_config_supported_and_lds_bounded(M):
         assert c.kernel in (L.KERNEL_GEMV, L.KERNEL_MFMA)
         ksteps = K // 64
         assert 1 <= c.split_k <= ksteps
-        klen = -(-ksteps // c.split_k) * 64
-        assert M * (klen + 64) * 2 <= 65536
+        steps = -(-ksteps // c.split_k)
+        pitch = steps * 128 + 32
+        assert max(M * pitch, c.waves * c.tiles_per_wave * 1024 * (c.k_waves > 1)) <= 160 * 1024 - 256
         ws = L.workspace_bytes(M, N, K, 0, None)
         n_pad = (N + 15) // 16 * 16
-        assert ws == (0 if c.split_k == 1 else c.split_k * M * n_pad * 4)
+        assert ws == (0 if c.split_k == 1 else 65536 + c.split_k * M * n_pad * 4)
+        assert ksteps // c.split_k >= c.k_waves
+
+
+def test_pick_config_covers_every_supported_shape():
+    """The automatic configuration is valid (instantiated kernel, LDS budget, k-slices) for every
+    M <= 16 and a wide range of N and K multiples of 64."""
+    Ks = [64 * k for k in (1, 2, 3, 5, 7, 8, 13, 20, 31, 64, 80, 96, 128, 200, 272, 300, 512)]
+    Ns = [1, 15, 16, 17, 100, 1000, 5120, 10240, 34816, 151936, 248320, 1 << 20]
+    for M in range(1, 17):
+        for K in Ks:
+            for N in Ns:
+                for layout in (0, 1):
+                    c = L.pick_config(M, N, K, layout)
+                    assert c is not None, (M, N, K, layout)
+                    assert c.k_waves in (1, 2, 4) and c.waves % c.k_waves == 0
 
 
 def test_workspace_for_explicit_config():
-    c = L.Config.from_seq((2, 4, 2, 4, 4, 0))
-    assert L.workspace_bytes(5, 1000, 1024, 0, c) == 4 * 5 * 1008 * 4
-    c1 = L.Config.from_seq((2, 1, 2, 4, 4, 0))
+    c = L.Config.from_seq((2, 4, 2, 4, 4, 0, 1))      # 63 tiles / (4 x 2) -> 8 workgroups
+    assert L.workspace_bytes(5, 1000, 1024, 0, c) == 65536 + 4 * 5 * 1008 * 4
+    c1 = L.Config.from_seq((2, 1, 2, 4, 4, 0, 1))
     assert L.workspace_bytes(5, 1000, 1024, 0, c1) == 0
+    c2 = L.Config.from_seq((2, 2, 1, 16, 8, 1, 4))    # 4 tile groups x 4 k-slices
+    assert L.workspace_bytes(5, 1000, 1024, 0, c2) == 65536 + 2 * 5 * 1008 * 4
+    bad = L.Config.from_seq((2, 8, 1, 16, 8, 1, 4))   # 16 steps / 8 splits < 4 k-slices
+    assert L.workspace_bytes(5, 1000, 1024, 0, bad) == 0
 
 
 def _gemm(x=16, ldx=64, w=16, ldw=64, layout=0, s=16, y=16, ldy=64, dt=0, M=5, N=64, K=64, cfg=None,
@@ -84,13 +104,15 @@ def test_gemm_argument_validation_host_only():
     assert _gemm(x=fake, w=fake, s=fake, y=fake, K=96, ldx=96, ldw=96) == L.ERR_UNSUPPORTED  # K % 64
     assert _gemm(x=fake + 2, w=fake, s=fake, y=fake) == L.ERR_UNSUPPORTED           # misaligned x
     assert _gemm(x=fake, w=fake, s=fake, y=fake, ldx=68) == L.ERR_UNSUPPORTED       # ldx % 8
-    gemv_big_m = L.Config.from_seq((L.KERNEL_GEMV, 1, 4, 4, 4, 0))
+    gemv_big_m = L.Config.from_seq((L.KERNEL_GEMV, 1, 4, 4, 4, 0, 1))
     assert _gemm(x=fake, w=fake, s=fake, y=fake, cfg=gemv_big_m) == L.ERR_UNSUPPORTED  # gemv needs M <= 4
-    bad_tiles = L.Config.from_seq((L.KERNEL_MFMA, 1, 3, 4, 4, 0))
+    bad_tiles = L.Config.from_seq((L.KERNEL_MFMA, 1, 3, 4, 4, 0, 1))
     assert _gemm(x=fake, w=fake, s=fake, y=fake, cfg=bad_tiles) == L.ERR_UNSUPPORTED
-    split = L.Config.from_seq((L.KERNEL_MFMA, 4, 2, 4, 4, 0))
+    split = L.Config.from_seq((L.KERNEL_MFMA, 4, 2, 4, 4, 0, 1))
     assert _gemm(x=fake, w=fake, s=fake, y=fake, K=1024, ldx=1024, ldw=1024, cfg=split) == L.ERR_WORKSPACE
-    too_many = L.Config.from_seq((L.KERNEL_MFMA, 99, 2, 4, 4, 0))
+    too_many = L.Config.from_seq((L.KERNEL_MFMA, 99, 2, 4, 4, 0, 1))
+    bad_shape = L.Config.from_seq((L.KERNEL_MFMA, 1, 1, 6, 4, 0, 4))   # 6 waves not divisible by 4
+    assert _gemm(x=fake, w=fake, s=fake, y=fake, cfg=bad_shape) == L.ERR_UNSUPPORTED
     assert _gemm(x=fake, w=fake, s=fake, y=fake, cfg=too_many) == L.ERR_INVALID_ARG
 
 

@@ -47,24 +47,59 @@ def test_small_shapes_every_m(oracle, M):
         check(oracle, inp, bf16_bits(run(x, w, s)), label=f"auto M={M} N={N} K={K}")
 
 
-MFMA_CFGS = [(nt, d, h) for nt in (1, 2, 4) for d in (2, 4, 8) for h in (0, 1)]
+WNWK = [(4, 1), (8, 1), (2, 2), (4, 2), (8, 2), (1, 4), (2, 4), (4, 4), (1, 8), (2, 8)]
+MFMA_CFGS = [(nt, wn, wk, d, h) for nt in (1, 2) for (wn, wk) in WNWK for d in (4, 8) for h in (0, 1)]
 
 
-@pytest.mark.parametrize("nt,depth,hint", MFMA_CFGS)
-def test_mfma_configs(oracle, nt, depth, hint):
+@pytest.mark.parametrize("nt,wn,wk,depth,hint", MFMA_CFGS)
+def test_mfma_configs(oracle, nt, wn, wk, depth, hint):
     M, N, K = 5, 1040, 5120
-    inp = oracle.gen_inputs(M, N, K, seed=nt * 100 + depth * 10 + hint)
+    inp = oracle.gen_inputs(M, N, K, seed=nt * 1000 + wn * 100 + wk * 10 + depth + hint)
     x, w, s = dev_inputs(inp, DEV)
     wt = qf.to_tiled(w)
     outs = {}
     for sk in (1, 3, 8):
-        cfg = qf.W8A16Config(L.KERNEL_MFMA, sk, nt, 4, depth, hint)
+        cfg = qf.W8A16Config(L.KERNEL_MFMA, sk, nt, wn * wk, depth, hint, wk)
         for layout, ww in ((qf.ROWMAJOR, w), (qf.TILED, wt)):
             y = bf16_bits(run(x, ww, s, cfg, layout))
             outs[(sk, layout)] = y
         # the two layouts hold the same values in the same per-lane order: identical results
         assert np.array_equal(outs[(sk, qf.ROWMAJOR)], outs[(sk, qf.TILED)])
-        check(oracle, inp, outs[(sk, qf.ROWMAJOR)], label=f"mfma nt={nt} d={depth} h={hint} sk={sk}")
+        check(oracle, inp, outs[(sk, qf.ROWMAJOR)], label=f"mfma nt={nt} wn={wn} wk={wk} d={depth} h={hint} sk={sk}")
+
+
+def test_fused_split_k_counters_return_to_zero(oracle):
+    """Every split-K call leaves the arrival counters at the front of the workspace at zero, so the
+    persistent workspace serves the next call: repeated calls give identical, correct results."""
+    from qwen_fastpath import w8a16 as W
+    M, N, K = 5, 5120, 8192
+    inp = oracle.gen_inputs(M, N, K, seed=77)
+    x, w, s = dev_inputs(inp, DEV)
+    ys = []
+    for sk, wk in ((2, 4), (4, 4), (7, 2), (16, 1), (3, 8)):
+        cfg = qf.W8A16Config(L.KERNEL_MFMA, sk, 1, 16 if wk > 1 else 4, 8, 1, wk)
+        for _ in range(3):
+            ys.append(bf16_bits(run(x, w, s, cfg)))
+            ws = W._workspaces[0]
+            assert int(ws[:65536].view(torch.int32).abs().sum()) == 0
+        assert np.array_equal(ys[-1], ys[-2]) and np.array_equal(ys[-1], ys[-3])
+        check(oracle, inp, ys[-1], label=f"fused split-K sk={sk} wk={wk}")
+        # the second-pass kernel sums the same partials in the same order: identical bits
+        cfg2 = cfg._replace(reduce=1)
+        assert np.array_equal(bf16_bits(run(x, w, s, cfg2)), ys[-1])
+
+
+@pytest.mark.parametrize("name", ["o_proj", "qkv"])
+def test_large_lds_without_split(oracle, name):
+    """x slices above 64 KiB of LDS (gfx950 allows 160 KiB per workgroup), no K split."""
+    N, K = LAYER[name]
+    inp = oracle.gen_inputs(5, N, K, seed=3)
+    x, w, s = dev_inputs(inp, DEV)
+    wt = qf.to_tiled(w)
+    for (wn, wk) in ((2, 8), (1, 8), (4, 4)):
+        cfg = qf.W8A16Config(L.KERNEL_MFMA, 1, 1, wn * wk, 8, 1, wk, 0)
+        y = bf16_bits(run(x, wt, s, cfg, qf.TILED))
+        check(oracle, inp, y, label=f"{name} lds>64K wn={wn} wk={wk}")
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4])
@@ -75,9 +110,9 @@ def test_gemv_configs(oracle, M):
         for rpw in (2, 4):
             for hint in (0, 1):
                 for sk in (1, 2, 5):
-                    if sk > K // 64:
-                        continue
-                    cfg = qf.W8A16Config(L.KERNEL_GEMV, sk, rpw, 4, 0, hint)
+                    if sk > K // 64 or M * -(-(K // 64) // sk) * 64 * 2 > 160 * 1024 - 256:
+                        continue  # more k-steps than splits, or the x slice exceeds the LDS budget
+                    cfg = qf.W8A16Config(L.KERNEL_GEMV, sk, rpw, 4, 0, hint, 1)
                     check(oracle, inp, bf16_bits(run(x, w, s, cfg)),
                           label=f"gemv M={M} N={N} K={K} rpw={rpw} h={hint} sk={sk}")
 
@@ -106,7 +141,7 @@ def test_gate_up_m_sweep(oracle, M):
     x, w, s = dev_inputs(inp, DEV)
     check(oracle, inp, bf16_bits(run(x, w, s)), label=f"gate_up M={M}")
     if M <= 4:
-        cfg = qf.W8A16Config(L.KERNEL_GEMV, 1, 4, 4, 0, 0)
+        cfg = qf.W8A16Config(L.KERNEL_GEMV, 1, 4, 4, 0, 0, 1)
         check(oracle, inp, bf16_bits(run(x, w, s, cfg)), label=f"gate_up gemv M={M}")
 
 
@@ -114,7 +149,7 @@ def test_determinism_and_row_independence(oracle):
     N, K = 5120, 17408
     inp = oracle.gen_inputs(16, N, K, seed=21)
     x, w, s = dev_inputs(inp, DEV)
-    cfg = qf.W8A16Config(L.KERNEL_MFMA, 16, 2, 4, 4, 0)
+    cfg = qf.W8A16Config(L.KERNEL_MFMA, 16, 2, 8, 4, 0, 2)
     ys = [bf16_bits(run(x, w, s, cfg)) for _ in range(3)]
     assert all(np.array_equal(ys[0], y) for y in ys[1:])
     for M in (1, 5, 9):
@@ -132,7 +167,7 @@ def test_one_hot_closed_form(oracle):
     x = to_dev_bf16(xb, DEV)
     w = torch.from_numpy(inp.w).to(DEV)
     s = torch.from_numpy(inp.s).to(DEV)
-    for cfg in (None, qf.W8A16Config(L.KERNEL_MFMA, 4, 1, 4, 2, 1)):
+    for cfg in (None, qf.W8A16Config(L.KERNEL_MFMA, 4, 1, 8, 4, 1, 2)):
         y = bf16_bits(run(x, w.t(), s, cfg))
         want = oracle.bf16_from_f64(inp.w[:, ks].T.astype(np.float64) * inp.s.astype(np.float64))
         assert np.array_equal(y, want)
