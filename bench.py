@@ -3,9 +3,10 @@
 Default workload (one "step"): the four per-layer GEMMs of a dense GQA 27B-class transformer at M = 5
 tokens (1 verified + 4 draft): qkv K=5120 N=10240, o_proj K=8192 N=5120, gate_up K=5120 N=34816,
 down K=17408 N=5120; int8 [N, K] weights with fp32 per-channel scales |N(0,1)|*0.002+1e-4, bf16
-N(0,1) activations, synthetic and seeded.  Each step runs one layer's GEMMs from a hipGraph; the
-weights rotate over several distinct layers (more bytes than the 256 MB MALL), so every step streams
-its weights from HBM.  Output: one JSON line on stdout.
+N(0,1) activations, synthetic and seeded.  Each step runs one layer's GEMMs; the weights rotate over
+several distinct layers (more bytes than the 256 MB MALL), so every step streams
+its weights from HBM.  Steps are captured 32 to a graph, as a decode forward pass is.  Output: one JSON
+line on stdout.
 
   value        algorithmic bytes of all timed steps / wall time of the timed steps (GB/s)
   roofline     the dominant kernel (gate_up): algorithmic bytes per launch / its mean duration from
@@ -42,6 +43,7 @@ GEMMS = {  # name: (N, K)
     "down": (5120, 17408),
 }
 DOMINANT = "gate_up"
+GRAPH_STEPS = 32  # decode steps captured per graph (a multiple of the rotated layer count)
 PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "w8a16_gate_up_m5_pmc.txt")
 
 
@@ -205,17 +207,30 @@ def main():
     layers = [Layer(torch, qf, dev, 1000 + i, M, layout) for i in range(R)]
     bytes_per_step = sum(algo_bytes(M, N, K) for (N, K) in GEMMS.values())
 
-    def step_fn(L_):
-        return lambda: [L_.gemm(qf, torch, n) for n in GEMMS]
+    # Steps are captured GRAPH_STEPS at a time (step i runs layer i % R), as a decode forward pass
+    # captures all of its layers in one graph; K steps = K // GRAPH_STEPS replays of that graph plus
+    # one graph holding the remaining K % GRAPH_STEPS steps.
+    def steps_fn(first, count):
+        return lambda: [layers[(first + i) % R].gemm(qf, torch, n) for i in range(count) for n in GEMMS]
 
-    graphs = [capture(torch, step_fn(L_))[0] for L_ in layers]
+    gsteps = GRAPH_STEPS - GRAPH_STEPS % R if GRAPH_STEPS >= R else R
+    block = capture(torch, steps_fn(0, gsteps))[0]
 
-    for i in range(args.warmup):
-        graphs[i % R].replay()
+    def run_steps(k):
+        for _ in range(k // gsteps):
+            block.replay()
+        return k % gsteps
+
+    rest_w = run_steps(args.warmup)
+    torch.cuda.synchronize()
+    tail = capture(torch, steps_fn(0, args.steps % gsteps))[0] if args.steps % gsteps else None
+    if rest_w:
+        capture(torch, steps_fn(0, rest_w))[0].replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        graphs[i % R].replay()
+    run_steps(args.steps)
+    if tail is not None:
+        tail.replay()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     value = args.steps * bytes_per_step / elapsed / 1e9
@@ -282,7 +297,7 @@ def main():
         "config": {"workload": "dense GQA 27B-class layer GEMMs at M=5: qkv 10240x5120, o_proj 5120x8192, "
                                "gate_up 34816x5120, down 5120x17408 (N x K int8)",
                    "M": M, "layers_rotated": R, "bytes_per_step": bytes_per_step, "weight_layout": args.layout,
-                   "timing": "one hipGraph per layer, replayed; weights rotate over distinct layers"},
+                   "timing": f"hipGraphs of {GRAPH_STEPS} steps replayed; step i runs layer i % {R}"},
         "us_per_layer": round(ms_per_step * 1e3, 2),
         "pct_of_peak": round(100 * value / PEAK_GBS, 2),
         "per_gemm": per_gemm,

@@ -85,7 +85,7 @@ int qf_abi_version(void);
 const char* qf_status_string(int status);
 
 /* Fill *cfg with the configuration used for (M, N, K, layout).  Returns QF_ERR_UNSUPPORTED when the
- * shape is not served (M outside 1..16, K % 64 != 0, TILED with N % 16 != 0), mirroring
+ * shape is not served (M outside 1..16, N < 1, K % 64 != 0, unknown layout), mirroring
  * pick_config() returning None.  Host-only; touches no device. */
 int qf_w8a16_pick_config(int M, int N, int K, int layout, qf_w8a16_config* cfg);
 
