@@ -7,7 +7,7 @@
  * (the W8A8 checkpoint layout; the [K, N] column-major view vLLM keeps for CUTLASS is the same
  * memory), scale is fp32 per output channel [N], y is bf16 (or fp32) [M, N] with row stride ldy.
  * Accumulation is fp32; the scale is applied after the K reduction; split-K partial sums are
- * reduced in a fixed order by a second pass, so results are bitwise reproducible run to run.
+ * reduced in a fixed (split) order, so results are bitwise reproducible run to run.
  *
  * The ABI uses only plain pointers and sizes.  `stream` is a hipStream_t (NULL = the null stream).
  * No entry point allocates, frees, synchronises or retains a pointer after it returns, so every

@@ -7,7 +7,8 @@
 // accumulated in fp32, the per-channel scale is applied once after the K reduction, and the result
 // is rounded to bf16 with round-to-nearest-even.  Where the reference reduces split-K partials with
 // fp32 atomics (w8a16.py:43-44, order-dependent), this file writes the partials to a workspace and
-// sums them in split order in a second kernel, so every result is bitwise reproducible.
+// sums them in split order -- in the last workgroup of each n-block to finish, or in a second
+// kernel -- so every result is bitwise reproducible.
 //
 // Two kernels compute the product:
 //   * mfma: v_mfma_f32_16x16x32_bf16 over 1 KiB weight fragments (16 output channels x 64 k).  The
@@ -152,6 +153,9 @@ __device__ __forceinline__ f32x4_t load_scale4(const float* scale, int N, int n)
   }
   return s;
 }
+
+// s_waitcnt immediate (gfx9 encoding) that waits for vmcnt == 0 and leaves expcnt / lgkmcnt free.
+constexpr int kWaitVmcnt0 = 0x0F70;
 
 // LDS row pitch (bytes) of a staged x slice of `steps` k-steps: the row bytes plus 32, so the rows
 // that the 16 lanes of an MFMA fragment read start in distinct 32-byte bank groups.
@@ -379,24 +383,27 @@ __global__ void __launch_bounds__(WN * WK * kWave) w8a16_mfma_kernel(const GemmA
     }
     return;
   }
+  // The partials are written with device-scope stores (written through to the device's coherence
+  // point) and every wavefront waits for its stores to complete; after the barrier, thread 0 counts
+  // the workgroup's arrival.  The last arrival reads the partials with device-scope loads, issued
+  // only once the increment has returned and selected this workgroup.  (A device-scope release
+  // fence would instead write back the XCD's whole L2, once per workgroup: measured, that costs
+  // more than the second-pass kernel it replaces.)
   if (holder) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const int tile = tile0 + t;
       if (tile < ntiles) {
         float* dst = a.partial + (int64_t)split * plane + (int64_t)r * a.n_pad + tile * kTileN + 4 * g;
-        *reinterpret_cast<f32x4_t*>(dst) = acc[t];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) __hip_atomic_store(dst + i, acc[t][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
-  // Arrival count.  The barrier orders every wavefront's partial stores before thread 0's
-  // device-scope release increment (which writes the XCD's L2 back).  The last arrival reads the
-  // partials with device-coherent loads, which fetch from the coherence point rather than a stale
-  // L2 line, so no cache-wide invalidate is needed; they are issued only once the increment has
-  // returned and selected this workgroup.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(a.counters + blockIdx.x, 1u, __ATOMIC_RELEASE,
+    const unsigned prev = __hip_atomic_fetch_add(a.counters + blockIdx.x, 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
     last_arrival = prev == (unsigned)(a.split_k - 1);
   }
@@ -814,9 +821,18 @@ int validate_config(int M, int N, int K, int layout, const qf_w8a16_config& c) {
 // Automatic configuration (host only).  Returns false when unsupported.  Chosen from measured
 // sweeps at M = 5 on MI355X (TILED layout): one 16-row tile per wavefront, 8 wavefronts per
 // workgroup, a 4-step weight prefetch ring; the K range is split inside the workgroup (k_waves,
-// reduced through LDS) so that a wavefront streams ~20-40 KiB, and across workgroups only when
-// K > 128 k-steps or the staged activation slice would not fit in LDS; such splits are reduced by
-// the second-pass kernel, which measured faster than the last-arrival reduction.
+// reduced through LDS), and across workgroups only when K > 128 k-steps or the staged activation
+// slice would not fit in LDS; such splits are summed by the last workgroup of each n-block.
+// A workgroup shape measured better for a particular (N, K) overrides the k_waves rule, as the
+// reference keeps a tuned table beside its heuristic (plugin/qwen_fastpath/w8a16.py:47-55).
+struct TunedShape {
+  int N, K, max_m, k_waves;
+};
+constexpr TunedShape kTuned[] = {
+    {10240, 5120, 8, 2},  // dense 27B-class qkv: 4 tiles x 2 k-slices per workgroup (11.9 us against 13.6 us)
+    {5120, 17408, 8, 2},  // dense 27B-class down, split 3 (19.0 us against 19.4 us)
+};
+
 bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
   if (M < 1 || M > QF_W8A16_MAX_M || N < 1 || K < QF_W8A16_K_ALIGN || K % QF_W8A16_K_ALIGN) return false;
   if (layout != QF_LAYOUT_ROWMAJOR && layout != QF_LAYOUT_TILED) return false;
@@ -826,7 +842,7 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
   c->depth = 4;
   c->load_hint = layout == QF_LAYOUT_TILED ? 1 : 0;
   c->waves = 8;
-  c->reduce = 1;
+  c->reduce = 0;
   const int ksteps = K / kStepK;
   if (layout == QF_LAYOUT_ROWMAJOR && M <= 2) {
     // Row-major weights at M <= 2: the GEMV kernel's contiguous 1 KiB row reads win over the
@@ -837,6 +853,7 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
     c->tiles_per_wave = 4;
     c->load_hint = 1;
     c->split_k = 1;
+    c->reduce = 1;
     while (lds_bytes(*c, M, ksteps) > kMaxLds && c->split_k < ksteps) ++c->split_k;
     return validate_config(M, N, K, layout, *c) == QF_OK;
   }
@@ -847,6 +864,15 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
     if (lds_bytes(*c, M, ksteps) <= kMaxLds || c->split_k >= ksteps) break;
     ++c->split_k;
   }
+  for (const TunedShape& t : kTuned) {
+    if (t.N == N && t.K == K && M <= t.max_m) {
+      qf_w8a16_config tc = *c;
+      tc.k_waves = t.k_waves;
+      if (validate_config(M, N, K, layout, tc) == QF_OK) *c = tc;
+    }
+  }
+  // The fused reduction needs one arrival counter per workgroup column.
+  if (c->split_k > 1 && (size_t)workgroups(*c, N) * 4 > QF_W8A16_COUNTER_BYTES) c->reduce = 1;
   return validate_config(M, N, K, layout, *c) == QF_OK;
 }
 
