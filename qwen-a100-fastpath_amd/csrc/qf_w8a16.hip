@@ -157,19 +157,29 @@ __device__ __forceinline__ f32x4_t load_scale4(const float* scale, int N, int n)
 // s_waitcnt immediate (gfx9 encoding) that waits for vmcnt == 0 and leaves expcnt / lgkmcnt free.
 constexpr int kWaitVmcnt0 = 0x0F70;
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also orders global memory, for
+// which it waits until every global load of the wavefront has returned: issued after a prefetch,
+// that drains the prefetch before the first step.  Here the global loads stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // LDS row pitch (bytes) of a staged x slice of `steps` k-steps: the row bytes plus 32, so the rows
 // that the 16 lanes of an MFMA fragment read start in distinct 32-byte bank groups.
 __host__ __device__ __forceinline__ int x_pitch(int steps) { return steps * kStepK * 2 + 32; }
 
 // Copy of x[0:M][64*s_begin : 64*(s_begin + steps)] into LDS (row m at byte m * x_pitch(steps)) in
-// 16-byte pieces, in two phases so that the caller can issue its weight requests in between:
-// load() requests the first kBatch pieces of every thread into registers, store() writes them to
-// LDS (waiting only for these loads, which were issued first) and copies any remaining pieces.
+// 16-byte pieces.  When one batch of kBatch pieces per thread holds the slice, the copy is done in
+// two phases so that the caller can issue its weight requests in between: load_batch() requests the
+// pieces into registers, store_batch() writes them to LDS (waiting only for these loads, which were
+// issued first).  Larger slices are copied by copy_all() before the weight requests.
 // Pieces are indexed (row << shift) | column, the column space padded to a power of two, so row and
 // column come from a shift and a mask.
 template <int THREADS>
 struct XStage {
-  static constexpr int kBatch = 8;
+  static constexpr int kBatch = 12;  // pieces per thread requested before the first LDS write
   u32x4_t v[kBatch];
   const uint16_t* src0;
   int row_pieces, shift, mask, span, pitch;
@@ -183,29 +193,39 @@ struct XStage {
     src0 = a.x + (int64_t)s_begin * kStepK;
   }
 
+  // Piece indices past the slice (or in a row's padding) are clamped to a piece of the slice, so
+  // every thread loads and stores unconditionally: a clamped lane copies an in-slice piece again, to
+  // the same LDS address.  Without branches around them, the compiler counts the loads in flight
+  // exactly and lets the weight requests that follow stay in flight.
+  __device__ __forceinline__ void piece(int base, int b, int& m, int& j) const {
+    const int f = min(base + b * THREADS + (int)threadIdx.x, span - 1);
+    m = f >> shift;
+    j = min(f & mask, row_pieces - 1);
+  }
+
   __device__ __forceinline__ void load_batch(const GemmArgs& a, int base) {
 #pragma unroll
     for (int b = 0; b < kBatch; ++b) {
-      const int f = base + b * THREADS + (int)threadIdx.x;
-      const int m = f >> shift, j = f & mask;
-      if (f < span && j < row_pieces) v[b] = *reinterpret_cast<const u32x4_t*>(src0 + (int64_t)m * a.ldx + j * 8);
+      int m, j;
+      piece(base, b, m, j);
+      v[b] = *reinterpret_cast<const u32x4_t*>(src0 + (int64_t)m * a.ldx + j * 8);
     }
   }
 
   __device__ __forceinline__ void store_batch(uint8_t* smem, int base) {
 #pragma unroll
     for (int b = 0; b < kBatch; ++b) {
-      const int f = base + b * THREADS + (int)threadIdx.x;
-      const int m = f >> shift, j = f & mask;
-      if (f < span && j < row_pieces) *reinterpret_cast<u32x4_t*>(smem + m * pitch + j * 16) = v[b];
+      int m, j;
+      piece(base, b, m, j);
+      *reinterpret_cast<u32x4_t*>(smem + m * pitch + j * 16) = v[b];
     }
   }
 
-  __device__ __forceinline__ void load(const GemmArgs& a) { load_batch(a, 0); }
+  // Whether one batch holds the whole slice (the pipelined path); otherwise copy_all() stages it.
+  __device__ __forceinline__ bool single_batch() const { return span <= THREADS * kBatch; }
 
-  __device__ __forceinline__ void store(const GemmArgs& a, uint8_t* smem) {
-    store_batch(smem, 0);
-    for (int base = THREADS * kBatch; base < span; base += THREADS * kBatch) {
+  __device__ __forceinline__ void copy_all(const GemmArgs& a, uint8_t* smem) {
+    for (int base = 0; base < span; base += THREADS * kBatch) {
       load_batch(a, base);
       store_batch(smem, base);
     }
@@ -222,7 +242,8 @@ __device__ __forceinline__ void split_range(int split, int splits, int ksteps, i
 // MFMA kernel
 //
 // Workgroup = WN x WK wavefronts over NT-tile groups: wavefront (wn, wk) owns the NT consecutive
-// 16-row n-tiles of group wn and slice wk of the workgroup's k-steps; blockIdx.y is the split of K
+// 16-row n-tiles of group wn and the k-steps wk, wk + WK, ... of the workgroup's range (k-slice wk);
+// blockIdx.y is the split of K
 // across workgroups.  Lane l (group g = l / 16, r = l % 16) loads, for every 64-k step s:
 //   rowmajor: w[tile*16 + r][s*64 + 16g .. +15]
 //   tiled:    bytes [16 l, 16 l + 16) of the 1 KiB tile (tile, s), which hold the same values
@@ -251,18 +272,21 @@ __global__ void __launch_bounds__(WN * WK * kWave) w8a16_mfma_kernel(const GemmA
   int s_begin, s_end;
   split_range(split, a.split_k, a.ksteps, s_begin, s_end);
   const int wg_steps = s_end - s_begin;  // k-steps staged by this workgroup
-  int k_lo, k_hi;
-  split_range(wk, WK, wg_steps, k_lo, k_hi);  // this wavefront's slice, relative to s_begin
+  // The WK k-waves of a tile group interleave at step granularity: k-wave wk takes the steps
+  // wk, wk + WK, wk + 2 WK, ... of the workgroup's range, so the group's waves read adjacent KiB of
+  // the weight stream at any moment (one stream per tile rather than WK).  wg_steps >= WK.
+  const int k_lo = wk;
+  const int k_count = (wg_steps - wk + WK - 1) / WK;
   const int ntiles = a.n_pad / kTileN;
   const int tile0 = (blockIdx.x * WN + wn) * NT;
   // >= 1: the host keeps wg_steps >= WK.  A wavefront whose tiles lie past N (only in the last
   // workgroup column) runs one clamped step instead of skipping the loop, so no branch surrounds
   // the loads; its results are never stored.
-  const int nsteps = tile0 < ntiles ? k_hi - k_lo : 1;
+  const int nsteps = tile0 < ntiles ? k_count : 1;
 
   // Weight fragment pointers at this wavefront's first step, and the byte stride between steps.
   const int8_t* wp[NT];
-  constexpr int64_t step_bytes = (LAYOUT == QF_LAYOUT_ROWMAJOR) ? kStepK : kTileN * kStepK;
+  constexpr int64_t step_bytes = ((LAYOUT == QF_LAYOUT_ROWMAJOR) ? kStepK : kTileN * kStepK) * WK;
   const int s0 = s_begin + k_lo;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -285,19 +309,27 @@ __global__ void __launch_bounds__(WN * WK * kWave) w8a16_mfma_kernel(const GemmA
   // step s - 1, so it can be issued before step s's fragment is consumed.
   const int pitch = x_pitch(wg_steps);
   XStage<WAVES * kWave> xst(a, s_begin, wg_steps);
-  xst.load(a);
-  __builtin_amdgcn_sched_barrier(0);  // the x requests go out before the weight requests
   constexpr int RING = DEPTH + 1;
   u32x4_t buf[RING][NT];
+  auto prologue = [&]() {
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) {
-    const int sd = min(d, nsteps - 1);
+    for (int d = 0; d < DEPTH; ++d) {
+      const int sd = min(d, nsteps - 1);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) buf[d][t] = load16<NTH>(wp[t] + sd * step_bytes);
+      for (int t = 0; t < NT; ++t) buf[d][t] = load16<NTH>(wp[t] + sd * step_bytes);
+    }
+  };
+  if (xst.single_batch()) {  // uniform
+    xst.load_batch(a, 0);
+    __builtin_amdgcn_sched_barrier(0);  // the x requests go out before the weight requests
+    prologue();
+    __builtin_amdgcn_sched_barrier(0);
+    xst.store_batch(smem, 0);
+  } else {
+    xst.copy_all(a, smem);
+    prologue();
   }
-  __builtin_amdgcn_sched_barrier(0);
-  xst.store(a, smem);
-  __syncthreads();
+  lds_barrier();  // the weight requests issued above stay in flight across it
 
   f32x4_t acc[NT];
 #pragma unroll
@@ -308,7 +340,7 @@ __global__ void __launch_bounds__(WN * WK * kWave) w8a16_mfma_kernel(const GemmA
     // instead: MFMA column r only feeds output column r, which is never stored.
     const int xr = min(r, a.M - 1);
     const uint8_t* xs = smem + xr * pitch + (k_lo * kStepK + 16 * g) * 2;
-    constexpr int xs_stride = kStepK * 2;
+    constexpr int xs_stride = kStepK * 2 * WK;
 
     for (int base = 0; base < nsteps; base += RING) {
 #pragma unroll
@@ -336,13 +368,13 @@ __global__ void __launch_bounds__(WN * WK * kWave) w8a16_mfma_kernel(const GemmA
 
   // Sum the WK slices through LDS (the x slice is no longer read): slice 0 adds slices 1.. WK-1.
   if constexpr (WK > 1) {
-    __syncthreads();
+    lds_barrier();
     f32x4_t* red = reinterpret_cast<f32x4_t*>(smem);
     if (wk > 0) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) red[((wk * WN + wn) * NT + t) * kWave + lane] = acc[t];
     }
-    __syncthreads();
+    lds_barrier();
     if (wk == 0) {
       for (int j = 1; j < WK; ++j) {
 #pragma unroll
