@@ -15,9 +15,11 @@ line on stdout.
   cpu_baseline the oracle's fp32-dequant restatement of the reference CPU path
                (F.linear(x.float(), W.float() * s[:, None])) on a bounded sample, host cores
 
-Other modes: --workload stack64 (64 distinct layers, one hipGraph per decode step, activations
-re-normalised between layers); --profile-gemm NAME --iters N (only that GEMM, for rocprofv3);
---copy-probe (a plain device copy of known size, for counter calibration).
+Other modes, one JSON line each: --workload stack64 (64 distinct layers, one hipGraph per decode
+step, activations re-normalised between layers); --workload msweep (gate_up at M = 1..16);
+--workload lm_head (int8 draft head 151936x5120 + pad-masked argmax at M = 1, 4);
+--profile-gemm NAME --iters N (only that GEMM, for rocprofv3); --copy-probe (a plain device copy
+of known size, for counter calibration).
 """
 from __future__ import annotations
 
@@ -153,7 +155,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--workload", choices=["layer", "stack64"], default="layer")
+    ap.add_argument("--workload", choices=["layer", "stack64", "msweep", "lm_head"], default="layer")
     ap.add_argument("--layers", type=int, default=4, help="distinct layers rotated through (layer workload)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--profile-gemm", choices=list(GEMMS), default=None)
@@ -199,6 +201,12 @@ def main():
 
     if args.workload == "stack64":
         run_stack64(torch, qf, dev, args)
+        return
+    if args.workload == "msweep":
+        run_msweep(torch, qf, dev, args)
+        return
+    if args.workload == "lm_head":
+        run_lm_head(torch, qf, dev, args)
         return
 
     M = M_TOKENS
@@ -338,6 +346,89 @@ def read_ceiling(torch, qf, dev, window: int) -> float:
     us = sorted(times)[len(times) // 2]
     del buf
     return window / us / 1e3
+
+
+def time_graph(torch, fn, launches, reps=10):
+    """Median µs per launch of a captured fn() that issues `launches` launches."""
+    g, _ = capture(torch, fn)
+    g.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e3 / launches)
+    del g
+    return sorted(times)[len(times) // 2]
+
+
+def run_msweep(torch, qf, dev, args):
+    """gate_up (N=34816, K=5120) at M = 1, 2, 3, 5, 8, 12, 16 over 4 rotating weight sets."""
+    layout = qf.TILED if args.layout == "tiled" else qf.ROWMAJOR
+    N, K = GEMMS["gate_up"]
+    R = 4
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    sets = []
+    for i in range(R):
+        w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g).t()
+        sets.append((qf.to_tiled(w) if layout == qf.TILED else w,
+                     (torch.randn(N, device=dev, generator=g).abs() * 0.002 + 1e-4).float()))
+    rows = {}
+    for M in (1, 2, 3, 5, 8, 12, 16):
+        xs = [torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16) for _ in range(R)]
+        reps = 8
+        us = time_graph(torch, lambda: [qf.w8a16_mm(xs[i], w, s, None, torch.bfloat16, layout)
+                                        for _ in range(reps) for i, (w, s) in enumerate(sets)], reps * R)
+        b = algo_bytes(M, N, K)
+        rows[M] = {"us": round(us, 2), "GB_s": round(b / us / 1e3, 1), "pct_peak": round(100 * b / us / 1e3 / PEAK_GBS, 1),
+                   "config": list(qf.resolve_config(M, N, K, layout))}
+        log(f"  gate_up M={M:2d}: {us:7.2f} us  {b / us / 1e3:7.0f} GB/s  {100 * b / us / 1e3 / PEAK_GBS:5.1f}%")
+    worst = min(r["GB_s"] for r in rows.values())
+    line = {"metric": METRIC, "value": worst, "unit": "GB/s", "n_gpus": 1, "steps": 10, "warmup": 2,
+            "ms_per_step": round(rows[5]["us"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded int8 weights, fp32 scales, bf16 activations)",
+            "config": {"workload": "gate_up 34816x5120 M sweep (value = the slowest M's GB/s)", "weight_layout": args.layout},
+            "per_m": rows}
+    print(json.dumps(line), flush=True)
+
+
+def run_lm_head(torch, qf, dev, args):
+    """Int8 MTP draft head: V=151936, H=5120, at M = 1 and 4.  One step = W8A16 logits for M hidden rows
+    plus the pad-masked argmax (64 pad columns, vocab offset 0); weights rotate over 2 copies (1.56 GB)."""
+    V, H, num_pad = 151936, 5120, 64
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    heads = []
+    for i in range(2):
+        w = (torch.randn(V, H, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        heads.append(qf.make_int8_head(w, num_pad))
+        del w
+    rows = {}
+    for M in (1, 4):
+        hs = [torch.randn(M, H, device=dev, generator=g).to(torch.bfloat16) for _ in heads]
+
+        def step(i):
+            logits = qf.int8_logits(heads[i], hs[i])
+            return qf.top_tokens(logits, num_pad, 0)
+        reps = 8
+        us = time_graph(torch, lambda: [step(i) for _ in range(reps) for i in range(len(heads))], reps * len(heads))
+        gemm = algo_bytes(M, V, H)
+        b = gemm + 2 * M * V + 8 * M  # the argmax reads the logits and writes M ids
+        rows[M] = {"us_per_draft_step": round(us, 2), "GB_s": round(b / us / 1e3, 1),
+                   "pct_peak": round(100 * b / us / 1e3 / PEAK_GBS, 1), "algorithmic_bytes": b}
+        log(f"  lm_head M={M}: {us:7.2f} us  {b / us / 1e3:7.0f} GB/s  {100 * b / us / 1e3 / PEAK_GBS:5.1f}%")
+    line = {"metric": METRIC, "value": rows[1]["GB_s"], "unit": "GB/s", "n_gpus": 1, "steps": 10, "warmup": 2,
+            "ms_per_step": round(rows[1]["us_per_draft_step"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic (bf16 N(0,0.02) head quantised per row to int8)",
+            "config": {"workload": "int8 draft lm_head 151936x5120 + pad-masked argmax (value = M=1 GB/s)",
+                       "weight_layout": "tiled"},
+            "per_m": rows}
+    print(json.dumps(line), flush=True)
 
 
 def run_stack64(torch, qf, dev, args):

@@ -179,7 +179,7 @@ __host__ __device__ __forceinline__ int x_pitch(int steps) { return steps * kSte
 // column come from a shift and a mask.
 template <int THREADS>
 struct XStage {
-  static constexpr int kBatch = 12;  // pieces per thread requested before the first LDS write
+  static constexpr int kBatch = 10;  // pieces per thread requested before the first LDS write
   u32x4_t v[kBatch];
   const uint16_t* src0;
   int row_pieces, shift, mask, span, pitch;
@@ -679,37 +679,72 @@ __device__ __forceinline__ bool argmax_better(float av, int ai, float bv, int bi
   return ai < bi;
 }
 
-__global__ void __launch_bounds__(256) argmax_rows_kernel(const uint16_t* logits, int64_t ld, int n_valid,
-                                                          int64_t index_offset, int64_t* out) {
-  __shared__ float sv[256];
-  __shared__ int si[256];
+constexpr int kArgmaxThreads = 1024;
+
+// Better of two (value, index) candidates, folded into (bv, bi).
+__device__ __forceinline__ void argmax_fold(float v, int i, float& bv, int& bi) {
+  if (argmax_better(v, i, bv, bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+// One workgroup of 1024 threads per row.  With VEC each thread reads 8 logits per 16-byte load,
+// four loads in flight, and walks each group in index order; the row tail (n_valid % 8) and
+// unaligned rows are read one logit at a time.  The workgroup reduction is a fixed butterfly plus an
+// LDS tree, so the result does not depend on timing; argmax_better makes it order-independent anyway.
+template <bool VEC>
+__global__ void __launch_bounds__(kArgmaxThreads) argmax_rows_kernel(const uint16_t* logits, int64_t ld, int n_valid,
+                                                                     int64_t index_offset, int64_t* out) {
+  __shared__ float sv[kArgmaxThreads / kWave];
+  __shared__ int si[kArgmaxThreads / kWave];
   const uint16_t* row = logits + (int64_t)blockIdx.x * ld;
   float bv = -__builtin_inff();
   int bi = 0x7fffffff;
-  for (int n = threadIdx.x; n < n_valid; n += 256) {
-    const float v = __uint_as_float((uint32_t)row[n] << 16);
-    if (argmax_better(v, n, bv, bi)) {
-      bv = v;
-      bi = n;
-    }
-  }
-  sv[threadIdx.x] = bv;
-  si[threadIdx.x] = bi;
-  __syncthreads();
-  for (int stride = 128; stride >= 1; stride >>= 1) {
-    if ((int)threadIdx.x < stride) {
-      const float ov = sv[threadIdx.x + stride];
-      const int oi = si[threadIdx.x + stride];
-      if (argmax_better(ov, oi, sv[threadIdx.x], si[threadIdx.x])) {
-        sv[threadIdx.x] = ov;
-        si[threadIdx.x] = oi;
+  int scalar_from = 0;
+  if constexpr (VEC) {
+    const int nvec = n_valid / 8;
+    const u32x4_t* vrow = reinterpret_cast<const u32x4_t*>(row);
+    auto fold8 = [&](const u32x4_t v, int c) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t d = v[j];
+        argmax_fold(__uint_as_float(d << 16), c * 8 + 2 * j, bv, bi);
+        argmax_fold(__uint_as_float(d & 0xffff0000u), c * 8 + 2 * j + 1, bv, bi);
       }
+    };
+    int c = threadIdx.x;
+    for (; c + 3 * kArgmaxThreads < nvec; c += 4 * kArgmaxThreads) {
+      const u32x4_t v0 = vrow[c];
+      const u32x4_t v1 = vrow[c + kArgmaxThreads];
+      const u32x4_t v2 = vrow[c + 2 * kArgmaxThreads];
+      const u32x4_t v3 = vrow[c + 3 * kArgmaxThreads];
+      fold8(v0, c);
+      fold8(v1, c + kArgmaxThreads);
+      fold8(v2, c + 2 * kArgmaxThreads);
+      fold8(v3, c + 3 * kArgmaxThreads);
     }
-    __syncthreads();
+    for (; c < nvec; c += kArgmaxThreads) fold8(vrow[c], c);
+    scalar_from = nvec * 8;
   }
+  for (int n = scalar_from + threadIdx.x; n < n_valid; n += kArgmaxThreads)
+    argmax_fold(__uint_as_float((uint32_t)row[n] << 16), n, bv, bi);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, kWave);
+    const int oi = __shfl_xor(bi, off, kWave);
+    argmax_fold(ov, oi, bv, bi);
+  }
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
   if (threadIdx.x == 0) {
+    for (int w = 1; w < kArgmaxThreads / kWave; ++w) argmax_fold(sv[w], si[w], bv, bi);
     // every column -inf (or no valid column): torch.argmax returns the first index
-    const int idx = (si[0] == 0x7fffffff) ? 0 : si[0];
+    const int idx = (bi == 0x7fffffff) ? 0 : bi;
     out[blockIdx.x] = (int64_t)idx + index_offset;
   }
 }
@@ -889,6 +924,22 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
     while (lds_bytes(*c, M, ksteps) > kMaxLds && c->split_k < ksteps) ++c->split_k;
     return validate_config(M, N, K, layout, *c) == QF_OK;
   }
+  if (M >= 8 && round_up16(N) / (kTileN * 16) >= 128) {  // wide N only: >= 128 workgroups of 256 rows
+    // Wide M and N: the staged x slice grows with M, so a workgroup covers more weight rows per
+    // staged byte -- 8 tile groups of 2 tiles, each wavefront over the whole K range of its split
+    // (gate_up: M = 8 35.0 us, M = 12 36.5 us against 44 and 48 us with the M = 5 shape); from
+    // M = 13 K is split so that the slice stays near 56 KiB (M = 16: 39.7 us against 54 us).
+    c->tiles_per_wave = 2;
+    c->k_waves = 1;
+    c->split_k = M >= 13 ? ceil_div((int)((int64_t)M * K * 2), 56 * 1024) : 1;
+    if (c->split_k > ksteps) c->split_k = ksteps;
+    while (lds_bytes(*c, M, ksteps) > kMaxLds && c->split_k < ksteps) ++c->split_k;
+    if (c->split_k > 1) c->reduce = 1;
+    if ((size_t)workgroups(*c, N) * 4 > QF_W8A16_COUNTER_BYTES) c->reduce = 1;
+    return validate_config(M, N, K, layout, *c) == QF_OK;
+  }
+  // Narrow M at 1..2 tokens: 4-wavefront workgroups (gate_up M = 1: 30.4 us against 35.1 us).
+  if (M <= 2) c->waves = 4;
   c->split_k = ceil_div(ksteps, 128);
   for (;;) {
     const int per_split = ksteps / c->split_k;
@@ -1075,8 +1126,13 @@ int qf_argmax_rows_bf16(const uint16_t* logits, int64_t ld, int M, int N, int n_
                         int64_t* out, void* stream) {
   if (logits == nullptr || out == nullptr || M < 1 || N < 1 || ld < N || n_valid < 0 || n_valid > N)
     return QF_ERR_INVALID_ARG;
-  hipLaunchKernelGGL(argmax_rows_kernel, dim3(M), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), logits, ld,
-                     n_valid, index_offset, out);
+  const bool vec = aligned16(logits) && (ld % 8) == 0;
+  if (vec)
+    hipLaunchKernelGGL(argmax_rows_kernel<true>, dim3(M), dim3(kArgmaxThreads), 0, reinterpret_cast<hipStream_t>(stream),
+                       logits, ld, n_valid, index_offset, out);
+  else
+    hipLaunchKernelGGL(argmax_rows_kernel<false>, dim3(M), dim3(kArgmaxThreads), 0, reinterpret_cast<hipStream_t>(stream),
+                       logits, ld, n_valid, index_offset, out);
   return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
 }
 

@@ -22,7 +22,7 @@ from typing import Callable, NamedTuple, Optional
 import torch
 
 from . import _lib as L
-from .w8a16 import ROWMAJOR, SMALL_M, TILED, pick_config, w8a16_mm
+from .w8a16 import ROWMAJOR, SMALL_M, TILED, pick_config, to_tiled, w8a16_mm
 
 logger = logging.getLogger("vllm.qwen_fastpath")
 
@@ -229,10 +229,12 @@ class W8A16LinearMethod:
 class Int8Head(NamedTuple):
     """What the reference stores as draft_model._qf_head_i8 (patches.py:149)."""
 
-    w_t: torch.Tensor      # int8 [H, V] view with stride (1, H) of the [V, H] quantised head
+    w_t: torch.Tensor      # int8 [H, V] view with stride (1, H) of the [V, H] quantised head, or its
+                           # TILED image (layout == TILED)
     scale: torch.Tensor    # fp32 [V]
     num_pad: int           # padded vocabulary rows at the end
     cfg: object            # pick_config(V, H)
+    layout: int = ROWMAJOR
 
 
 def quantize_lm_head(weight: torch.Tensor):
@@ -252,10 +254,18 @@ def quantize_lm_head(weight: torch.Tensor):
     return w8, scale
 
 
-def make_int8_head(weight: torch.Tensor, num_pad: int = 0) -> Int8Head:
+def make_int8_head(weight: torch.Tensor, num_pad: int = 0, layout: int = TILED) -> Int8Head:
+    """The draft head's int8 copy.  The copy is this plugin's own (the checkpoint's bf16 head is left
+    as it is), so it is kept in the TILED layout the kernel streams fastest; layout=ROWMAJOR keeps the
+    reference's [V, H] row-major copy (patches.py:149)."""
     w8, scale = quantize_lm_head(weight)
     V, H = w8.shape
-    return Int8Head(w8.t(), scale, int(num_pad), pick_config(V, H))
+    cfg = pick_config(V, H, layout)
+    if layout == TILED and cfg is not None:
+        w_img = to_tiled(w8.t())
+        del w8
+        return Int8Head(w_img, scale, int(num_pad), cfg, TILED)
+    return Int8Head(w8.t(), scale, int(num_pad), pick_config(V, H), ROWMAJOR)
 
 
 def int8_logits(head: Optional[Int8Head], hidden_states: torch.Tensor, logits_as_input: bool = False,
@@ -267,7 +277,7 @@ def int8_logits(head: Optional[Int8Head], hidden_states: torch.Tensor, logits_as
             or scale != 1.0 or draft_id_to_target_id is not None or head.cfg is None):
         return None
     x = hidden_states if hidden_states.stride(-1) == 1 else hidden_states.contiguous()
-    return w8a16_mm(x, head.w_t, head.scale, head.cfg, torch.bfloat16)
+    return w8a16_mm(x, head.w_t, head.scale, head.cfg, torch.bfloat16, head.layout)
 
 
 def top_tokens(logits: torch.Tensor, num_pad: int = 0, vocab_start: int = 0) -> torch.Tensor:

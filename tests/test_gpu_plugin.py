@@ -121,15 +121,20 @@ def test_draft_head_logits_and_argmax(oracle):
     g.manual_seed(6)
     w_dev = (torch.randn(V, H, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
     wb = bf16_bits(w_dev)
-    head = qf.make_int8_head(w_dev, num_pad)
+    head = qf.make_int8_head(w_dev, num_pad)  # TILED copy
+    head_rm = qf.make_int8_head(w_dev, num_pad, qf.ROWMAJOR)  # the reference's row-major copy
+    assert head.layout == qf.TILED and head_rm.layout == qf.ROWMAJOR
     q, s = oracle.quantize_rows(wb)
     assert np.array_equal(head.scale.cpu().numpy(), s)
+    assert np.array_equal(qf.from_tiled(head.w_t, V, H).cpu().numpy(), head_rm.w_t.cpu().numpy())
     for M in (1, 4):
         hb = oracle.bf16_from_f64(rng.standard_normal((M, H)))
         logits = qf.int8_logits(head, to_dev_bf16(hb, DEV))
         assert logits is not None and logits.shape == (M, V)
         rep = oracle.check_w8a16(bf16_bits(logits), hb, q, s)
         assert rep.ok, rep
+        rep_rm = oracle.check_w8a16(bf16_bits(qf.int8_logits(head_rm, to_dev_bf16(hb, DEV))), hb, q, s)
+        assert rep_rm.ok, rep_rm
         ids = qf.top_tokens(logits, num_pad, start).cpu().numpy()
         want = oracle.argmax_rows(bf16_bits(logits), V - num_pad, start)
         assert np.array_equal(ids, want)  # same logits: argmax semantics must agree exactly
@@ -160,3 +165,22 @@ def test_top_tokens_semantics():
     v[3, :] = -float("inf")            # all -inf -> first index
     ids = qf.top_tokens(v.to(torch.bfloat16).to(DEV), num_pad=4, vocab_start=10).cpu().tolist()
     assert ids == [20, 15, 17, 10]
+
+
+def test_top_tokens_vector_path(oracle):
+    """Rows whose stride allows 16-byte loads (8 logits per load) plus a scalar tail."""
+    N, num_pad, start = 41000, 5, 17
+    v = np.full((5, N), -1.0)
+    v[0, 100] = v[0, 40000] = 4.0          # tie across vector groups -> first
+    v[1, N - 2] = 9.0                      # in the pad
+    v[1, N - num_pad - 1] = 8.0            # last valid column, in the scalar tail
+    v[2, 33333] = np.nan
+    v[2, 9999] = np.nan                    # first NaN wins
+    v[3, :] = -np.inf
+    v[4, 7] = v[4, N - num_pad - 2] = 6.0  # tie between a vector group and the tail -> first
+    bits = oracle.bf16_from_f64(v)
+    logits = torch.from_numpy(bits.view(np.int16)).to(DEV).view(torch.bfloat16)
+    ids = qf.top_tokens(logits, num_pad, start).cpu().numpy()
+    want = oracle.argmax_rows(bits, N - num_pad, start)
+    assert np.array_equal(ids, want)
+    assert list(ids) == [100 + start, N - num_pad - 1 + start, 9999 + start, start, 7 + start]
