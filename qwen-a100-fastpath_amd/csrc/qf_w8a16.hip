@@ -749,6 +749,110 @@ __global__ void __launch_bounds__(kArgmaxThreads) argmax_rows_kernel(const uint1
   }
 }
 
+// Row split over workgroups: for rows of many logits (the draft head's 151936) one workgroup per
+// row is bound by the latency of its own loads, so each row is cut into chunks of kArgmaxChunk
+// logits, one 256-thread workgroup each (grid = chunks x rows).  A workgroup writes its candidate (value,
+// index) with device-scope stores into a small device-resident table, waits for them, and counts
+// its arrival on the row's counter; the last workgroup of the row folds all candidates (the order
+// is total -- value, then index, NaN highest -- so the fold does not depend on arrival order),
+// writes the index and resets the counter to zero.  Calls that overlap on one device share the
+// table and must not run at the same time.
+constexpr int kArgmaxSplitThreads = 256;
+constexpr int kArgmaxChunk = 8192;            // logits per workgroup (16 KiB)
+constexpr int kArgmaxMaxBlocks = 64;          // chunks per row
+constexpr int kArgmaxMaxRows = QF_W8A16_MAX_M;
+__device__ float g_argmax_val[kArgmaxMaxRows * kArgmaxMaxBlocks];
+__device__ int g_argmax_idx[kArgmaxMaxRows * kArgmaxMaxBlocks];
+__device__ unsigned g_argmax_arrivals[kArgmaxMaxRows];
+
+__device__ __forceinline__ void argmax_block_reduce(float& bv, int& bi, float* sv, int* si) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, kWave);
+    const int oi = __shfl_xor(bi, off, kWave);
+    argmax_fold(ov, oi, bv, bi);
+  }
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < (int)(blockDim.x / kWave); ++w) argmax_fold(sv[w], si[w], bv, bi);
+  }
+}
+
+__global__ void __launch_bounds__(kArgmaxSplitThreads) argmax_rows_split_kernel(const uint16_t* logits, int64_t ld,
+                                                                                int n_valid, int64_t index_offset,
+                                                                                int64_t* out) {
+  __shared__ float sv[kArgmaxSplitThreads / kWave];
+  __shared__ int si[kArgmaxSplitThreads / kWave];
+  __shared__ int last;
+  const int m = blockIdx.y;
+  const int b = blockIdx.x;
+  const int nb = gridDim.x;
+  const uint16_t* row = logits + (int64_t)m * ld;
+  const int c0 = b * (kArgmaxChunk / 8);                        // first 8-logit group of the chunk
+  const int c1 = min(c0 + kArgmaxChunk / 8, n_valid / 8);
+  const u32x4_t* vrow = reinterpret_cast<const u32x4_t*>(row);
+  float bv = -__builtin_inff();
+  int bi = 0x7fffffff;
+  int c = c0 + threadIdx.x;
+  for (; c + 3 * kArgmaxSplitThreads < c1; c += 4 * kArgmaxSplitThreads) {
+    const u32x4_t v0 = vrow[c];
+    const u32x4_t v1 = vrow[c + kArgmaxSplitThreads];
+    const u32x4_t v2 = vrow[c + 2 * kArgmaxSplitThreads];
+    const u32x4_t v3 = vrow[c + 3 * kArgmaxSplitThreads];
+    const u32x4_t vs[4] = {v0, v1, v2, v3};
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int base = (c + q * kArgmaxSplitThreads) * 8 + 2 * j;
+        argmax_fold(__uint_as_float(vs[q][j] << 16), base, bv, bi);
+        argmax_fold(__uint_as_float(vs[q][j] & 0xffff0000u), base + 1, bv, bi);
+      }
+  }
+  for (; c < c1; c += kArgmaxSplitThreads) {
+    const u32x4_t v = vrow[c];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      argmax_fold(__uint_as_float(v[j] << 16), c * 8 + 2 * j, bv, bi);
+      argmax_fold(__uint_as_float(v[j] & 0xffff0000u), c * 8 + 2 * j + 1, bv, bi);
+    }
+  }
+  if (b == nb - 1) {  // the row tail past the last full 8-logit group
+    for (int n = (n_valid / 8) * 8 + threadIdx.x; n < n_valid; n += kArgmaxSplitThreads)
+      argmax_fold(__uint_as_float((uint32_t)row[n] << 16), n, bv, bi);
+  }
+  argmax_block_reduce(bv, bi, sv, si);
+  if (threadIdx.x == 0) {
+    const int slot = m * kArgmaxMaxBlocks + b;
+    __hip_atomic_store(&g_argmax_val[slot], bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&g_argmax_idx[slot], bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    const unsigned prev = __hip_atomic_fetch_add(&g_argmax_arrivals[m], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = prev == (unsigned)(nb - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  bv = -__builtin_inff();
+  bi = 0x7fffffff;
+  if ((int)threadIdx.x < nb) {
+    const int slot = m * kArgmaxMaxBlocks + threadIdx.x;
+    bv = __hip_atomic_load(&g_argmax_val[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bi = __hip_atomic_load(&g_argmax_idx[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();  // sv / si are reused
+  argmax_block_reduce(bv, bi, sv, si);
+  if (threadIdx.x == 0) {
+    const int idx = (bi == 0x7fffffff) ? 0 : bi;
+    out[m] = (int64_t)idx + index_offset;
+    __hip_atomic_store(&g_argmax_arrivals[m], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // Read-bandwidth probe: every byte of [buf, buf + bytes) read once with 16-byte loads, grid-stride.
 // One 32-bit xor per workgroup is written to sink so the loads cannot be dropped.
@@ -1127,7 +1231,11 @@ int qf_argmax_rows_bf16(const uint16_t* logits, int64_t ld, int M, int N, int n_
   if (logits == nullptr || out == nullptr || M < 1 || N < 1 || ld < N || n_valid < 0 || n_valid > N)
     return QF_ERR_INVALID_ARG;
   const bool vec = aligned16(logits) && (ld % 8) == 0;
-  if (vec)
+  const int chunks = ceil_div(n_valid, kArgmaxChunk);
+  if (vec && M <= kArgmaxMaxRows && chunks >= 2 && chunks <= kArgmaxMaxBlocks) {
+    hipLaunchKernelGGL(argmax_rows_split_kernel, dim3(chunks, M), dim3(kArgmaxSplitThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), logits, ld, n_valid, index_offset, out);
+  } else if (vec)
     hipLaunchKernelGGL(argmax_rows_kernel<true>, dim3(M), dim3(kArgmaxThreads), 0, reinterpret_cast<hipStream_t>(stream),
                        logits, ld, n_valid, index_offset, out);
   else

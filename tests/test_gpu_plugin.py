@@ -184,3 +184,22 @@ def test_top_tokens_vector_path(oracle):
     want = oracle.argmax_rows(bits, N - num_pad, start)
     assert np.array_equal(ids, want)
     assert list(ids) == [100 + start, N - num_pad - 1 + start, 9999 + start, start, 7 + start]
+
+
+@pytest.mark.parametrize("M,N,num_pad", [(1, 16384, 0), (16, 16392, 3), (3, 151936, 64), (16, 8192 * 64, 1)])
+def test_top_tokens_row_split(oracle, M, N, num_pad):
+    """Rows cut into 8192-logit chunks across workgroups, folded by the last one: random rows with a
+    planted maximum in a random chunk and a tie later in the row, against the oracle."""
+    rng = np.random.default_rng(M * 100 + N % 97)
+    v = rng.standard_normal((M, N))
+    for m in range(M):
+        j = int(rng.integers(0, N - num_pad))
+        v[m, j] = 50.0 + m
+        v[m, min(j + 1 + int(rng.integers(0, 9000)), N - num_pad - 1)] = 50.0 + m  # tie: first wins
+        if num_pad:
+            v[m, N - 1] = 1e4                                                       # pad ignored
+    bits = oracle.bf16_from_f64(v)
+    logits = torch.from_numpy(bits.view(np.int16)).to(DEV).view(torch.bfloat16)
+    for _ in range(2):  # the arrival counters are back at zero for the next call
+        ids = qf.top_tokens(logits, num_pad, 5).cpu().numpy()
+        assert np.array_equal(ids, oracle.argmax_rows(bits, N - num_pad, 5))
