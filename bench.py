@@ -16,7 +16,7 @@ line on stdout.
                (F.linear(x.float(), W.float() * s[:, None])) on a bounded sample, host cores
 
 Other modes, one JSON line each: --workload stack64 (64 distinct layers, one hipGraph per decode
-step, activations re-normalised between layers); --workload msweep (gate_up at M = 1..16);
+step, the layer output re-normalised to unit RMS as the next layer's input); --workload msweep (gate_up at M = 1..16);
 --workload lm_head (int8 draft head 151936x5120 + pad-masked argmax at M = 1, 4);
 --profile-gemm NAME --iters N (only that GEMM, for rocprofv3); --copy-probe (a plain device copy
 of known size, for counter calibration).
@@ -161,6 +161,7 @@ def main():
     ap.add_argument("--profile-gemm", choices=list(GEMMS), default=None)
     ap.add_argument("--iters", type=int, default=200)
     ap.add_argument("--copy-probe", action="store_true")
+    ap.add_argument("--read-probe", action="store_true", help="only the library's read probe over the dominant GEMM's bytes")
     ap.add_argument("--layout", choices=["tiled", "rowmajor"], default="tiled",
                     help="weight layout: tiled = pre-permuted at load (default), rowmajor = checkpoint layout")
     ap.add_argument("--cfg", default=None, help="explicit config kernel,split_k,tiles,waves,depth,hint (profile mode)")
@@ -186,6 +187,11 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         log(f"copy probe: {args.iters} copies of {n} bytes")
+        return
+
+    if args.read_probe:
+        ceiling = read_ceiling(torch, qf, dev, algo_bytes(M_TOKENS, *GEMMS[DOMINANT]))
+        log(f"read probe: {ceiling:.0f} GB/s")
         return
 
     if args.profile_gemm:
@@ -276,6 +282,25 @@ def main():
             dominant_us = us
         del g
 
+    # The reference's single-linear case at one token: N = K = 5120, M = 1 (reported beside the step).
+    single = {}
+    N1, K1 = 5120, 5120
+    g1 = torch.Generator(device=dev)
+    g1.manual_seed(99)
+    sets1 = []
+    for i in range(16):  # 16 x 26 MB rotate past the 256 MB MALL
+        w1 = torch.randint(-127, 128, (N1, K1), dtype=torch.int8, device=dev, generator=g1).t()
+        sets1.append((qf.to_tiled(w1) if layout == qf.TILED else w1,
+                      (torch.randn(N1, device=dev, generator=g1).abs() * 0.002 + 1e-4).float(),
+                      torch.randn(1, K1, device=dev, generator=g1).to(torch.bfloat16)))
+    us1 = time_graph(torch, lambda: [qf.w8a16_mm(x1, w1, s1, None, torch.bfloat16, layout)
+                                     for _ in range(8) for (w1, s1, x1) in sets1], 8 * len(sets1))
+    b1 = algo_bytes(1, N1, K1)
+    single = {"N": N1, "K": K1, "M": 1, "us": round(us1, 2), "GB_s": round(b1 / us1 / 1e3, 1),
+              "pct_peak": round(100 * b1 / us1 / 1e3 / PEAK_GBS, 1), "config": list(qf.resolve_config(1, N1, K1, layout))}
+    log(f"  single linear M=1 N=K=5120: {us1:7.2f} us  {b1 / us1 / 1e3:7.0f} GB/s  {100 * b1 / us1 / 1e3 / PEAK_GBS:5.1f}%")
+    del sets1
+
     dom_bytes = algo_bytes(M, *GEMMS[DOMINANT])
     achieved = dom_bytes / dominant_us / 1e3
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
@@ -309,6 +334,7 @@ def main():
         "us_per_layer": round(ms_per_step * 1e3, 2),
         "pct_of_peak": round(100 * value / PEAK_GBS, 2),
         "per_gemm": per_gemm,
+        "single_linear_m1": single,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
@@ -433,28 +459,25 @@ def run_lm_head(torch, qf, dev, args):
 
 def run_stack64(torch, qf, dev, args):
     """64 layers x 4 GEMMs at M=5 with distinct weights, one hipGraph per decode step.  Glue between
-    GEMMs: o_proj reads the first 8192 qkv outputs, down reads silu(gate) * up; each GEMM input is
-    re-normalised to unit RMS per row."""
+    GEMMs (the workload leaves it open): o_proj reads the first 8192 qkv outputs and down the first
+    17408 gate_up outputs, both as strided views (no copy); the next layer's input is the layer output
+    re-normalised to unit RMS per row (one fused torch rms_norm)."""
     M = M_TOKENS
     nl = 64
     log(f"stack64: allocating {nl} layers ({nl * sum(N * K for N, K in GEMMS.values()) / 1e9:.1f} GB)")
     layout = qf.TILED if args.layout == "tiled" else qf.ROWMAJOR
     layers = [Layer(torch, qf, dev, 5000 + i, M, layout) for i in range(nl)]
     x0 = torch.randn(M, 5120, device=dev).to(torch.bfloat16)
-
-    def rms(t):
-        t = t.float()
-        return (t * torch.rsqrt(t.pow(2).mean(dim=-1, keepdim=True))).to(torch.bfloat16)
+    rms = lambda t: torch.nn.functional.rms_norm(t, (t.shape[-1],))  # noqa: E731
 
     def step():
         h = x0
         for L_ in layers:
             mm = lambda a, n: qf.w8a16_mm(a, L_.w[n], L_.s[n], None, torch.bfloat16, layout)  # noqa: E731
             qkv = mm(h, "qkv")
-            o = mm(rms(qkv[:, :8192]), "o_proj")
-            gu = mm(rms(o), "gate_up")
-            g, u = gu[:, :17408].float(), gu[:, 17408:].float()
-            d = mm(rms(torch.nn.functional.silu(g) * u), "down")
+            o = mm(qkv[:, :8192], "o_proj")
+            gu = mm(o, "gate_up")
+            d = mm(gu[:, :17408], "down")
             h = rms(d)
         return h
 
@@ -470,13 +493,14 @@ def run_stack64(torch, qf, dev, args):
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     value = steps * bytes_per_step / el / 1e9
+    log(f"stack64: {steps} steps, {el / steps * 1e3:.3f} ms/step, {value:.0f} GB/s ({100 * value / PEAK_GBS:.1f}% of 8 TB/s)")
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps,
         "warmup": max(1, args.warmup // 10), "ms_per_step": round(el / steps * 1e3, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded int8 weights, fp32 scales, bf16 activations)",
         "config": {"workload": "64-layer decode-step linear stack at M=5 (4 GEMMs/layer, distinct weights, "
-                               "unit-RMS glue), one hipGraph per step", "M": M, "layers": nl,
+                               "one rms_norm per layer), one hipGraph per step", "M": M, "layers": nl,
                    "bytes_per_step": bytes_per_step},
         "us_per_layer": round(el / steps / nl * 1e6, 2),
         "pct_of_peak": round(100 * value / PEAK_GBS, 2),
