@@ -155,7 +155,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--workload", choices=["layer", "stack64", "msweep", "lm_head"], default="layer")
+    ap.add_argument("--workload", choices=["layer", "stack64", "msweep", "lm_head", "prefill"], default="layer")
     ap.add_argument("--layers", type=int, default=4, help="distinct layers rotated through (layer workload)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--profile-gemm", choices=list(GEMMS), default=None)
@@ -213,6 +213,9 @@ def main():
         return
     if args.workload == "lm_head":
         run_lm_head(torch, qf, dev, args)
+        return
+    if args.workload == "prefill":
+        run_prefill(torch, qf, dev, args)
         return
 
     M = M_TOKENS
@@ -419,6 +422,35 @@ def run_msweep(torch, qf, dev, args):
             "ms_per_step": round(rows[5]["us"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded int8 weights, fp32 scales, bf16 activations)",
             "config": {"workload": "gate_up 34816x5120 M sweep (value = the slowest M's GB/s)", "weight_layout": args.layout},
+            "per_m": rows}
+    print(json.dumps(line), flush=True)
+
+
+def run_prefill(torch, qf, dev, args):
+    """gate_up (N=34816, K=5120) at prefill widths M = 64, 256, 1024, 2048 on TILED weights: the
+    chunked exact bf16 widening + library bf16 GEMM path, against 16-row slices of the decode kernel."""
+    N, K = GEMMS["gate_up"]
+    g = torch.Generator(device=dev)
+    g.manual_seed(13)
+    w = qf.to_tiled(torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g).t())
+    s = (torch.randn(N, device=dev, generator=g).abs() * 0.002 + 1e-4).float()
+    rows = {}
+    for M in (64, 256, 1024, 2048):
+        x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+        us = time_graph(torch, lambda: qf.w8a16_mm_prefill(x, w, s, torch.bfloat16, qf.TILED), 1, reps=5)
+        tflops = 2.0 * M * N * K / us / 1e6
+        entry = {"us": round(us, 1), "TFLOP_s": round(tflops, 1), "pct_bf16_mfma_peak": round(100 * tflops / 2500.0, 1)}
+        if M <= 256:
+            us_sl = time_graph(torch, lambda: [qf.w8a16_mm(x[i:i + 16], w, s, None, torch.bfloat16, qf.TILED)
+                                               for i in range(0, M, 16)], 1, reps=5)
+            entry["us_16row_slices"] = round(us_sl, 1)
+        rows[M] = entry
+        log(f"  prefill gate_up M={M:5d}: {us:9.1f} us  {tflops:7.1f} TFLOP/s"
+            + (f"  (16-row slices {entry['us_16row_slices']:.1f} us)" if "us_16row_slices" in entry else ""))
+    line = {"metric": METRIC, "value": rows[2048]["TFLOP_s"], "unit": "TFLOP/s", "n_gpus": 1, "steps": 5, "warmup": 2,
+            "ms_per_step": round(rows[2048]["us"] / 1e3, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded int8 weights, fp32 scales, bf16 activations)",
+            "config": {"workload": "gate_up 34816x5120 prefill widths on TILED weights (value = M=2048 TFLOP/s)"},
             "per_m": rows}
     print(json.dumps(line), flush=True)
 

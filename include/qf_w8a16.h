@@ -123,6 +123,15 @@ int qf_w8a16_repack(const int8_t* w_rowmajor, int64_t ldw, int8_t* w_tiled,
 int qf_w8a16_unpack(const int8_t* w_tiled, int8_t* w_rowmajor, int64_t ldw,
                     int N, int K, void* stream);
 
+/* Exact int8 -> bf16 copy of weight rows [n0, n0 + rows) of an [N, K] weight in either layout (TILED:
+ * the image made by qf_w8a16_repack) into the row-major bf16 matrix out (row stride ldo elements,
+ * ldo % 8 == 0, 16-byte aligned).  No scale is applied.  It feeds a library bf16 GEMM (fp32
+ * accumulation, scale after the K reduction) for M beyond QF_W8A16_MAX_M on weights kept in the
+ * TILED layout, which no W8A8 library kernel can read.  No reference counterpart: the reference
+ * routes M > 16 to CUTLASS W8A8 on the checkpoint layout (plugin/qwen_fastpath/patches.py:99-100). */
+int qf_w8a16_dequant_bf16(const int8_t* w, int64_t ldw, int layout, int N, int K,
+                          int n0, int rows, uint16_t* out, int64_t ldo, void* stream);
+
 /* Per-row symmetric int8 quantisation of a bf16 [V, H] matrix (row stride ldw elements):
  *   s[v] = max(max_h |w[v,h]|, 1e-8) / 127   (fp32, IEEE division)
  *   q[v,h] = clamp(round_half_even(w[v,h] / s[v]), -127, 127)

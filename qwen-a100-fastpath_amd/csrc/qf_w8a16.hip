@@ -637,6 +637,36 @@ __global__ void __launch_bounds__(256) repack_kernel(const int8_t* src, int8_t* 
 }
 
 // ---------------------------------------------------------------------------------------------
+// Exact int8 -> bf16 copy of weight rows [n0, n0 + rows) into a row-major bf16 matrix (row stride
+// ldo), from either layout: the operand of a library bf16 GEMM for M beyond the decode widths.  One
+// thread per 16 weights: a 16-byte gathered read (for TILED, one lane's chunk of a 1 KiB tile) and
+// a 32-byte coalesced write.  The scale is not applied (it follows the K reduction).
+// ---------------------------------------------------------------------------------------------
+template <int LAYOUT>
+__global__ void __launch_bounds__(256) dequant_bf16_kernel(const int8_t* w, int64_t ldw, int ksteps, int n0,
+                                                           int64_t pieces, uint16_t* out, int64_t ldo) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= pieces) return;
+  const int kp = ksteps * 4;  // 16-weight pieces per row
+  const int64_t r = q / kp;   // output row
+  const int c = (int)(q - r * kp);
+  const int64_t n = n0 + r;
+  const int8_t* src;
+  if constexpr (LAYOUT == QF_LAYOUT_ROWMAJOR) {
+    src = w + n * ldw + c * 16;
+  } else {
+    const int64_t tile = n / kTileN;
+    const int lane = (c & 3) * 16 + (int)(n % kTileN);
+    src = w + ((tile * ksteps + (c >> 2)) * kWave + lane) * 16;
+  }
+  bf16x8_t a0, a1;
+  dequant16(*reinterpret_cast<const u32x4_t*>(src), a0, a1);
+  u32x4_t* dst = reinterpret_cast<u32x4_t*>(out + r * ldo + c * 16);
+  dst[0] = __builtin_bit_cast(u32x4_t, a0);
+  dst[1] = __builtin_bit_cast(u32x4_t, a1);
+}
+
+// ---------------------------------------------------------------------------------------------
 // Draft-head per-row int8 quantiser (plugin/qwen_fastpath/patches.py:139-147).  One workgroup per
 // row.  s = max(amax, 1e-8) * fl(1/127): the reference divides a CUDA tensor by the Python scalar
 // 127.0, which PyTorch evaluates as a multiply by the fp32 reciprocal; w / s is an IEEE division.
@@ -1209,6 +1239,27 @@ int qf_w8a16_unpack(const int8_t* w_tiled, int8_t* w_rowmajor, int64_t ldw, int 
   const int64_t blocks = (pieces + 255) / 256;
   hipLaunchKernelGGL(repack_kernel<true>, dim3((unsigned)blocks), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), w_tiled, w_rowmajor, ldw, N, ksteps, pieces);
+  return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
+}
+
+int qf_w8a16_dequant_bf16(const int8_t* w, int64_t ldw, int layout, int N, int K, int n0, int rows, uint16_t* out,
+                          int64_t ldo, void* stream) {
+  if (w == nullptr || out == nullptr || N < 1 || K < 1 || rows < 1 || n0 < 0 || (int64_t)n0 + rows > N || ldo < K)
+    return QF_ERR_INVALID_ARG;
+  if (layout != QF_LAYOUT_ROWMAJOR && layout != QF_LAYOUT_TILED) return QF_ERR_INVALID_ARG;
+  if (layout == QF_LAYOUT_ROWMAJOR && ldw < K) return QF_ERR_INVALID_ARG;
+  if (K % QF_W8A16_K_ALIGN || ldo % 8 || !aligned16(w) || !aligned16(out)) return QF_ERR_UNSUPPORTED;
+  if (layout == QF_LAYOUT_ROWMAJOR && ldw % 16) return QF_ERR_UNSUPPORTED;
+  const int ksteps = K / kStepK;
+  const int64_t pieces = (int64_t)rows * ksteps * 4;
+  const int64_t blocks = (pieces + 255) / 256;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (layout == QF_LAYOUT_ROWMAJOR)
+    hipLaunchKernelGGL(dequant_bf16_kernel<QF_LAYOUT_ROWMAJOR>, dim3((unsigned)blocks), dim3(256), 0, s, w, ldw, ksteps,
+                       n0, pieces, out, ldo);
+  else
+    hipLaunchKernelGGL(dequant_bf16_kernel<QF_LAYOUT_TILED>, dim3((unsigned)blocks), dim3(256), 0, s, w, ldw, ksteps, n0,
+                       pieces, out, ldo);
   return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
 }
 

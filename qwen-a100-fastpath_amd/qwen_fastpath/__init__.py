@@ -13,7 +13,9 @@ accepted and ignored.
 import logging
 import os
 
-from .w8a16 import AUTO, ROWMAJOR, SMALL_M, TILED, W8A16Config, from_tiled, pick_config, resolve_config, to_tiled, w8a16_mm  # noqa: F401
+from .w8a16 import (  # noqa: F401
+    AUTO, ROWMAJOR, SMALL_M, TILED, W8A16Config, dequant_bf16, from_tiled, pick_config, resolve_config, tiled_numel,
+    to_tiled, w8a16_mm, w8a16_mm_prefill)
 from .patches import (  # noqa: F401
     Int8Head,
     W8A16LinearMethod,
@@ -24,6 +26,7 @@ from .patches import (  # noqa: F401
     patch_int8_linear,
     qf_int8_linear,
     quantize_lm_head,
+    repack_layer_weight,
     top_tokens,
     w8a8_reference,
 )

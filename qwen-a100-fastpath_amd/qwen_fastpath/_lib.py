@@ -41,6 +41,7 @@ EXPORTS = (
     "qf_w8a16_tiled_bytes",
     "qf_w8a16_repack",
     "qf_w8a16_unpack",
+    "qf_w8a16_dequant_bf16",
     "qf_quantize_rows_int8",
     "qf_argmax_rows_bf16",
     "qf_read_probe",
@@ -113,6 +114,8 @@ def load() -> ctypes.CDLL:
     L.qf_w8a16_repack.restype = i32
     L.qf_w8a16_unpack.argtypes = [p, p, i64, i32, i32, p]
     L.qf_w8a16_unpack.restype = i32
+    L.qf_w8a16_dequant_bf16.argtypes = [p, i64, i32, i32, i32, i32, i32, p, i64, p]
+    L.qf_w8a16_dequant_bf16.restype = i32
     L.qf_quantize_rows_int8.argtypes = [p, i64, p, p, i32, i32, p]
     L.qf_quantize_rows_int8.restype = i32
     L.qf_argmax_rows_bf16.argtypes = [p, i64, i32, i32, i32, i64, p, p]

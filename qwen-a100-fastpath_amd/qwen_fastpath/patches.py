@@ -22,7 +22,7 @@ from typing import Callable, NamedTuple, Optional
 import torch
 
 from . import _lib as L
-from .w8a16 import ROWMAJOR, SMALL_M, TILED, pick_config, to_tiled, w8a16_mm
+from .w8a16 import ROWMAJOR, SMALL_M, TILED, pick_config, to_tiled, w8a16_mm, w8a16_mm_prefill
 
 logger = logging.getLogger("vllm.qwen_fastpath")
 
@@ -72,14 +72,22 @@ def w8a8_reference(x2: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, bias:
 
 
 _fallback_impl: Optional[Callable] = None
+TILED_SLICE_MAX_M = 192
 
 
 def _fallback(x2, w_q, w_s, bias, out_dtype, layout):
     if layout == TILED:
-        # The permuted image is readable only by this library's kernel: run it over 16-row slices.
-        ys = [w8a16_mm(x2[i:i + SMALL_M], w_q, w_s.reshape(-1), None, out_dtype, layout)
-              for i in range(0, x2.shape[0], SMALL_M)]
-        y = torch.cat(ys, dim=0)
+        # No W8A8 library kernel reads the permuted image.  Up to TILED_SLICE_MAX_M rows the decode
+        # kernel runs over 16-row slices (each re-reads the weights); above, the weights are widened
+        # to bf16 chunk by chunk for a library bf16 GEMM (fp32 accumulation, scale after the K
+        # reduction), whose fixed cost is one full widening pass (gate_up: 168 / 622 us for slices
+        # at M = 64 / 256 against 366 / 504 us).
+        if x2.shape[0] <= TILED_SLICE_MAX_M:
+            ys = [w8a16_mm(x2[i:i + SMALL_M], w_q, w_s.reshape(-1), None, out_dtype, layout)
+                  for i in range(0, x2.shape[0], SMALL_M)]
+            y = torch.cat(ys, dim=0)
+        else:
+            y = w8a16_mm_prefill(x2.contiguous(), w_q, w_s, out_dtype, TILED)
         return y if bias is None else y + bias
     global _fallback_impl
     if _fallback_impl is None:
@@ -171,9 +179,51 @@ def _import_attr(path: str):
     return getattr(importlib.import_module(mod), attr)
 
 
-def patch_int8_linear(kernel_cls=None) -> bool:
+def tiled_layout_requested() -> bool:
+    """QWEN_FAST_LINEAR_LAYOUT=tiled: repack W8A8 linear weights into the TILED image at load time."""
+    return os.environ.get("QWEN_FAST_LINEAR_LAYOUT", "rowmajor").strip().lower() == "tiled"
+
+
+def repack_layer_weight(layer) -> bool:
+    """Replace a dynamic-per-token int8 layer's [K, N] (stride (1, K)) weight by its TILED image, in
+    place of the row-major copy (one weight copy is kept), and tag the layer.  Returns False and
+    leaves the layer unchanged when it is not an eligible int8 layer."""
+    w = getattr(layer, "weight", None)
+    if getattr(layer, "_qf_layout", ROWMAJOR) == TILED:
+        return True
+    if w is None or w.dtype != torch.int8 or w.dim() != 2 or not w.is_cuda or w.stride(0) != 1:
+        return False
+    if any(getattr(layer, n, None) is not None for n in ("input_scale", "input_zero_point", "azp_adj")):
+        return False
+    K, N = w.shape
+    if pick_config(N, K, TILED) is None:
+        return False
+    img = to_tiled(w.detach())
+    layer.weight = torch.nn.Parameter(img, requires_grad=False)
+    layer._qf_layout = TILED
+    return True
+
+
+def make_process_weights_after_loading(orig: Callable) -> Callable:
+    """Wrap a kernel class's ``process_weights_after_loading(self, layer)`` so that, once the
+    original has laid the int8 weight out as [K, N] column-major (the CUTLASS view), the weight is
+    repacked into the TILED image.  Rows marked "next" for the weight-load path: the reference
+    streams the checkpoint layout as is (plugin/qwen_fastpath/w8a16.py:1-7)."""
+
+    def process_weights_after_loading(self, layer):
+        orig(self, layer)
+        repack_layer_weight(layer)
+
+    process_weights_after_loading._qwen_fastpath = True
+    return process_weights_after_loading
+
+
+def patch_int8_linear(kernel_cls=None, tiled: Optional[bool] = None) -> bool:
     """Install the W8A16 decode path on ``kernel_cls`` (default: vLLM's int8 scaled-mm kernel
-    classes).  Idempotent (patches.py:80-82).  Returns False when no class could be patched."""
+    classes).  Idempotent (patches.py:80-82).  Returns False when no class could be patched.
+    With ``tiled`` (default: QWEN_FAST_LINEAR_LAYOUT=tiled) the weights are also repacked into the
+    TILED image after loading; M > 16 calls on such layers run the W8A16 kernel over 16-row slices."""
+    tiled = tiled_layout_requested() if tiled is None else bool(tiled)
     classes = [kernel_cls] if kernel_cls is not None else []
     if kernel_cls is None:
         for path in VLLM_INT8_KERNEL_CLASSES:
@@ -187,9 +237,11 @@ def patch_int8_linear(kernel_cls=None) -> bool:
         return False
     for cls in classes:
         orig = cls.apply_weights
-        if getattr(orig, "_qwen_fastpath", False):
-            continue
-        cls.apply_weights = make_apply_weights(orig)
+        if not getattr(orig, "_qwen_fastpath", False):
+            cls.apply_weights = make_apply_weights(orig)
+        pw = getattr(cls, "process_weights_after_loading", None)
+        if tiled and pw is not None and not getattr(pw, "_qwen_fastpath", False):
+            cls.process_weights_after_loading = make_process_weights_after_loading(pw)
     logger.info("qwen_fastpath: W8A16 decode path for W8A8-int8 linears (M <= %d), W8A8 above", SMALL_M)
     return True
 

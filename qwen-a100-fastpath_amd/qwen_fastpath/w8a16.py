@@ -205,3 +205,49 @@ def from_tiled(w_tiled: torch.Tensor, N: int, K: int) -> torch.Tensor:
     stream = torch.cuda.current_stream(w_tiled.device).cuda_stream
     L.check(L.load().qf_w8a16_unpack(w_tiled.data_ptr(), out.data_ptr(), K, N, K, stream), "qf_w8a16_unpack")
     return out.t()
+
+
+# ------------------------------------------------------------------------------------------------
+# M beyond the decode widths (prefill) on weights this library laid out
+# ------------------------------------------------------------------------------------------------
+
+PREFILL_CHUNK_ROWS = 8192
+
+
+def dequant_bf16(w: torch.Tensor, N: int, K: int, layout: int = ROWMAJOR, n0: int = 0, rows: int | None = None,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """Exact bf16 copy [rows, K] of weight rows [n0, n0 + rows) (no scale), from a [K, N] stride-(1, K)
+    view or from the TILED image."""
+    rows = N - n0 if rows is None else rows
+    ldw = _weight_geometry(w, N, K, layout)
+    if out is None:
+        out = torch.empty((rows, K), dtype=torch.bfloat16, device=w.device)
+    if out.dtype != torch.bfloat16 or out.dim() != 2 or out.shape[0] < rows or out.shape[1] < K or out.stride(1) != 1:
+        raise ValueError("out must be a bf16 [>= rows, >= K] matrix with unit column stride")
+    stream = torch.cuda.current_stream(w.device).cuda_stream
+    L.check(L.load().qf_w8a16_dequant_bf16(w.data_ptr(), ldw, layout, N, K, n0, rows, out.data_ptr(), out.stride(0),
+                                          stream), "qf_w8a16_dequant_bf16")
+    return out
+
+
+def w8a16_mm_prefill(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, out_dtype: torch.dtype,
+                     layout: int = TILED, chunk_rows: int = PREFILL_CHUNK_ROWS) -> torch.Tensor:
+    """y[M, N] = (x @ W^T) * w_scale for any M, the same product as w8a16_mm: the int8 weights are
+    widened to bf16 exactly, chunk_rows output channels at a time, multiplied by a library bf16 GEMM
+    with fp32 accumulation (hipBLASLt through torch.mm), and scaled after the K reduction, then
+    rounded to out_dtype.  This serves M > 16 on weights kept in the TILED layout; the reference sends
+    M > 16 to CUTLASS W8A8 on the checkpoint layout (plugin/qwen_fastpath/patches.py:99-100)."""
+    if x.dim() != 2 or x.dtype != torch.bfloat16:
+        raise TypeError("x must be a 2-D bf16 tensor")
+    M, K = x.shape
+    N = w_scale.numel()
+    s = w_scale.reshape(-1).float()
+    y = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    rows = min(chunk_rows, N)
+    wb = torch.empty((rows, K), dtype=torch.bfloat16, device=x.device)
+    for n0 in range(0, N, rows):
+        r = min(rows, N - n0)
+        dequant_bf16(w, N, K, layout, n0, r, wb)
+        y32 = torch.mm(x, wb[:r].t(), out_dtype=torch.float32)
+        y[:, n0:n0 + r] = (y32 * s[n0:n0 + r]).to(out_dtype)
+    return y

@@ -203,3 +203,35 @@ def test_top_tokens_row_split(oracle, M, N, num_pad):
     for _ in range(2):  # the arrival counters are back at zero for the next call
         ids = qf.top_tokens(logits, num_pad, 5).cpu().numpy()
         assert np.array_equal(ids, oracle.argmax_rows(bits, N - num_pad, 5))
+
+
+def test_load_time_tiled_repack(oracle):
+    """QWEN_FAST_LINEAR_LAYOUT=tiled: after the kernel class's own process_weights_after_loading has
+    laid the checkpoint's [N, K] weight out as the [K, N] column-major view, the weight is replaced by
+    its TILED image (one copy); decode calls and M > 16 calls (16-row slices) both stay correct."""
+    class Kernel:  # stand-in for vLLM's int8 scaled-mm kernel class
+        def process_weights_after_loading(self, layer):
+            layer.weight = torch.nn.Parameter(layer.weight.t(), requires_grad=False)
+
+        def _get_layer_params(self, layer):
+            return layer.weight, layer.weight_scale, layer.input_scale, None, None
+
+        def apply_weights(self, layer, x, bias=None):
+            raise AssertionError("the original path must not run for a dynamic int8 layer")
+
+    assert P.patch_int8_linear(Kernel, tiled=True)
+    M, N, K = 5, 1000, 2048
+    inp = oracle.gen_inputs(M, N, K, seed=8)
+    layer = _Layer(torch.from_numpy(inp.w).to(DEV), torch.from_numpy(inp.s).to(DEV))
+    Kernel().process_weights_after_loading(layer)
+    assert layer._qf_layout == qf.TILED and layer.weight.numel() == qf.tiled_numel(N, K)
+    x = to_dev_bf16(inp.x, DEV)
+    y = Kernel().apply_weights(layer, x)
+    torch.cuda.synchronize()
+    assert oracle.check_w8a16(bf16_bits(y), inp.x, inp.w, inp.s).ok
+    rng = np.random.default_rng(9)
+    x20 = oracle.bf16_from_f64(rng.standard_normal((20, K)))
+    y20 = Kernel().apply_weights(layer, to_dev_bf16(x20, DEV))
+    torch.cuda.synchronize()
+    assert y20.shape == (20, N) and oracle.check_w8a16(bf16_bits(y20), x20, inp.w, inp.s).ok
+    assert not qf.repack_layer_weight(_Layer(torch.zeros(4, 4, dtype=torch.float32, device=DEV), None))
