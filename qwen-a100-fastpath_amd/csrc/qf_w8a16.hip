@@ -1072,6 +1072,18 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
     if ((size_t)workgroups(*c, N) * 4 > QF_W8A16_COUNTER_BYTES) c->reduce = 1;
     return validate_config(M, N, K, layout, *c) == QF_OK;
   }
+  if (M >= 12) {
+    // Wide M, narrow N: the x slice of a 5120-k row set is 10 KiB per token, so K is split at least
+    // three ways (at most 48 k-steps a split) and the splits are summed by the second-pass kernel
+    // (M = 16: qkv 14.4 us, o_proj 13.7 us, down 21.9 us against 21.0, 18.5 and 35.6 us).
+    c->split_k = ceil_div(ksteps, 48);
+    if (c->split_k < 3) c->split_k = 3;
+    if (c->split_k > ksteps) c->split_k = ksteps;
+    c->k_waves = (c->split_k <= 3 && ksteps / c->split_k >= 40) ? 2 : 1;  // o_proj: 2; qkv, down: 1
+    c->reduce = 1;
+    while (lds_bytes(*c, M, ksteps) > kMaxLds && c->split_k < ksteps) ++c->split_k;
+    return validate_config(M, N, K, layout, *c) == QF_OK;
+  }
   // Narrow M at 1..2 tokens: 4-wavefront workgroups (gate_up M = 1: 30.4 us against 35.1 us).
   if (M <= 2) c->waves = 4;
   c->split_k = ceil_div(ksteps, 128);
