@@ -1045,20 +1045,25 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
   c->waves = 8;
   c->reduce = 0;
   const int ksteps = K / kStepK;
-  if (layout == QF_LAYOUT_ROWMAJOR && M <= 2) {
-    // Row-major weights at M <= 2: the GEMV kernel's contiguous 1 KiB row reads win over the
-    // MFMA tiles' 64-byte row pieces (gate_up, M = 1: 30.5 us against 46 us).
+  const bool wide_n = round_up16(N) / (kTileN * 16) >= 128;  // >= 128 groups of 256 rows
+  if (layout == QF_LAYOUT_ROWMAJOR && (M == 1 || (M == 2 && wide_n))) {
+    // Row-major weights at M = 1, and at M = 2 on wide N: the GEMV kernel's contiguous 1 KiB row
+    // reads win over the MFMA tiles' 64-byte row pieces (M = 1: gate_up 30.9 us against 46 us, down
+    // 17.7 us against 21.0 us; at M = 2 narrow N the MFMA tiles are level or ahead).
     c->kernel = QF_KERNEL_GEMV;
     c->waves = 4;
     c->k_waves = 1;
-    c->tiles_per_wave = 4;
+    c->tiles_per_wave = 2;  // rows per wavefront (gate_up M = 2: 37.6 us against 41.6 us with 4)
     c->load_hint = 1;
     c->split_k = 1;
     c->reduce = 1;
     while (lds_bytes(*c, M, ksteps) > kMaxLds && c->split_k < ksteps) ++c->split_k;
     return validate_config(M, N, K, layout, *c) == QF_OK;
   }
-  if (M >= 8 && round_up16(N) / (kTileN * 16) >= 128) {  // wide N only: >= 128 workgroups of 256 rows
+  // wide N only (>= 128 workgroups of 256 rows), and only on the TILED layout, whose 1 KiB fragments
+  // stay contiguous however many tiles a wavefront holds (row-major gate_up at M = 8: 63 us with this
+  // shape against 42 us without)
+  if (M >= 8 && layout == QF_LAYOUT_TILED && wide_n) {
     // Wide M and N: the staged x slice grows with M, so a workgroup covers more weight rows per
     // staged byte -- 8 tile groups of 2 tiles, each wavefront over the whole K range of its split
     // (gate_up: M = 8 35.0 us, M = 12 36.5 us against 44 and 48 us with the M = 5 shape); from
@@ -1072,6 +1077,36 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
     if ((size_t)workgroups(*c, N) * 4 > QF_W8A16_COUNTER_BYTES) c->reduce = 1;
     return validate_config(M, N, K, layout, *c) == QF_OK;
   }
+  if (layout == QF_LAYOUT_ROWMAJOR && (wide_n || M < 12)) {
+    // Row-major weights: a wavefront's 16 rows are read as 64-byte row pieces, so workgroups are
+    // kept at 4 wavefronts with one k-slice each and more of them run: wide N at M >= 8 splits K
+    // 2 ways (3 from M = 12) with the second-pass sum (gate_up M = 8: 48.8 us, M = 16: 51.6 us,
+    // against 53.6 and 57.6 us with the tiled-layout shape); narrow N splits K 3 ways once fewer
+    // than 160 workgroups would run or M >= 8, summed in-kernel (M = 5: o_proj 11.7 us, down
+    // 22.2 us, qkv 13.7 us unsplit, against 14.2, 25.9 and 14.6 us).
+    if (wide_n && M < 8) {
+      // M = 3..7 on wide N: the tiled-layout shape below measured best (gate_up M = 5: 43.4 us).
+    } else {
+      c->waves = 4;
+      c->k_waves = 1;
+      if (wide_n) {
+        c->split_k = M >= 12 ? 3 : 2;
+        c->k_waves = M >= 12 ? 1 : 2;
+        c->depth = M >= 12 ? 8 : 4;
+        c->reduce = 1;
+      } else {
+        const int wgs = ceil_div(round_up16(N) / kTileN, c->waves);
+        c->split_k = (wgs >= 160 && M < 8) ? 1 : 3;
+        c->reduce = 0;
+      }
+      if (c->split_k > ksteps) c->split_k = ksteps;
+      if (ksteps / c->split_k < c->k_waves) c->k_waves = 1;
+      if (!wide_n && ksteps / c->split_k >= 64) c->depth = 8;  // down: 21.2 us against 21.8 at M = 2
+      while (lds_bytes(*c, M, ksteps) > kMaxLds && c->split_k < ksteps) ++c->split_k;
+      if (c->split_k > 1 && (size_t)workgroups(*c, N) * 4 > QF_W8A16_COUNTER_BYTES) c->reduce = 1;
+      return validate_config(M, N, K, layout, *c) == QF_OK;
+    }
+  }
   if (M >= 12) {
     // Wide M, narrow N: the x slice of a 5120-k row set is 10 KiB per token, so K is split at least
     // three ways (at most 48 k-steps a split) and the splits are summed by the second-pass kernel
@@ -1080,6 +1115,10 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
     if (c->split_k < 3) c->split_k = 3;
     if (c->split_k > ksteps) c->split_k = ksteps;
     c->k_waves = (c->split_k <= 3 && ksteps / c->split_k >= 40) ? 2 : 1;  // o_proj: 2; qkv, down: 1
+    if (layout == QF_LAYOUT_ROWMAJOR && c->k_waves == 2) {
+      c->waves = 4;  // row-major o_proj M = 16: 14.3 us against 15.3 us
+      c->k_waves = 1;
+    }
     c->reduce = 1;
     while (lds_bytes(*c, M, ksteps) > kMaxLds && c->split_k < ksteps) ++c->split_k;
     return validate_config(M, N, K, layout, *c) == QF_OK;
