@@ -207,8 +207,8 @@ def repack_layer_weight(layer) -> bool:
 def make_process_weights_after_loading(orig: Callable) -> Callable:
     """Wrap a kernel class's ``process_weights_after_loading(self, layer)`` so that, once the
     original has laid the int8 weight out as [K, N] column-major (the CUTLASS view), the weight is
-    repacked into the TILED image.  Rows marked "next" for the weight-load path: the reference
-    streams the checkpoint layout as is (plugin/qwen_fastpath/w8a16.py:1-7)."""
+    repacked into the TILED image.  No reference counterpart: the reference streams the checkpoint
+    layout as is (plugin/qwen_fastpath/w8a16.py:1-7)."""
 
     def process_weights_after_loading(self, layer):
         orig(self, layer)
@@ -222,7 +222,8 @@ def patch_int8_linear(kernel_cls=None, tiled: Optional[bool] = None) -> bool:
     """Install the W8A16 decode path on ``kernel_cls`` (default: vLLM's int8 scaled-mm kernel
     classes).  Idempotent (patches.py:80-82).  Returns False when no class could be patched.
     With ``tiled`` (default: QWEN_FAST_LINEAR_LAYOUT=tiled) the weights are also repacked into the
-    TILED image after loading; M > 16 calls on such layers run the W8A16 kernel over 16-row slices."""
+    TILED image after loading; M > 16 calls on such layers run the W8A16 kernel over 16-row slices
+    up to TILED_SLICE_MAX_M rows, and a bf16 library GEMM over exactly widened weights above."""
     tiled = tiled_layout_requested() if tiled is None else bool(tiled)
     classes = [kernel_cls] if kernel_cls is not None else []
     if kernel_cls is None:
