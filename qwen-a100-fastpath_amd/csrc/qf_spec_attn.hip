@@ -1,0 +1,585 @@
+// qf_spec_attn.hip — split-KV, GQA-packed verification attention for MI355X (gfx950).
+//
+// Causal attention for a uniform speculative-decode batch (every request has q_len query tokens)
+// over a paged bf16 KV cache; the C ABI is declared in include/qf_spec_attn.h.  Same decomposition
+// as the reference (plugin/qwen_fastpath/spec_attn.py:1-10): the cached prefix, which every query of a
+// request sees in full, is split across workgroups that stream each kv head once for all the
+// q_len * G query rows sharing it; a second kernel attends this step's q_len positions causally and
+// merges everything by log-sum-exp.  The kernels themselves are designed for CDNA4:
+//
+//   prefix kernel, one 256-thread workgroup per (split, request, kv head):
+//   * K and V rows of a 32-position stage are copied global -> LDS with 16-byte direct-to-LDS loads
+//     (no VGPR staging), 16-byte pieces XOR-swizzled per row so that the MFMA fragment reads below
+//     are free of bank conflicts; a ring of kRing stages keeps kRing - 2 stages in flight while a
+//     stage is computed, with one barrier per stage.
+//   * S^T = K . Q^T on v_mfma_f32_16x16x32_bf16 with K as the A operand (16 positions x 32 d) and the
+//     packed query rows as B (16 rows), so each lane's accumulator holds 4 positions of ONE row: the
+//     online softmax needs only two cross-lane steps per row, and the probabilities in a lane are
+//     already the B fragment of the next product.
+//   * O^T = V^T . P^T on the same instruction, with the 32 positions of a stage ordered so that the
+//     B fragment is the lane's own 8 probabilities; V^T fragments are gathered from the LDS rows.
+//   * Every wavefront computes the scores of all rows (cheap at 2M flop/byte) and accumulates its own
+//     quarter of the head dimension, so wavefronts never exchange softmax state.
+//   suffix/combine kernel, one 256-thread workgroup per (token, head): the row's partials are merged
+//   by 4 thread groups, the in-flight positions by the first, then the groups by LDS.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <mutex>
+#include <unordered_set>
+
+#include "qf_spec_attn.h"
+
+namespace qfa {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef const void __attribute__((address_space(1)))* gptr_t;
+typedef void __attribute__((address_space(3)))* lptr_t;
+
+constexpr int kWave = 64;
+constexpr int kWaves = 4;
+constexpr int kThreads = kWave * kWaves;
+constexpr int kKeyBlock = QF_SPEC_ATTN_KEY_BLOCK;  // positions per stage
+constexpr int kMaxRows = QF_SPEC_ATTN_MAX_ROWS;
+constexpr int kTablePages = 1024;  // block-table entries a prefix workgroup holds in LDS at once
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr size_t kMaxDynLds = 160 * 1024 - 8 * 1024;  // gfx950 LDS per workgroup, less the static arrays
+constexpr size_t kDefaultLds = 64 * 1024;
+
+struct AttnArgs {
+  const uint16_t* q;
+  int64_t sq_t, sq_h;
+  const uint16_t* kc;
+  int64_t sk_b, sk_t, sk_h;
+  const uint16_t* vc;
+  int64_t sv_b, sv_t, sv_h;
+  const int32_t* bt;
+  int64_t sbt;
+  const int32_t* seq_lens;
+  uint16_t* out;
+  int64_t so_t, so_h;
+  float* o_part;    // [B][HKV][S][R][D]
+  float* lse_part;  // [B][HKV][S][R]
+  int B, Q, H, HKV, G, R, page, splits, min_chunk;
+  float qk_scale;  // softmax scale * log2(e): scores are kept in base 2
+};
+
+// Positions per prefix split (the reference's split arithmetic, spec_attn.py:38-40, with this
+// kernel's key block): both kernels derive it from the sequence length alone.
+__device__ __forceinline__ int split_chunk(int prefix, int splits, int min_chunk) {
+  int c = (prefix + splits - 1) / splits;
+  c = c > min_chunk ? c : min_chunk;
+  return (c + kKeyBlock - 1) / kKeyBlock * kKeyBlock;
+}
+
+// Workgroup barrier for the copy ring.  Each wavefront has already waited for its own copies of the
+// stage (wait_vmcnt); no release fence is used, because at workgroup scope it would also wait for
+// the copies of later stages, which are LDS writes still in flight.  The acquire fence keeps the
+// stage's LDS reads (and the next copies into the ring) after the barrier.
+__device__ __forceinline__ void ring_barrier() {
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// s_waitcnt with vmcnt = n (0..63) and the other counters unconstrained.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+__device__ __forceinline__ float wave_max_q(float v) {  // over the 4 lanes l, l^16, l^32, l^48
+  v = fmaxf(v, __shfl_xor(v, 16));
+  return fmaxf(v, __shfl_xor(v, 32));
+}
+__device__ __forceinline__ float wave_sum_q(float v) {
+  v += __shfl_xor(v, 16);
+  return v + __shfl_xor(v, 32);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// bf16 <-> fp32 on 32-bit words (element order: low half first)
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ f32x4_t bf16x4_to_f32(u32x2_t w) {
+  return f32x4_t{bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y)};
+}
+// two fp32 -> two bf16 (round to nearest even), `a` in the low half
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)a) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)b) << 16);
+}
+
+// Geometry of the prefix kernel for head size D.
+template <int D>
+struct Geo {
+  static constexpr int kRowBytes = 2 * D;                         // one cache row (bf16)
+  static constexpr int kChunks = D / 8;                           // 16-byte pieces per row
+  static constexpr int kStageBytes = kKeyBlock * kRowBytes;       // one tensor, one stage
+  static constexpr int kCopies = kStageBytes / (kWaves * 1024);   // 1 KiB copies per wavefront per tensor
+  static constexpr int kRowsPerCopy = 1024 / kRowBytes;
+  static constexpr int kRing = 4;                                 // stages resident in LDS
+  static constexpr int kLds = kRing * 2 * kStageBytes;  // dynamic LDS (the block-table window is static)
+  static constexpr int kDTiles = D / 16 / kWaves;                 // 16-wide d tiles per wavefront
+  static constexpr int kDChunks = D / 32;                         // 32-d MFMA steps of a score
+  static_assert(kCopies >= 1 && kStageBytes % (kWaves * 1024) == 0, "stage must split into wave copies");
+  static_assert(kDTiles >= 1, "head size too small");
+  static_assert(kLds + kTablePages * 4 <= kMaxDynLds + 8 * 1024 - 256, "LDS budget");
+  // The 16-byte piece of row n that lands at LDS position p is piece p ^ swz(n): 16 consecutive rows
+  // read at one piece index then hit 16 distinct bank groups.
+  __device__ static __forceinline__ int swz(int n) { return kChunks >= 16 ? (n & 15) : ((n >> 1) & 7); }
+};
+
+// One wavefront per SIMD (128 KiB of LDS per workgroup at D = 256): the whole register file is usable.
+template <int D, int RT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void spec_prefix_kernel(
+    AttnArgs a) {
+  using Gm = Geo<D>;
+  constexpr int kRing = Gm::kRing;
+  constexpr int NJ = Gm::kCopies;
+  extern __shared__ __align__(16) uint8_t lds[];
+  __shared__ int32_t tbl[kTablePages];  // block-table entries of the current window
+
+  const int split = blockIdx.x;
+  const int b = blockIdx.y / a.HKV;
+  const int hkv = blockIdx.y - b * a.HKV;
+  const int seq = a.seq_lens[b];
+  const int prefix = seq - a.Q > 0 ? seq - a.Q : 0;
+  const int chunk = split_chunk(prefix, a.splits, a.min_chunk);
+  const int start = split * chunk;
+  if (start >= prefix) return;  // uniform: the whole workgroup leaves
+  const int end = min(start + chunk, prefix);
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int l16 = lane & 15;
+  const int qg = lane >> 4;
+
+  // ---- packed query rows: B fragments of the score product (rows >= R repeat row R - 1) ----
+  bf16x8_t qf[RT][Gm::kDChunks];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int r = min(rt * 16 + l16, a.R - 1);
+    const int qi = r / a.G;
+    const int h = hkv * a.G + (r - qi * a.G);
+    const uint16_t* qrow = a.q + (int64_t)(b * a.Q + qi) * a.sq_t + (int64_t)h * a.sq_h + qg * 8;
+#pragma unroll
+    for (int c = 0; c < Gm::kDChunks; ++c) qf[rt][c] = *reinterpret_cast<const bf16x8_t*>(qrow + c * 32);
+  }
+
+  // ---- copy schedule: per stage, wavefront `wave` moves NJ KiB of K and NJ KiB of V ----
+  const int32_t* bt_row = a.bt + (int64_t)b * a.sbt;
+  const uint16_t* kbase = a.kc + (int64_t)hkv * a.sk_h;
+  const uint16_t* vbase = a.vc + (int64_t)hkv * a.sv_h;
+  int row_of[NJ], piece_of[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int t = (wave * NJ + j) * Gm::kRowsPerCopy + lane / Gm::kChunks;
+    row_of[j] = t;
+    piece_of[j] = (lane % Gm::kChunks) ^ Gm::swz(t);
+  }
+
+  float m_run[RT], l_run[RT];
+  f32x4_t o_acc[RT][Gm::kDTiles];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    m_run[rt] = -__builtin_inff();
+    l_run[rt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < Gm::kDTiles; ++dt) o_acc[rt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // The split is walked in windows of at most kTablePages pages (one window unless the split spans
+  // more pages than that); each window's block-table entries are read into LDS first, so inside the
+  // pipelined loop the only vector-memory instructions are the stage copies and the explicit vmcnt
+  // waits below count exactly those.
+  for (int wstart = start; wstart < end;) {
+    const int p0 = wstart / a.page;
+    const int wend = min(end, (p0 + kTablePages) * a.page);
+    const int npg = (wend - 1) / a.page - p0 + 1;
+    for (int i = threadIdx.x; i < npg; i += kThreads) tbl[i] = bt_row[p0 + i];
+    wait_vmcnt<0>();  // the query loads too: nothing may be left in flight before the exact waits below
+    __syncthreads();
+    const int nst = (wend - wstart + kKeyBlock - 1) / kKeyBlock;
+
+    auto copy_stage = [&](int st) {
+      uint8_t* slot = lds + (st % kRing) * 2 * Gm::kStageBytes;
+      const int sbase = wstart + st * kKeyBlock;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int pos = min(sbase + row_of[j], wend - 1);  // rows past the window repeat its last position
+        const int pg = pos / a.page;
+        const int64_t blk = tbl[pg - p0];
+        const int off = pos - pg * a.page;
+        const int copy = wave * NJ + j;
+        const int64_t kel = blk * a.sk_b + (int64_t)off * a.sk_t + piece_of[j] * 8;
+        const int64_t vel = blk * a.sv_b + (int64_t)off * a.sv_t + piece_of[j] * 8;
+        __builtin_amdgcn_global_load_lds((gptr_t)(kbase + kel), (lptr_t)(slot + copy * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((gptr_t)(vbase + vel), (lptr_t)(slot + Gm::kStageBytes + copy * 1024),
+                                         16, 0, 0);
+      }
+    };
+
+    // prologue: stages 0 .. kRing-2 in flight
+#pragma unroll
+    for (int s = 0; s < kRing - 1; ++s)
+      if (s < nst) copy_stage(s);
+
+    constexpr int kCopiesPerStage = 2 * NJ;  // vector-memory instructions of one stage
+    for (int st = 0; st < nst; ++st) {
+      // Stage st has landed once at most the later issued stages' copies are outstanding.
+      const int after = min(kRing - 2, nst - 1 - st);
+      if (after >= 2) {
+        wait_vmcnt<2 * kCopiesPerStage>();
+      } else if (after == 1) {
+        wait_vmcnt<kCopiesPerStage>();
+      } else {
+        wait_vmcnt<0>();
+      }
+      ring_barrier();
+
+      const uint8_t* ks = lds + (st % kRing) * 2 * Gm::kStageBytes;
+      const uint8_t* vs = ks + Gm::kStageBytes;
+      const int sbase = wstart + st * kKeyBlock;
+
+      // S^T tiles: positions 16 kt + 4 qg + i, row 16 rt + l16
+      f32x4_t sc[2][RT];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < Gm::kDChunks; ++c) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          const int n = kt * 16 + l16;
+          const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(
+              ks + n * Gm::kRowBytes + (((4 * c + qg) ^ Gm::swz(n)) << 4));
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt)
+            sc[kt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[rt][c], sc[kt][rt], 0, 0, 0);
+        }
+      }
+
+      // online softmax in base 2; the lane's 8 probabilities form its B fragment of O^T = V^T P^T
+      bf16x8_t pf[RT];
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        float v[8];
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int pos = sbase + kt * 16 + qg * 4 + i;
+            const float x = pos < wend ? sc[kt][rt][i] * a.qk_scale : -__builtin_inff();
+            v[kt * 4 + i] = x;
+            mx = fmaxf(mx, x);
+          }
+        mx = wave_max_q(mx);
+        const float m_new = fmaxf(m_run[rt], mx);  // finite: every stage holds a valid position
+        const float alpha = fast_exp2(m_run[rt] - m_new);
+        float psum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          v[i] = fast_exp2(v[i] - m_new);
+          psum += v[i];
+        }
+        l_run[rt] = l_run[rt] * alpha + psum;
+        m_run[rt] = m_new;
+#pragma unroll
+        for (int dt = 0; dt < Gm::kDTiles; ++dt) o_acc[rt][dt] *= alpha;
+        pf[rt] = __builtin_bit_cast(bf16x8_t, u32x4_t{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]),
+                                                      pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7])});
+      }
+
+      // O^T += V^T P^T over this wavefront's d tiles.  k slot 8 qg + i holds position
+      // (i < 4 ? 4 qg + i : 16 + 4 qg + i - 4), the positions of the lane's own probabilities.
+#pragma unroll
+      for (int dt = 0; dt < Gm::kDTiles; ++dt) {
+        const int d = (wave * Gm::kDTiles + dt) * 16 + l16;
+        const int dpiece = d >> 3;
+        const int dbyte = (d & 7) * 2;
+        uint32_t h[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int n = (i < 4 ? 0 : 16) + qg * 4 + (i & 3);
+          h[i] = *reinterpret_cast<const uint16_t*>(vs + n * Gm::kRowBytes + ((dpiece ^ Gm::swz(n)) << 4) + dbyte);
+        }
+        const bf16x8_t vf = __builtin_bit_cast(
+            bf16x8_t, u32x4_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)});
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+          o_acc[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[rt], o_acc[rt][dt], 0, 0, 0);
+      }
+
+      // Refill the slot every wavefront finished with before this stage's barrier.
+      if (st + kRing - 1 < nst) copy_stage(st + kRing - 1);
+    }
+    wait_vmcnt<0>();
+    __syncthreads();  // the next window rewrites the table and the ring
+    wstart = wend;
+  }
+
+  // ---- partial output (normalised) and base-2 log-sum-exp of each packed row ----
+  const int64_t part = ((int64_t)blockIdx.y * a.splits + split) * a.R;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const float l_tot = wave_sum_q(l_run[rt]);
+    const float inv = 1.f / l_tot;
+    const int r = rt * 16 + l16;
+    if (r < a.R) {
+      float* orow = a.o_part + (part + r) * D;
+#pragma unroll
+      for (int dt = 0; dt < Gm::kDTiles; ++dt)
+        *reinterpret_cast<f32x4_t*>(orow + (wave * Gm::kDTiles + dt) * 16 + qg * 4) = o_acc[rt][dt] * inv;
+      if (wave == 0 && qg == 0) a.lse_part[part + r] = m_run[rt] + __log2f(l_tot);
+    }
+  }
+}
+
+// One (token, head) row per workgroup: the causal in-flight positions and the active prefix splits,
+// merged by log-sum-exp (the reference's _suffix_combine_kernel, spec_attn.py:78-132).
+template <int D>
+__global__ __launch_bounds__(kThreads) void spec_combine_kernel(AttnArgs a) {
+  constexpr int NQ = D / 4;          // threads per group, 4 d values each
+  constexpr int NGRP = kThreads / NQ;
+  __shared__ float sm_m[NGRP], sm_l[NGRP];
+  __shared__ __align__(16) float sm_acc[NGRP][D];
+
+  const int row = blockIdx.x;
+  const int tok = row / a.H;
+  const int h = row - tok * a.H;
+  const int b = tok / a.Q;
+  const int qi = tok - b * a.Q;
+  const int hkv = h / a.G;
+  const int r = qi * a.G + (h - hkv * a.G);
+  const int grp = threadIdx.x / NQ;
+  const int dq = threadIdx.x - grp * NQ;
+
+  const int seq = a.seq_lens[b];
+  const int prefix = seq - a.Q > 0 ? seq - a.Q : 0;
+  const int chunk = split_chunk(prefix, a.splits, a.min_chunk);
+  const int n_active = prefix > 0 ? (prefix + chunk - 1) / chunk : 0;
+
+  float m = -__builtin_inff(), l = 0.f;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  // merge one part (base-2 log-sum-exp `e`, normalised output `o`) into the running state
+  auto merge = [&](float e, f32x4_t o) {
+    const float mn = fmaxf(m, e);
+    const float c_old = fast_exp2(m - mn);
+    const float w = fast_exp2(e - mn);
+    acc = acc * c_old + o * w;
+    l = l * c_old + w;
+    m = mn;
+  };
+
+  // prefix splits: group grp takes splits grp, grp + NGRP, ...
+  const int64_t part0 = ((int64_t)(b * a.HKV + hkv) * a.splits) * a.R + r;
+  {
+    int sp = grp;
+    for (; sp + 3 * NGRP < n_active; sp += 4 * NGRP) {
+      float e[4];
+      f32x4_t o[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t idx = part0 + (int64_t)(sp + u * NGRP) * a.R;
+        e[u] = a.lse_part[idx];
+        o[u] = *reinterpret_cast<const f32x4_t*>(a.o_part + idx * D + dq * 4);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) merge(e[u], o[u]);
+    }
+    for (; sp < n_active; sp += NGRP) {
+      const int64_t idx = part0 + (int64_t)sp * a.R;
+      merge(a.lse_part[idx], *reinterpret_cast<const f32x4_t*>(a.o_part + idx * D + dq * 4));
+    }
+  }
+
+  // in-flight positions seq - Q .. seq - Q + qi (group 0): each is a part with e = score, o = v
+  if (grp == 0) {
+    const uint16_t* qrow = a.q + (int64_t)tok * a.sq_t + (int64_t)h * a.sq_h + dq * 4;
+    const f32x4_t qv = bf16x4_to_f32(*reinterpret_cast<const u32x2_t*>(qrow));
+    const int32_t* bt_row = a.bt + (int64_t)b * a.sbt;
+    for (int j = 0; j <= qi; ++j) {
+      const int pos = seq - a.Q + j;
+      if (pos < 0) continue;  // uniform across the workgroup
+      const int pg = pos / a.page;
+      const int64_t blk = bt_row[pg];
+      const int off = pos - pg * a.page;
+      const f32x4_t kv = bf16x4_to_f32(*reinterpret_cast<const u32x2_t*>(
+          a.kc + blk * a.sk_b + (int64_t)off * a.sk_t + (int64_t)hkv * a.sk_h + dq * 4));
+      const f32x4_t vv = bf16x4_to_f32(*reinterpret_cast<const u32x2_t*>(
+          a.vc + blk * a.sv_b + (int64_t)off * a.sv_t + (int64_t)hkv * a.sv_h + dq * 4));
+      float dot = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dot += kv[i] * qv[i];
+#pragma unroll
+      for (int off2 = NQ / 2; off2 >= 1; off2 >>= 1) dot += __shfl_xor(dot, off2);
+      merge(dot * a.qk_scale, vv);
+    }
+  }
+
+  if (dq == 0) {
+    sm_m[grp] = m;
+    sm_l[grp] = l;
+  }
+  *reinterpret_cast<f32x4_t*>(&sm_acc[grp][dq * 4]) = acc;
+  __syncthreads();
+  if (grp != 0) return;
+  float mt = -__builtin_inff();
+#pragma unroll
+  for (int g = 0; g < NGRP; ++g) mt = fmaxf(mt, sm_m[g]);
+  f32x4_t at = {0.f, 0.f, 0.f, 0.f};
+  float lt = 0.f;
+  if (mt != -__builtin_inff()) {
+#pragma unroll
+    for (int g = 0; g < NGRP; ++g) {
+      const float w = fast_exp2(sm_m[g] - mt);  // 0 for an empty group
+      at += *reinterpret_cast<const f32x4_t*>(&sm_acc[g][dq * 4]) * w;
+      lt += sm_l[g] * w;
+    }
+  }
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;  // a row that sees no position is written as zeros
+  *reinterpret_cast<u32x2_t*>(a.out + (int64_t)tok * a.so_t + (int64_t)h * a.so_h + dq * 4) =
+      u32x2_t{pack_bf16(at[0] * inv, at[1] * inv), pack_bf16(at[2] * inv, at[3] * inv)};
+}
+
+typedef void (*KernelFn)(AttnArgs);
+
+template <int D>
+KernelFn prefix_fn(int rt) {
+  switch (rt) {
+    case 1: return &spec_prefix_kernel<D, 1>;
+    case 2: return &spec_prefix_kernel<D, 2>;
+    case 3: return &spec_prefix_kernel<D, 3>;
+    case 4: return &spec_prefix_kernel<D, 4>;
+    default: return nullptr;
+  }
+}
+
+std::mutex g_lds_mutex;
+std::unordered_set<const void*> g_lds_raised;
+
+int launch(KernelFn fn, dim3 grid, size_t smem, hipStream_t stream, const AttnArgs& a) {
+  void* args[] = {const_cast<AttnArgs*>(&a)};
+  if (smem > kDefaultLds) {
+    std::lock_guard<std::mutex> lock(g_lds_mutex);
+    const void* key = reinterpret_cast<const void*>(fn);
+    if (g_lds_raised.find(key) == g_lds_raised.end()) {
+      if (hipFuncSetAttribute(key, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxDynLds) != hipSuccess)
+        return QF_ERR_HIP;
+      g_lds_raised.insert(key);
+    }
+  }
+  if (hipLaunchKernel(reinterpret_cast<const void*>(fn), grid, dim3(kThreads), args, smem, stream) != hipSuccess)
+    return QF_ERR_HIP;
+  return QF_OK;
+}
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+size_t workspace_for(int B, int Q, int H, int HKV, int D, int S) {
+  if (B < 1 || Q < 1 || H < 1 || HKV < 1 || H % HKV || D < 1 || S < 1) return 0;
+  const size_t R = (size_t)Q * (H / HKV);
+  const size_t n = (size_t)B * HKV * S * R * (D + 1) * sizeof(float);
+  return (n + 255) / 256 * 256;
+}
+
+}  // namespace qfa
+
+using namespace qfa;
+
+extern "C" {
+
+int qf_spec_attn_abi_version(void) { return QF_SPEC_ATTN_ABI_VERSION; }
+
+size_t qf_spec_attn_workspace_bytes(int num_reqs, int q_len, int num_heads, int num_kv_heads, int head_size,
+                                    int num_splits) {
+  return workspace_for(num_reqs, q_len, num_heads, num_kv_heads, head_size, num_splits);
+}
+
+int qf_spec_attention(const uint16_t* query, int64_t q_stride_tok, int64_t q_stride_head,
+                      const uint16_t* key_cache, int64_t k_stride_block, int64_t k_stride_tok,
+                      int64_t k_stride_head,
+                      const uint16_t* value_cache, int64_t v_stride_block, int64_t v_stride_tok,
+                      int64_t v_stride_head,
+                      const int32_t* block_table, int64_t bt_stride,
+                      const int32_t* seq_lens,
+                      uint16_t* out, int64_t o_stride_tok, int64_t o_stride_head,
+                      int num_reqs, int q_len, int num_heads, int num_kv_heads, int head_size,
+                      int page_size, float scale, int num_splits, int min_chunk,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  if (!query || !key_cache || !value_cache || !block_table || !seq_lens || !out) return QF_ERR_INVALID_ARG;
+  if (num_reqs < 1 || q_len < 1 || num_heads < 1 || num_kv_heads < 1 || page_size < 1 || num_splits < 1 ||
+      num_splits > 65535 || min_chunk < 1 || bt_stride < 0)
+    return QF_ERR_INVALID_ARG;
+  if (!(scale == scale)) return QF_ERR_INVALID_ARG;
+  if (num_heads % num_kv_heads) return QF_ERR_UNSUPPORTED;
+  const int G = num_heads / num_kv_heads;
+  const int R = q_len * G;
+  if (R > kMaxRows || page_size < QF_SPEC_ATTN_MIN_PAGE) return QF_ERR_UNSUPPORTED;
+  if (head_size != 64 && head_size != 128 && head_size != 256) return QF_ERR_UNSUPPORTED;
+  if ((int64_t)num_reqs * num_kv_heads > 65535 || (int64_t)num_reqs * q_len * num_heads > 0x7fffffff)
+    return QF_ERR_UNSUPPORTED;
+  const int64_t strides[] = {q_stride_tok, q_stride_head, k_stride_block, k_stride_tok, k_stride_head,
+                             v_stride_block, v_stride_tok, v_stride_head, o_stride_tok, o_stride_head};
+  for (int64_t s : strides)
+    if (s < 0 || s % 8) return QF_ERR_UNSUPPORTED;
+  if (!aligned16(query) || !aligned16(key_cache) || !aligned16(value_cache) || !aligned16(out))
+    return QF_ERR_UNSUPPORTED;
+  const size_t need = workspace_for(num_reqs, q_len, num_heads, num_kv_heads, head_size, num_splits);
+  if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)) return QF_ERR_WORKSPACE;
+
+  AttnArgs a;
+  a.q = query;
+  a.sq_t = q_stride_tok;
+  a.sq_h = q_stride_head;
+  a.kc = key_cache;
+  a.sk_b = k_stride_block;
+  a.sk_t = k_stride_tok;
+  a.sk_h = k_stride_head;
+  a.vc = value_cache;
+  a.sv_b = v_stride_block;
+  a.sv_t = v_stride_tok;
+  a.sv_h = v_stride_head;
+  a.bt = block_table;
+  a.sbt = bt_stride;
+  a.seq_lens = seq_lens;
+  a.out = out;
+  a.so_t = o_stride_tok;
+  a.so_h = o_stride_head;
+  const size_t n_o = (size_t)num_reqs * num_kv_heads * num_splits * R * head_size;
+  a.o_part = static_cast<float*>(workspace);
+  a.lse_part = a.o_part + n_o;
+  a.B = num_reqs;
+  a.Q = q_len;
+  a.H = num_heads;
+  a.HKV = num_kv_heads;
+  a.G = G;
+  a.R = R;
+  a.page = page_size;
+  a.splits = num_splits;
+  a.min_chunk = min_chunk;
+  a.qk_scale = scale * kLog2e;
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int rt = (R + 15) / 16;
+  KernelFn pre = nullptr, comb = nullptr;
+  size_t lds = 0;
+  switch (head_size) {
+    case 64: pre = prefix_fn<64>(rt); comb = &spec_combine_kernel<64>; lds = Geo<64>::kLds; break;
+    case 128: pre = prefix_fn<128>(rt); comb = &spec_combine_kernel<128>; lds = Geo<128>::kLds; break;
+    default: pre = prefix_fn<256>(rt); comb = &spec_combine_kernel<256>; lds = Geo<256>::kLds; break;
+  }
+  if (pre == nullptr) return QF_ERR_UNSUPPORTED;
+  int st = launch(pre, dim3(num_splits, num_reqs * num_kv_heads), lds, s, a);
+  if (st != QF_OK) return st;
+  return launch(comb, dim3(num_reqs * q_len * num_heads), 0, s, a);
+}
+
+}  // extern "C"

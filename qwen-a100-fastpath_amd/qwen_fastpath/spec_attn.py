@@ -1,0 +1,83 @@
+"""Split-KV, GQA-packed verification attention (QWEN_FAST_ATTN) on MI355X.
+
+``gqa_packed_spec_attention`` has the signature and meaning of the reference's function
+(plugin/qwen_fastpath/spec_attn.py:135-173): causal attention for a uniform decode batch of
+``num_reqs`` requests x ``Q`` query tokens (token b*Q + qi) over a paged KV cache, written into
+``out``.  Query qi of request b attends cached positions [0, seq_lens[b] - Q + qi]; this step's K/V
+must already be in the cache.  The work runs in libqf_spec_attn.so (hand-written HIP for gfx950):
+one launch streams each kv head's cached prefix once for the Q*G query rows sharing it, split across
+workgroups, and a second attends the in-flight positions and merges by log-sum-exp.  Both grids are
+fixed for a batch shape and nothing is read back to the host, so the call can be captured in a HIP
+graph (its split workspace comes from torch's caching allocator, as the reference's does).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _attn_lib as AL
+
+LOG2E = 1.4426950408889634
+
+# Defaults of the reference's call (spec_attn.py:136).  block_n / num_warps / num_stages /
+# combine_warps are Triton launch knobs there; the HIP kernels have fixed shapes and ignore them.
+DEFAULT_NUM_SPLITS = 64
+DEFAULT_MIN_CHUNK = 128
+
+
+def _check_bf16_rows(t: torch.Tensor, name: str):
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16, got {t.dtype}")
+    if t.stride(-1) != 1:
+        raise ValueError(f"{name} must be contiguous in its last dimension")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+
+
+def supported(query: torch.Tensor, key_cache: torch.Tensor, Q: int, num_kv_heads: int) -> bool:
+    """Shapes the library serves: head size 64/128/256, Q * (H / H_kv) <= 64 packed rows,
+    pages of at least 16 positions, 16-byte aligned rows."""
+    H, D = query.shape[1], query.shape[2]
+    if D not in AL.HEAD_SIZES or H % num_kv_heads or Q < 1 or Q * (H // num_kv_heads) > AL.MAX_ROWS:
+        return False
+    if key_cache.shape[1] < AL.MIN_PAGE:
+        return False
+    return True
+
+
+def gqa_packed_spec_attention(query, key_cache, value_cache, out, seq_lens, block_table, num_reqs, Q, num_kv_heads,
+                              scale, num_splits=DEFAULT_NUM_SPLITS, min_chunk=DEFAULT_MIN_CHUNK, block_n=32,
+                              num_warps=4, num_stages=2, combine_warps=2):
+    """query/out [>= num_reqs*Q, H, D] bf16; key_cache/value_cache [num_blocks, PAGE, H_kv, D] bf16 (strided
+    views are fine); seq_lens int32 [num_reqs]; block_table int32 [num_reqs, max_blocks].  Returns out."""
+    del block_n, num_warps, num_stages, combine_warps
+    for t, n in ((query, "query"), (key_cache, "key_cache"), (value_cache, "value_cache"), (out, "out")):
+        _check_bf16_rows(t, n)
+    if seq_lens.dtype != torch.int32 or block_table.dtype != torch.int32:
+        raise TypeError("seq_lens and block_table must be int32")
+    if block_table.stride(-1) != 1:
+        raise ValueError("block_table must be contiguous in its last dimension")
+    B = int(num_reqs)
+    H, D = query.shape[1], query.shape[2]
+    if out.shape[1] != H or out.shape[2] != D or key_cache.shape[3] != D or value_cache.shape[3] != D:
+        raise ValueError("query, out and the caches must share the head size and head count")
+    if key_cache.shape[2] != num_kv_heads or value_cache.shape[2] != num_kv_heads:
+        raise ValueError("cache kv-head count does not match num_kv_heads")
+    if query.shape[0] < B * Q or out.shape[0] < B * Q or seq_lens.numel() < B or block_table.shape[0] < B:
+        raise ValueError("batch tensors are smaller than num_reqs * Q")
+    page = key_cache.shape[1]
+    L = AL.load()
+    ws_bytes = AL.workspace_bytes(B, Q, H, num_kv_heads, D, num_splits)
+    if ws_bytes == 0:
+        raise ValueError("invalid attention sizes")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
+    stream = torch.cuda.current_stream(query.device).cuda_stream
+    rc = L.qf_spec_attention(
+        query.data_ptr(), query.stride(0), query.stride(1),
+        key_cache.data_ptr(), key_cache.stride(0), key_cache.stride(1), key_cache.stride(2),
+        value_cache.data_ptr(), value_cache.stride(0), value_cache.stride(1), value_cache.stride(2),
+        block_table.data_ptr(), block_table.stride(0), seq_lens.data_ptr(),
+        out.data_ptr(), out.stride(0), out.stride(1),
+        B, int(Q), H, int(num_kv_heads), D, page, float(scale), int(num_splits), int(min_chunk),
+        ws.data_ptr(), ws_bytes, stream)
+    AL.check(rc, "qf_spec_attention")
+    return out

@@ -130,3 +130,58 @@ def test_other_entry_points_validate_host_only():
     assert lib.qf_w8a16_unpack(1 << 20, 1 << 21, 96, 16, 96, None) == L.ERR_UNSUPPORTED  # K % 64
     assert lib.qf_quantize_rows_int8(None, 8, None, None, 1, 8, None) == L.ERR_INVALID_ARG
     assert lib.qf_argmax_rows_bf16(1 << 20, 8, 1, 8, 9, 0, 1 << 21, None) == L.ERR_INVALID_ARG  # n_valid > N
+
+
+# ---- libqf_spec_attn.so (include/qf_spec_attn.h) ----
+
+ATTN_HEADER = os.path.join(os.path.dirname(HEADER), "qf_spec_attn.h")
+
+
+def test_attention_header_declares_the_python_export_list():
+    from qwen_fastpath import _attn_lib as AL
+    text = open(ATTN_HEADER).read()
+    syms = sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(qf_\w+)\(", text, flags=re.M)))
+    assert syms == sorted(AL.EXPORTS)
+    lib = AL.load()
+    for name in syms:
+        assert hasattr(lib, name), name
+    m = re.search(r"#define QF_SPEC_ATTN_ABI_VERSION (\d+)", text)
+    assert lib.qf_spec_attn_abi_version() == int(m.group(1)) == AL.ABI_VERSION
+    for macro, value in (("MAX_ROWS", AL.MAX_ROWS), ("MIN_PAGE", AL.MIN_PAGE), ("KEY_BLOCK", AL.KEY_BLOCK)):
+        assert int(re.search(rf"#define QF_SPEC_ATTN_{macro} (\d+)", text).group(1)) == value
+
+
+def test_attention_workspace_bytes():
+    from qwen_fastpath import _attn_lib as AL
+    B, Q, H, HKV, D, S = 2, 3, 24, 4, 256, 64
+    R = Q * H // HKV
+    n = B * HKV * S * R * (D + 1) * 4
+    assert AL.workspace_bytes(B, Q, H, HKV, D, S) == (n + 255) // 256 * 256
+    assert AL.workspace_bytes(0, Q, H, HKV, D, S) == 0
+    assert AL.workspace_bytes(B, Q, 25, HKV, D, S) == 0   # H not a multiple of H_kv
+
+
+def _attn_call(lib, *, D=256, H=24, HKV=4, Q=3, page=800, splits=64, min_chunk=128, ws_bytes=None,
+               stride=None, ptr_offset=0):
+    """qf_spec_attention on 16-byte aligned host dummies: every case here is rejected before any HIP call."""
+    buf = (ctypes.c_uint8 * 4096)()
+    base = (ctypes.addressof(buf) + 15) // 16 * 16
+    p = base + ptr_offset
+    st = 8 if stride is None else stride
+    ws = lib.qf_spec_attn_workspace_bytes(1, Q, H, HKV, D, splits) if ws_bytes is None else ws_bytes
+    return lib.qf_spec_attention(p, st, st, p, st, st, st, p, st, st, st, base, 1, base, p, st, st,
+                                 1, Q, H, HKV, D, page, 0.0625, splits, min_chunk, base, ws, None)
+
+
+def test_attention_rejects_before_launch():
+    from qwen_fastpath import _attn_lib as AL
+    lib = AL.load()
+    assert _attn_call(lib, D=96) == L.ERR_UNSUPPORTED
+    assert _attn_call(lib, Q=11) == L.ERR_UNSUPPORTED          # 66 packed rows
+    assert _attn_call(lib, HKV=5) == L.ERR_UNSUPPORTED         # 24 % 5
+    assert _attn_call(lib, page=8) == L.ERR_UNSUPPORTED
+    assert _attn_call(lib, stride=12) == L.ERR_UNSUPPORTED
+    assert _attn_call(lib, ptr_offset=8) == L.ERR_UNSUPPORTED
+    assert _attn_call(lib, splits=0) == L.ERR_INVALID_ARG
+    assert _attn_call(lib, min_chunk=0) == L.ERR_INVALID_ARG
+    assert _attn_call(lib, ws_bytes=1024) == L.ERR_WORKSPACE
