@@ -18,6 +18,8 @@ line on stdout.
 Other modes, one JSON line each: --workload stack64 (64 distinct layers, one hipGraph per decode
 step, the layer output re-normalised to unit RMS as the next layer's input); --workload msweep (gate_up at M = 1..16);
 --workload lm_head (int8 draft head 151936x5120 + pad-masked argmax at M = 1, 4);
+--workload spec_attn (split-KV verification attention of one full-attention layer, H=24, H_kv=4,
+D=256, 800-position pages, at the reference's contexts and batch shapes);
 --profile-gemm NAME --iters N (only that GEMM, for rocprofv3); --copy-probe (a plain device copy
 of known size, for counter calibration).
 """
@@ -155,7 +157,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--workload", choices=["layer", "stack64", "msweep", "lm_head", "prefill"], default="layer")
+    ap.add_argument("--workload", choices=["layer", "stack64", "msweep", "lm_head", "prefill", "spec_attn"],
+                    default="layer")
     ap.add_argument("--layers", type=int, default=4, help="distinct layers rotated through (layer workload)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--profile-gemm", choices=list(GEMMS), default=None)
@@ -165,6 +168,8 @@ def main():
     ap.add_argument("--layout", choices=["tiled", "rowmajor"], default="tiled",
                     help="weight layout: tiled = pre-permuted at load (default), rowmajor = checkpoint layout")
     ap.add_argument("--cfg", default=None, help="explicit config kernel,split_k,tiles,waves,depth,hint (profile mode)")
+    ap.add_argument("--attn-case", default=None,
+                    help="spec_attn profile mode: CTX,Q,B -- only that case, --iters calls, no JSON line")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -216,6 +221,9 @@ def main():
         return
     if args.workload == "prefill":
         run_prefill(torch, qf, dev, args)
+        return
+    if args.workload == "spec_attn":
+        run_spec_attn(torch, qf, dev, args)
         return
 
     M = M_TOKENS
@@ -486,6 +494,115 @@ def run_lm_head(torch, qf, dev, args):
             "config": {"workload": "int8 draft lm_head 151936x5120 + pad-masked argmax (value = M=1 GB/s)",
                        "weight_layout": "tiled"},
             "per_m": rows}
+    print(json.dumps(line), flush=True)
+
+
+# The reference kernel's published latency per full-attention layer on an A100 (µs), by (Q, requests)
+# and cached context: data/measurements.json "attention_kernel" (ours_Q3, ours_Q4, ours_Q3_B2).
+ATTN_REF_A100_US = {
+    (3, 1): {1000: 23.9, 8000: 41.6, 38000: 126.2, 100000: 294.1},
+    (4, 1): {1000: 24.4, 8000: 43.8, 38000: 129.1, 100000: 294.7},
+    (3, 2): {1000: 26.5, 8000: 70.2, 38000: 236.1, 100000: 565.5},
+}
+ATTN_METRIC = ("split-KV verification attention: KV-cache GB/s (% of 8 TB/s) and µs per full-attention layer, "
+               "38K context, Q=3, 1 request")
+
+
+def attn_kv_bytes(lens, HKV=4, D=256) -> int:
+    """Compulsory bytes of one call: every cached position's K and V rows of every kv head, once."""
+    return sum(int(n) for n in lens) * HKV * 2 * D * 2
+
+
+def attn_cpu_baseline(ctx=38000, Q=3):
+    """The oracle's fp64 restatement of the reference gold (bench/test_spec_attn.py:23-31) on one layer."""
+    import numpy as np
+    from oracle import attn as A
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, 16))
+    try:
+        from threadpoolctl import threadpool_limits
+        threadpool_limits(limits=cores)
+    except Exception:  # noqa: BLE001 - threadpoolctl optional
+        pass
+    inp = A.gen_spec_inputs(ctx, Q, 1, seed=0)
+    q, kc, vc = inp.query(), inp.key_cache(), inp.value_cache()
+    best = float("inf")
+    for _ in range(2):
+        t0 = time.perf_counter()
+        A.spec_attention(q, kc, vc, inp.seq_lens, inp.block_table, 1, Q, 4, 256 ** -0.5)
+        best = min(best, time.perf_counter() - t0)
+    b = attn_kv_bytes(inp.seq_lens)
+    return {"value": round(b / best / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"one layer at ctx={ctx}, Q={Q}, 1 request ({b / 1e6:.1f} MB of KV), fp64 numpy over "
+                      f"{cores} threads, best of 2: {best * 1e3:.0f} ms/layer"}
+
+
+def run_spec_attn(torch, qf, dev, args):
+    """One full-attention layer of the 27B model (H=24, H_kv=4, D=256, 800-position pages, K and V
+    interleaved per row as [page][H_kv][PAGE][2D]) at the reference's contexts and batch shapes
+    (bench/test_spec_attn.py:7-19).  Each layer's pages come from a shared 1.7 GB pool through its own
+    shuffled block table, and the calls rotate over enough layers (>= 2, > 512 MB) that every call
+    streams its KV from HBM; calls are captured in a graph."""
+    H, HKV, D, PAGE = 24, 4, 256, 800
+    npages = 520
+    g = torch.Generator(device=dev)
+    g.manual_seed(21)
+    kv = torch.randn(npages, HKV, PAGE, 2 * D, device=dev, generator=g).to(torch.bfloat16)
+    key_cache, value_cache = kv.transpose(1, 2).split(D, dim=-1)
+    rows = {}
+    cases = [(Q, B, ctx) for (Q, B) in ATTN_REF_A100_US for ctx in (1000, 8000, 38000, 100000)]
+    if args.attn_case:
+        ctx, Q, B = (int(v) for v in args.attn_case.split(","))
+        cases = [(Q, B, ctx)]
+    for Q, B, ctx in cases:
+        ref = ATTN_REF_A100_US.get((Q, B), {})
+        if True:
+            L = ctx + Q
+            lens = [max(L - 7 * b, 1) for b in range(B)]
+            nblk = (L + PAGE - 1) // PAGE + 1
+            per_layer = B * nblk
+            # enough layers that one pass reads > 640 MB of KV (2.5x the MALL), within the pool
+            n_layers = max(2, min(128, npages // per_layer, -(-(640 << 20) // attn_kv_bytes(lens, HKV, D))))
+            assert n_layers * per_layer <= npages
+            perm = torch.randperm(npages, device=dev, generator=g).to(torch.int32)
+            tables = [perm[i * per_layer:(i + 1) * per_layer].view(B, nblk).contiguous() for i in range(n_layers)]
+            seq_lens = torch.tensor(lens, dtype=torch.int32, device=dev)
+            q = torch.randn(B * Q, H, D, device=dev, generator=g).to(torch.bfloat16)
+            out = torch.empty_like(q)
+            scale = D ** -0.5
+
+            def call(i):
+                qf.gqa_packed_spec_attention(q, key_cache, value_cache, out, seq_lens, tables[i], B, Q, HKV, scale)
+            if args.attn_case:
+                for it in range(args.iters):
+                    call(it % n_layers)
+                torch.cuda.synchronize()
+                log(f"spec_attn profile: {args.iters} calls at ctx={ctx} Q={Q} B={B}, {n_layers} layers rotated")
+                return
+            reps = max(1, 32 // n_layers)
+            us = time_graph(torch, lambda: [call(i) for _ in range(reps) for i in range(n_layers)], reps * n_layers)
+            b = attn_kv_bytes(lens, HKV, D)
+            key = f"Q{Q}_B{B}_ctx{ctx}"
+            rows[key] = {"us": round(us, 2), "GB_s": round(b / us / 1e3, 1), "pct_peak": round(100 * b / us / 1e3 / PEAK_GBS, 1),
+                         "kv_bytes": b, "reference_a100_us": ref.get(ctx),
+                         "speedup_vs_reference_a100": round(ref[ctx] / us, 2) if ctx in ref else None,
+                         "layers_rotated": n_layers}
+            log(f"  spec_attn Q={Q} B={B} ctx={ctx:6d}: {us:8.2f} us  {b / us / 1e3:7.0f} GB/s  "
+                f"{100 * b / us / 1e3 / PEAK_GBS:5.1f}%  (reference on A100: {ref.get(ctx)} us)")
+    head = rows["Q3_B1_ctx38000"]
+    line = {"metric": ATTN_METRIC, "value": head["GB_s"], "unit": "GB/s", "n_gpus": 1, "steps": 10, "warmup": 2,
+            "ms_per_step": round(head["us"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic (N(0,1) bf16 queries and KV cache, shuffled pages)",
+            "config": {"workload": "one full-attention layer, H=24 H_kv=4 D=256, 800-position pages; value = "
+                                   "ctx 38000, Q=3, 1 request", "num_splits": 64, "min_chunk": 128},
+            "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": PEAK_GBS, "unit": "GB/s",
+                         "frac": round(head["GB_s"] / PEAK_GBS, 4), "traffic": None},
+            "per_case": rows}
+    if not args.no_cpu:
+        line["cpu_baseline"] = attn_cpu_baseline()
     print(json.dumps(line), flush=True)
 
 

@@ -15,9 +15,9 @@
  * graph):
  *   1. per (split, request, kv head): the q_len * G query rows that share the kv head are packed into
  *      one tile, and the split's slice of the cached prefix [0, seq_len - q_len) is streamed once for
- *      all of them; each split writes its normalised partial output and base-2 log-sum-exp;
- *   2. per (token, head): the row attends this step's q_len in-flight positions causally and merges
- *      them with the active prefix splits by log-sum-exp.
+ *      all of them; the last active split also takes this step's q_len in-flight positions, masked
+ *      causally per row; each split writes its normalised partial output and base-2 log-sum-exp;
+ *   2. per (token, head): the row's partials are merged by log-sum-exp.
  *
  * Layouts (strides in elements, the last dimension contiguous):
  *   query      bf16 [>= num_reqs * q_len, H, D]
@@ -26,8 +26,8 @@
  *   block_table int32 [num_reqs, >= blocks of the longest request], row stride bt_stride
  *   seq_lens   int32 [num_reqs]: cached positions of each request, this step's q_len included
  *   out        bf16 [>= num_reqs * q_len, H, D]
- * Alignment contract: every pointer 16-byte aligned and every stride a multiple of 8 elements;
- * otherwise QF_ERR_UNSUPPORTED.
+ * Alignment contract: every pointer 16-byte aligned and every stride a multiple of 8 elements, and
+ * 64 * (token stride of either cache) below 2^31; otherwise QF_ERR_UNSUPPORTED.
  *
  * Reference interfaces replaced (paths relative to the reference repository):
  *   qf_spec_attention             <- gqa_packed_spec_attention + _prefix_split_kernel +

@@ -7,21 +7,23 @@
 // q_len * G query rows sharing it; a second kernel attends this step's q_len positions causally and
 // merges everything by log-sum-exp.  The kernels themselves are designed for CDNA4:
 //
-//   prefix kernel, one 256-thread workgroup per (split, request, kv head):
+//   prefix kernel, one 256-thread workgroup per (split, request, kv head); the last active split also
+//   takes this step's q_len in-flight positions, masked causally per query row:
 //   * K and V rows of a 32-position stage are copied global -> LDS with 16-byte direct-to-LDS loads
 //     (no VGPR staging), 16-byte pieces XOR-swizzled per row so that the MFMA fragment reads below
-//     are free of bank conflicts; a ring of kRing stages keeps kRing - 2 stages in flight while a
+//     are free of bank conflicts; a ring of kRing stages keeps kRing - 1 stages in flight while a
 //     stage is computed, with one barrier per stage.
+//   * Wavefront w takes key tile w & 1 (16 of the stage's 32 positions) and d half w >> 1.
 //   * S^T = K . Q^T on v_mfma_f32_16x16x32_bf16 with K as the A operand (16 positions x 32 d) and the
 //     packed query rows as B (16 rows), so each lane's accumulator holds 4 positions of ONE row: the
-//     online softmax needs only two cross-lane steps per row, and the probabilities in a lane are
-//     already the B fragment of the next product.
-//   * O^T = V^T . P^T on the same instruction, with the 32 positions of a stage ordered so that the
-//     B fragment is the lane's own 8 probabilities; V^T fragments are gathered from the LDS rows.
-//   * Every wavefront computes the scores of all rows (cheap at 2M flop/byte) and accumulates its own
-//     quarter of the head dimension, so wavefronts never exchange softmax state.
-//   suffix/combine kernel, one 256-thread workgroup per (token, head): the row's partials are merged
-//   by 4 thread groups, the in-flight positions by the first, then the groups by LDS.
+//     online softmax needs only two cross-lane steps per row, and the lane's 4 probabilities are
+//     already its B fragment of the next product.
+//   * O^T = V^T . P^T on v_mfma_f32_16x16x16_bf16 over the tile's 16 positions and the wavefront's
+//     half of the head dimension; V^T fragments are gathered from the LDS rows.
+//   * The two key tiles keep separate softmax states (the two wavefronts of a d half compute the same
+//     scores), merged once per split through LDS; wavefronts never exchange state inside the loop.
+//   combine kernel, one 256-thread workgroup per (token, head): the row's split partials are merged by
+//   log-sum-exp in thread groups, then the groups through LDS.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -35,6 +37,7 @@ namespace qfa {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef const void __attribute__((address_space(1)))* gptr_t;
@@ -124,11 +127,12 @@ struct Geo {
   static constexpr int kRowsPerCopy = 1024 / kRowBytes;
   static constexpr int kRing = 4;                                 // stages resident in LDS
   static constexpr int kLds = kRing * 2 * kStageBytes;  // dynamic LDS (the block-table window is static)
-  static constexpr int kDTiles = D / 16 / kWaves;                 // 16-wide d tiles per wavefront
+  static constexpr int kDTiles = D / 32;                          // 16-wide d tiles per wavefront (half of D)
   static constexpr int kDChunks = D / 32;                         // 32-d MFMA steps of a score
   static_assert(kCopies >= 1 && kStageBytes % (kWaves * 1024) == 0, "stage must split into wave copies");
   static_assert(kDTiles >= 1, "head size too small");
   static_assert(kLds + kTablePages * 4 <= kMaxDynLds + 8 * 1024 - 256, "LDS budget");
+  static_assert(2 * 4 * kDTiles * 64 * 16 + 2 * 4 * 64 * 8 <= kLds, "key-tile merge fits the ring");
   // The 16-byte piece of row n that lands at LDS position p is piece p ^ swz(n): 16 consecutive rows
   // read at one piece index then hit 16 distinct bank groups.
   __device__ static __forceinline__ int swz(int n) { return kChunks >= 16 ? (n & 15) : ((n >> 1) & 7); }
@@ -150,44 +154,63 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const int seq = a.seq_lens[b];
   const int prefix = seq - a.Q > 0 ? seq - a.Q : 0;
   const int chunk = split_chunk(prefix, a.splits, a.min_chunk);
+  const int n_active = prefix > 0 ? (prefix + chunk - 1) / chunk : 0;
+  // Split s takes positions [s * chunk, min((s + 1) * chunk, prefix)); the last active split (split 0
+  // when the prefix is empty) also takes this step's in-flight positions [prefix, seq).  Query qi sees
+  // the positions up to seq - q_len + qi, which include the whole prefix, so one causal bound per
+  // row covers both kinds of position.
+  const int last_split = n_active > 0 ? n_active - 1 : 0;
   const int start = split * chunk;
-  if (start >= prefix) return;  // uniform: the whole workgroup leaves
-  const int end = min(start + chunk, prefix);
+  const int end = split == last_split ? seq : min(start + chunk, prefix);
+  if (split > last_split || start >= end) return;  // uniform: the whole workgroup leaves
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int l16 = lane & 15;
   const int qg = lane >> 4;
+  const int kh = wave & 1;   // key tile of each stage
+  const int dh = wave >> 1;  // half of the head dimension
 
   // ---- packed query rows: B fragments of the score product (rows >= R repeat row R - 1) ----
   bf16x8_t qf[RT][Gm::kDChunks];
+  int last[RT];  // last visible position of the lane's score row in each row tile
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int r = min(rt * 16 + l16, a.R - 1);
     const int qi = r / a.G;
     const int h = hkv * a.G + (r - qi * a.G);
+    last[rt] = seq - a.Q + qi;
     const uint16_t* qrow = a.q + (int64_t)(b * a.Q + qi) * a.sq_t + (int64_t)h * a.sq_h + qg * 8;
 #pragma unroll
     for (int c = 0; c < Gm::kDChunks; ++c) qf[rt][c] = *reinterpret_cast<const bf16x8_t*>(qrow + c * 32);
   }
 
-  // ---- copy schedule: per stage, wavefront `wave` moves NJ KiB of K and NJ KiB of V ----
+  // ---- copy schedule: per stage, wavefront `wave` moves NJ KiB of K and NJ KiB of V.  Lane offsets
+  // within a stage are fixed; per stage only the page bases change (computed in scalar registers) ----
   const int32_t* bt_row = a.bt + (int64_t)b * a.sbt;
-  const uint16_t* kbase = a.kc + (int64_t)hkv * a.sk_h;
-  const uint16_t* vbase = a.vc + (int64_t)hkv * a.sv_h;
-  int row_of[NJ], piece_of[NJ];
+  const char* kbytes = reinterpret_cast<const char*>(a.kc + (int64_t)hkv * a.sk_h);
+  const char* vbytes = reinterpret_cast<const char*>(a.vc + (int64_t)hkv * a.sv_h);
+  int row_of[NJ];
+  uint32_t koff[NJ], voff[NJ], poff[NJ];  // byte offsets: row t's piece, and the piece in row 0
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int t = (wave * NJ + j) * Gm::kRowsPerCopy + lane / Gm::kChunks;
+    const int piece = (lane % Gm::kChunks) ^ Gm::swz(t);
     row_of[j] = t;
-    piece_of[j] = (lane % Gm::kChunks) ^ Gm::swz(t);
+    poff[j] = piece * 16;
+    koff[j] = (uint32_t)(t * a.sk_t * 2) + poff[j];
+    voff[j] = (uint32_t)(t * a.sv_t * 2) + poff[j];
   }
 
-  float m_run[RT], l_run[RT];
+  // online softmax state: m_ref is the row's exponent reference, moved only when a score exceeds it
+  // by more than kRescale (log2 units), so the probabilities stay below 2^kRescale and the
+  // accumulators are rarely rescaled; the result equals the running-maximum form up to rounding
+  constexpr float kRescale = 8.f;
+  float m_ref[RT], l_run[RT];
   f32x4_t o_acc[RT][Gm::kDTiles];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    m_run[rt] = -__builtin_inff();
+    m_ref[rt] = -__builtin_inff();
     l_run[rt] = 0.f;
 #pragma unroll
     for (int dt = 0; dt < Gm::kDTiles; ++dt) o_acc[rt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -206,32 +229,64 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     __syncthreads();
     const int nst = (wend - wstart + kKeyBlock - 1) / kKeyBlock;
 
-    auto copy_stage = [&](int st) {
+    // Stages are copied in order; the next one starts in page pg_n at in-page offset og_n.  A stage
+    // of 32 positions spans at most 3 pages of >= 16 positions.
+    int issued = 0, pg_n = p0, og_n = wstart - p0 * a.page;
+    auto copy_next = [&]() {
+      const int st = issued++;
       uint8_t* slot = lds + (st % kRing) * 2 * Gm::kStageBytes;
-      const int sbase = wstart + st * kKeyBlock;
+      const int nvalid = min(kKeyBlock, wend - (wstart + st * kKeyBlock));
+      const int bnd1 = a.page - og_n;  // rows >= bnd1 lie in the next page, rows >= bnd2 in the one after
+      const int bnd2 = bnd1 + a.page;
+      const int e0 = pg_n - p0;
+      const int64_t blk0 = __builtin_amdgcn_readfirstlane(tbl[e0]);
+      const int64_t kb0 = (blk0 * a.sk_b + (int64_t)og_n * a.sk_t) * 2;
+      const int64_t vb0 = (blk0 * a.sv_b + (int64_t)og_n * a.sv_t) * 2;
+      if (bnd1 >= kKeyBlock && nvalid == kKeyBlock) {
+        // the whole stage lies in one page (uniform): one base per tensor
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int pos = min(sbase + row_of[j], wend - 1);  // rows past the window repeat its last position
-        const int pg = pos / a.page;
-        const int64_t blk = tbl[pg - p0];
-        const int off = pos - pg * a.page;
-        const int copy = wave * NJ + j;
-        const int64_t kel = blk * a.sk_b + (int64_t)off * a.sk_t + piece_of[j] * 8;
-        const int64_t vel = blk * a.sv_b + (int64_t)off * a.sv_t + piece_of[j] * 8;
-        __builtin_amdgcn_global_load_lds((gptr_t)(kbase + kel), (lptr_t)(slot + copy * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((gptr_t)(vbase + vel), (lptr_t)(slot + Gm::kStageBytes + copy * 1024),
-                                         16, 0, 0);
+        for (int j = 0; j < NJ; ++j) {
+          const int copy = wave * NJ + j;
+          __builtin_amdgcn_global_load_lds((gptr_t)(kbytes + kb0 + koff[j]), (lptr_t)(slot + copy * 1024), 16, 0, 0);
+          __builtin_amdgcn_global_load_lds((gptr_t)(vbytes + vb0 + voff[j]),
+                                           (lptr_t)(slot + Gm::kStageBytes + copy * 1024), 16, 0, 0);
+        }
+      } else {
+        const int64_t blk1 = __builtin_amdgcn_readfirstlane(tbl[min(e0 + 1, npg - 1)]);
+        const int64_t blk2 = __builtin_amdgcn_readfirstlane(tbl[min(e0 + 2, npg - 1)]);
+        const int64_t kb1 = (blk1 * a.sk_b + (int64_t)(og_n - a.page) * a.sk_t) * 2;
+        const int64_t kb2 = (blk2 * a.sk_b + (int64_t)(og_n - 2 * a.page) * a.sk_t) * 2;
+        const int64_t vb1 = (blk1 * a.sv_b + (int64_t)(og_n - a.page) * a.sv_t) * 2;
+        const int64_t vb2 = (blk2 * a.sv_b + (int64_t)(og_n - 2 * a.page) * a.sv_t) * 2;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const bool valid = row_of[j] < nvalid;  // rows past the window re-read the stage's first row
+          const int t = valid ? row_of[j] : 0;
+          const int64_t kb = t >= bnd2 ? kb2 : (t >= bnd1 ? kb1 : kb0);
+          const int64_t vb = t >= bnd2 ? vb2 : (t >= bnd1 ? vb1 : vb0);
+          const int copy = wave * NJ + j;
+          __builtin_amdgcn_global_load_lds((gptr_t)(kbytes + kb + (valid ? koff[j] : poff[j])),
+                                           (lptr_t)(slot + copy * 1024), 16, 0, 0);
+          __builtin_amdgcn_global_load_lds((gptr_t)(vbytes + vb + (valid ? voff[j] : poff[j])),
+                                           (lptr_t)(slot + Gm::kStageBytes + copy * 1024), 16, 0, 0);
+        }
+      }
+      og_n += kKeyBlock;
+      while (og_n >= a.page) {
+        og_n -= a.page;
+        ++pg_n;
       }
     };
 
     // prologue: stages 0 .. kRing-2 in flight
 #pragma unroll
     for (int s = 0; s < kRing - 1; ++s)
-      if (s < nst) copy_stage(s);
+      if (s < nst) copy_next();
 
     constexpr int kCopiesPerStage = 2 * NJ;  // vector-memory instructions of one stage
     for (int st = 0; st < nst; ++st) {
-      // Stage st has landed once at most the later issued stages' copies are outstanding.
+      // Stage st has landed once at most the later issued stages' copies are outstanding.  Stages
+      // up to st + kRing - 2 have been issued; st + kRing - 1 goes out after the barrier below.
       const int after = min(kRing - 2, nst - 1 - st);
       if (after >= 2) {
         wait_vmcnt<2 * kCopiesPerStage>();
@@ -241,113 +296,138 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
         wait_vmcnt<0>();
       }
       ring_barrier();
+      // Refill the slot every wavefront finished with before this barrier (stage st - 1's); three
+      // stages are then in flight while this one is computed.
+      if (st + kRing - 1 < nst) copy_next();
+      __builtin_amdgcn_sched_barrier(0);
 
       const uint8_t* ks = lds + (st % kRing) * 2 * Gm::kStageBytes;
       const uint8_t* vs = ks + Gm::kStageBytes;
       const int sbase = wstart + st * kKeyBlock;
 
-      // S^T tiles: positions 16 kt + 4 qg + i, row 16 rt + l16
-      f32x4_t sc[2][RT];
+      // S^T tile of this wavefront's key tile kh: positions 16 kh + 4 qg + i, row 16 rt + l16
+      f32x4_t sc[RT];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) sc[kt][rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int rt = 0; rt < RT; ++rt) sc[rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      const int n_k = kh * 16 + l16;
 #pragma unroll
       for (int c = 0; c < Gm::kDChunks; ++c) {
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          const int n = kt * 16 + l16;
-          const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(
-              ks + n * Gm::kRowBytes + (((4 * c + qg) ^ Gm::swz(n)) << 4));
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt)
-            sc[kt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[rt][c], sc[kt][rt], 0, 0, 0);
-        }
-      }
-
-      // online softmax in base 2; the lane's 8 probabilities form its B fragment of O^T = V^T P^T
-      bf16x8_t pf[RT];
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        float v[8];
-        float mx = -__builtin_inff();
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int pos = sbase + kt * 16 + qg * 4 + i;
-            const float x = pos < wend ? sc[kt][rt][i] * a.qk_scale : -__builtin_inff();
-            v[kt * 4 + i] = x;
-            mx = fmaxf(mx, x);
-          }
-        mx = wave_max_q(mx);
-        const float m_new = fmaxf(m_run[rt], mx);  // finite: every stage holds a valid position
-        const float alpha = fast_exp2(m_run[rt] - m_new);
-        float psum = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          v[i] = fast_exp2(v[i] - m_new);
-          psum += v[i];
-        }
-        l_run[rt] = l_run[rt] * alpha + psum;
-        m_run[rt] = m_new;
-#pragma unroll
-        for (int dt = 0; dt < Gm::kDTiles; ++dt) o_acc[rt][dt] *= alpha;
-        pf[rt] = __builtin_bit_cast(bf16x8_t, u32x4_t{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]),
-                                                      pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7])});
-      }
-
-      // O^T += V^T P^T over this wavefront's d tiles.  k slot 8 qg + i holds position
-      // (i < 4 ? 4 qg + i : 16 + 4 qg + i - 4), the positions of the lane's own probabilities.
-#pragma unroll
-      for (int dt = 0; dt < Gm::kDTiles; ++dt) {
-        const int d = (wave * Gm::kDTiles + dt) * 16 + l16;
-        const int dpiece = d >> 3;
-        const int dbyte = (d & 7) * 2;
-        uint32_t h[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int n = (i < 4 ? 0 : 16) + qg * 4 + (i & 3);
-          h[i] = *reinterpret_cast<const uint16_t*>(vs + n * Gm::kRowBytes + ((dpiece ^ Gm::swz(n)) << 4) + dbyte);
-        }
-        const bf16x8_t vf = __builtin_bit_cast(
-            bf16x8_t, u32x4_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)});
+        const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(
+            ks + n_k * Gm::kRowBytes + (((4 * c + qg) ^ Gm::swz(n_k)) << 4));
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
-          o_acc[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[rt], o_acc[rt][dt], 0, 0, 0);
+          sc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[rt][c], sc[rt], 0, 0, 0);
       }
 
-      // Refill the slot every wavefront finished with before this stage's barrier.
-      if (st + kRing - 1 < nst) copy_stage(st + kRing - 1);
+      // softmax weights in base 2; the lane's 4 probabilities are its B fragment of O^T = V^T P^T.
+      // A stage wholly inside every row's visible range needs no mask.
+      const int pos0 = sbase + kh * 16 + qg * 4;
+      const bool full = sbase + kKeyBlock <= wend && sbase + kKeyBlock - 1 <= seq - a.Q;
+      s16x4_t pf[RT];
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        float v[4];
+        if (full) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = sc[rt][i] * a.qk_scale;
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            v[i] = pos0 + i < wend && pos0 + i <= last[rt] ? sc[rt][i] * a.qk_scale : -__builtin_inff();
+        }
+        const float mx = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+        if (__any(mx > m_ref[rt] + kRescale)) {  // wave-uniform: move the references of all rows
+          const float m_new = fmaxf(m_ref[rt], wave_max_q(mx));
+          // -inf only for a row that has seen no position yet: exponent base 0 then
+          const float alpha = fast_exp2(m_ref[rt] - (m_new == -__builtin_inff() ? 0.f : m_new));
+          l_run[rt] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < Gm::kDTiles; ++dt) o_acc[rt][dt] *= alpha;
+          m_ref[rt] = m_new;
+        }
+        const float m_base = m_ref[rt] == -__builtin_inff() ? 0.f : m_ref[rt];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = fast_exp2(v[i] - m_base);
+        l_run[rt] += (v[0] + v[1]) + (v[2] + v[3]);
+        pf[rt] = __builtin_bit_cast(s16x4_t, u32x2_t{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3])});
+      }
+
+      // O^T += V^T P^T over this wavefront's d half and key tile (k slot 4 qg + i = position 4 qg + i)
+#pragma unroll
+      for (int dt = 0; dt < Gm::kDTiles; ++dt) {
+        const int d = (dh * Gm::kDTiles + dt) * 16 + l16;
+        const int dpiece = d >> 3;
+        const int dbyte = (d & 7) * 2;
+        uint32_t h[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int n = kh * 16 + qg * 4 + i;
+          h[i] = *reinterpret_cast<const uint16_t*>(vs + n * Gm::kRowBytes + ((dpiece ^ Gm::swz(n)) << 4) + dbyte);
+        }
+        const s16x4_t vf = __builtin_bit_cast(s16x4_t, u32x2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)});
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+          o_acc[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pf[rt], o_acc[rt][dt], 0, 0, 0);
+      }
     }
     wait_vmcnt<0>();
     __syncthreads();  // the next window rewrites the table and the ring
     wstart = wend;
   }
 
-  // ---- partial output (normalised) and base-2 log-sum-exp of each packed row ----
+  // ---- merge the two key tiles' states (wavefront kh = 1 hands its state to kh = 0 of the same d
+  // half through the now idle ring), then the partial output (normalised) and base-2 log-sum-exp of
+  // each packed row; a row that saw no position (possible only in the split holding the in-flight
+  // positions) is written as 0 with log-sum-exp -inf ----
+  float* xo = reinterpret_cast<float*>(lds);                        // [2][RT][kDTiles][64] x f32x4
+  float* xs = xo + 2 * RT * Gm::kDTiles * kWave * 4;               // [2][RT][64] x (m, l)
+  float l_tot[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) l_tot[rt] = wave_sum_q(l_run[rt]);
+  if (kh == 1) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+      for (int dt = 0; dt < Gm::kDTiles; ++dt)
+        *reinterpret_cast<f32x4_t*>(xo + (((dh * RT + rt) * Gm::kDTiles + dt) * kWave + lane) * 4) = o_acc[rt][dt];
+      xs[((dh * RT + rt) * kWave + lane) * 2] = m_ref[rt];
+      xs[((dh * RT + rt) * kWave + lane) * 2 + 1] = l_tot[rt];
+    }
+  }
+  __syncthreads();
+  if (kh == 1) return;
   const int64_t part = ((int64_t)blockIdx.y * a.splits + split) * a.R;
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    const float l_tot = wave_sum_q(l_run[rt]);
-    const float inv = 1.f / l_tot;
+    const float m1 = xs[((dh * RT + rt) * kWave + lane) * 2];
+    const float l1 = xs[((dh * RT + rt) * kWave + lane) * 2 + 1];
+    const float mt = fmaxf(m_ref[rt], m1);
+    const float mb = mt == -__builtin_inff() ? 0.f : mt;
+    const float a0 = fast_exp2(m_ref[rt] - mb), a1 = fast_exp2(m1 - mb);
+    const float lt = l_tot[rt] * a0 + l1 * a1;
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
     const int r = rt * 16 + l16;
     if (r < a.R) {
       float* orow = a.o_part + (part + r) * D;
 #pragma unroll
-      for (int dt = 0; dt < Gm::kDTiles; ++dt)
-        *reinterpret_cast<f32x4_t*>(orow + (wave * Gm::kDTiles + dt) * 16 + qg * 4) = o_acc[rt][dt] * inv;
-      if (wave == 0 && qg == 0) a.lse_part[part + r] = m_run[rt] + __log2f(l_tot);
+      for (int dt = 0; dt < Gm::kDTiles; ++dt) {
+        const f32x4_t o1 =
+            *reinterpret_cast<const f32x4_t*>(xo + (((dh * RT + rt) * Gm::kDTiles + dt) * kWave + lane) * 4);
+        *reinterpret_cast<f32x4_t*>(orow + (dh * Gm::kDTiles + dt) * 16 + qg * 4) =
+            (o_acc[rt][dt] * a0 + o1 * a1) * inv;
+      }
+      if (dh == 0 && qg == 0) a.lse_part[part + r] = lt > 0.f ? mt + __log2f(lt) : -__builtin_inff();
     }
   }
 }
 
-// One (token, head) row per workgroup: the causal in-flight positions and the active prefix splits,
-// merged by log-sum-exp (the reference's _suffix_combine_kernel, spec_attn.py:78-132).
+// One (token, head) row per workgroup: the row's split partials merged by log-sum-exp (the merge of
+// the reference's _suffix_combine_kernel, spec_attn.py:119-131).
 template <int D>
 __global__ __launch_bounds__(kThreads) void spec_combine_kernel(AttnArgs a) {
   constexpr int NQ = D / 4;          // threads per group, 4 d values each
   constexpr int NGRP = kThreads / NQ;
+  constexpr int kBatch = 16;         // parts a thread loads before merging them
   __shared__ float sm_m[NGRP], sm_l[NGRP];
   __shared__ __align__(16) float sm_acc[NGRP][D];
 
@@ -365,62 +445,35 @@ __global__ __launch_bounds__(kThreads) void spec_combine_kernel(AttnArgs a) {
   const int prefix = seq - a.Q > 0 ? seq - a.Q : 0;
   const int chunk = split_chunk(prefix, a.splits, a.min_chunk);
   const int n_active = prefix > 0 ? (prefix + chunk - 1) / chunk : 0;
+  // the in-flight positions ride with the last active split (split 0 when the prefix is empty)
+  const int n_list = n_active > 0 ? n_active : (seq > 0 ? 1 : 0);
 
   float m = -__builtin_inff(), l = 0.f;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  // merge one part (base-2 log-sum-exp `e`, normalised output `o`) into the running state
-  auto merge = [&](float e, f32x4_t o) {
-    const float mn = fmaxf(m, e);
-    const float c_old = fast_exp2(m - mn);
-    const float w = fast_exp2(e - mn);
-    acc = acc * c_old + o * w;
-    l = l * c_old + w;
-    m = mn;
-  };
-
-  // prefix splits: group grp takes splits grp, grp + NGRP, ...
   const int64_t part0 = ((int64_t)(b * a.HKV + hkv) * a.splits) * a.R + r;
-  {
-    int sp = grp;
-    for (; sp + 3 * NGRP < n_active; sp += 4 * NGRP) {
-      float e[4];
-      f32x4_t o[4];
+  // group grp merges the parts grp, grp + NGRP, ...
+  for (int base = grp; base < n_list; base += NGRP * kBatch) {
+    float e[kBatch];
+    f32x4_t o[kBatch];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int64_t idx = part0 + (int64_t)(sp + u * NGRP) * a.R;
+    for (int u = 0; u < kBatch; ++u) {
+      const int i = base + u * NGRP;
+      e[u] = -__builtin_inff();
+      if (i < n_list) {
+        const int64_t idx = part0 + (int64_t)i * a.R;
         e[u] = a.lse_part[idx];
         o[u] = *reinterpret_cast<const f32x4_t*>(a.o_part + idx * D + dq * 4);
       }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) merge(e[u], o[u]);
     }
-    for (; sp < n_active; sp += NGRP) {
-      const int64_t idx = part0 + (int64_t)sp * a.R;
-      merge(a.lse_part[idx], *reinterpret_cast<const f32x4_t*>(a.o_part + idx * D + dq * 4));
-    }
-  }
-
-  // in-flight positions seq - Q .. seq - Q + qi (group 0): each is a part with e = score, o = v
-  if (grp == 0) {
-    const uint16_t* qrow = a.q + (int64_t)tok * a.sq_t + (int64_t)h * a.sq_h + dq * 4;
-    const f32x4_t qv = bf16x4_to_f32(*reinterpret_cast<const u32x2_t*>(qrow));
-    const int32_t* bt_row = a.bt + (int64_t)b * a.sbt;
-    for (int j = 0; j <= qi; ++j) {
-      const int pos = seq - a.Q + j;
-      if (pos < 0) continue;  // uniform across the workgroup
-      const int pg = pos / a.page;
-      const int64_t blk = bt_row[pg];
-      const int off = pos - pg * a.page;
-      const f32x4_t kv = bf16x4_to_f32(*reinterpret_cast<const u32x2_t*>(
-          a.kc + blk * a.sk_b + (int64_t)off * a.sk_t + (int64_t)hkv * a.sk_h + dq * 4));
-      const f32x4_t vv = bf16x4_to_f32(*reinterpret_cast<const u32x2_t*>(
-          a.vc + blk * a.sv_b + (int64_t)off * a.sv_t + (int64_t)hkv * a.sv_h + dq * 4));
-      float dot = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dot += kv[i] * qv[i];
-#pragma unroll
-      for (int off2 = NQ / 2; off2 >= 1; off2 >>= 1) dot += __shfl_xor(dot, off2);
-      merge(dot * a.qk_scale, vv);
+    for (int u = 0; u < kBatch; ++u) {
+      if (e[u] == -__builtin_inff()) continue;  // an absent part, or a row that saw no position
+      const float mn = fmaxf(m, e[u]);
+      const float c_old = fast_exp2(m - mn);
+      const float w = fast_exp2(e[u] - mn);
+      acc = acc * c_old + o[u] * w;
+      l = l * c_old + w;
+      m = mn;
     }
   }
 
@@ -530,6 +583,9 @@ int qf_spec_attention(const uint16_t* query, int64_t q_stride_tok, int64_t q_str
                              v_stride_block, v_stride_tok, v_stride_head, o_stride_tok, o_stride_head};
   for (int64_t s : strides)
     if (s < 0 || s % 8) return QF_ERR_UNSUPPORTED;
+  // the prefix kernel keeps per-lane byte offsets of up to one stage of rows in 32 bits
+  if ((k_stride_tok > v_stride_tok ? k_stride_tok : v_stride_tok) * 2 * kKeyBlock >= ((int64_t)1 << 31))
+    return QF_ERR_UNSUPPORTED;
   if (!aligned16(query) || !aligned16(key_cache) || !aligned16(value_cache) || !aligned16(out))
     return QF_ERR_UNSUPPORTED;
   const size_t need = workspace_for(num_reqs, q_len, num_heads, num_kv_heads, head_size, num_splits);
