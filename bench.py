@@ -96,10 +96,10 @@ def capture(torch, fn):
     return g, out
 
 
-def read_traffic():
+def read_traffic(path=PROFILE_SUMMARY):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 summary, if any."""
     try:
-        text = open(PROFILE_SUMMARY).read()
+        text = open(path).read()
     except OSError:
         return None
     f = re.search(r"^fetch_bytes_per_launch:\s*([0-9.eE+]+)", text, re.M)
@@ -506,6 +506,7 @@ ATTN_REF_A100_US = {
 }
 ATTN_METRIC = ("split-KV verification attention: KV-cache GB/s (% of 8 TB/s) and µs per full-attention layer, "
                "38K context, Q=3, 1 request")
+ATTN_PROFILE = os.path.join(ROOT, "profiles", "spec_attn_kernel_trace.md")
 
 
 def attn_kv_bytes(lens, HKV=4, D=256) -> int:
@@ -598,8 +599,10 @@ def run_spec_attn(torch, qf, dev, args):
             "vs_baseline": None, "dtype": "bf16", "data": "synthetic (N(0,1) bf16 queries and KV cache, shuffled pages)",
             "config": {"workload": "one full-attention layer, H=24 H_kv=4 D=256, 800-position pages; value = "
                                    "ctx 38000, Q=3, 1 request", "num_splits": 64, "min_chunk": 128},
+            # achieved: KV bytes / duration of the whole layer call (prefix + combine kernels, HIP events
+            # on the launch stream); traffic: the prefix kernel's FETCH_SIZE + WRITE_SIZE bytes per launch
             "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": PEAK_GBS, "unit": "GB/s",
-                         "frac": round(head["GB_s"] / PEAK_GBS, 4), "traffic": None},
+                         "frac": round(head["GB_s"] / PEAK_GBS, 4), "traffic": read_traffic(ATTN_PROFILE)},
             "per_case": rows}
     if not args.no_cpu:
         line["cpu_baseline"] = attn_cpu_baseline()

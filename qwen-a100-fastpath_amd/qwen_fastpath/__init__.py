@@ -1,14 +1,13 @@
-"""qwen_fastpath on MI355X: the W8A16 decode GEMM behind QWEN_FAST_LINEAR and the int8 MTP draft head.
+"""qwen_fastpath on MI355X: the W8A16 decode GEMM behind QWEN_FAST_LINEAR, the int8 MTP draft head and
+the split-KV verification attention behind QWEN_FAST_ATTN.
 
 vLLM general plugin (entry point ``qwen_fastpath:register``, as plugin/qwen_fastpath/__init__.py:17-28
 in the reference).  Each patch can be switched off with an environment variable read once at
 register():
 
+  QWEN_FAST_ATTN=0        keep the original attention for speculative-decode verification batches
   QWEN_FAST_LINEAR=0      keep the original W8A8 path for small-batch (decode) int8 linears
   QWEN_FAST_DRAFT_HEAD=0  keep the bf16 lm_head for MTP draft proposals
-
-QWEN_FAST_ATTN (split-KV verification attention) is not provided by this package; the switch is
-accepted and ignored.
 """
 import logging
 import os
@@ -24,6 +23,7 @@ from .patches import (  # noqa: F401
     int8_logits,
     make_int8_head,
     patch_draft_lm_head,
+    patch_flash_attention,
     patch_int8_linear,
     qf_int8_linear,
     quantize_lm_head,
@@ -43,7 +43,7 @@ def register():
         return
     _registered = True
     if os.environ.get("QWEN_FAST_ATTN", "1") == "1":
-        logger.info("qwen_fastpath: QWEN_FAST_ATTN is not implemented by this package; attention unchanged")
+        patch_flash_attention()
     if os.environ.get("QWEN_FAST_LINEAR", "1") == "1":
         patch_int8_linear()
     if os.environ.get("QWEN_FAST_DRAFT_HEAD", "1") == "1":

@@ -1,4 +1,8 @@
-"""Plugin surface of the W8A16 decode path (reference: plugin/qwen_fastpath/patches.py:72-189).
+"""Plugin surface of the decode fast paths (reference: plugin/qwen_fastpath/patches.py:10-189).
+
+* ``patch_flash_attention`` -- routes uniform speculative-verification batches (every request has the
+  same 1 < Q <= 8 query tokens) of an eligible attention layer to the split-KV, GQA-packed kernel
+  (patches.py:10-69); everything else stays on the original forward.
 
 * ``qf_int8_linear`` -- the dispatcher op (patches.py:84-106): M <= 16 bf16 activations on an int8
   weight with stride(0) == 1 and one fp32 scale per output channel go to the HIP W8A16 kernel;
@@ -25,6 +29,119 @@ from . import _lib as L
 from .w8a16 import ROWMAJOR, SMALL_M, TILED, pick_config, to_tiled, w8a16_mm, w8a16_mm_prefill
 
 logger = logging.getLogger("vllm.qwen_fastpath")
+
+MAX_SPEC_QUERY_LEN = 8  # patches.py:7
+
+
+# ------------------------------------------------------------------------------------------------
+# verification attention (patches.py:10-69)
+# ------------------------------------------------------------------------------------------------
+
+def attn_switch_enabled() -> bool:
+    """QWEN_FAST_ATTN, default "1" (plugin/qwen_fastpath/__init__.py:23)."""
+    return os.environ.get("QWEN_FAST_ATTN", "1") == "1"
+
+
+def _interleaved_kv_split(kv_cache: torch.Tensor, head_size: int):
+    """The layer's cache as the reference reads it (patches.py:59): [blocks, H_kv, PAGE, 2D] with K
+    and V interleaved per row, viewed as two [blocks, PAGE, H_kv, D] tensors."""
+    return kv_cache.transpose(1, 2).split(head_size, dim=-1)
+
+
+def attn_impl_eligible(impl) -> bool:
+    """The reference's per-layer predicate (patches.py:24-44), evaluated once per layer object;
+    attributes a backend class does not define count as their neutral value."""
+    ok = getattr(impl, "_qf_eligible", None)
+    if ok is not None:
+        return ok
+    attn_type = getattr(impl, "attn_type", "decoder")
+    decoder = str(getattr(attn_type, "value", attn_type)).lower() == "decoder"
+    quantized = str(getattr(impl, "kv_cache_dtype", "auto")).startswith("fp8")
+    window = getattr(impl, "sliding_window", None)
+    ok = (decoder
+          and getattr(impl, "dcp_world_size", 1) == 1
+          and getattr(impl, "vllm_flash_attn_version", 2) == 2
+          and not getattr(impl, "fa4_hd256", False)
+          and (window is None or tuple(window) == (-1, -1))
+          and getattr(impl, "alibi_slopes", None) is None
+          and not getattr(impl, "logits_soft_cap", None)
+          and getattr(impl, "sinks", None) is None
+          and not quantized
+          and impl.num_heads % impl.num_kv_heads == 0
+          and impl.head_size in (64, 128, 256)
+          and getattr(impl, "kv_sharing_target_layer_name", None) is None)
+    impl._qf_eligible = ok
+    return ok
+
+
+def spec_batch_q_len(md) -> Optional[int]:
+    """Q when the metadata describes a uniform verification batch the kernel serves (patches.py:49-58),
+    else None."""
+    if md is None or getattr(md, "causal", True) is not True or getattr(md, "use_cascade", False):
+        return None
+    if getattr(md, "mm_prefix_query_range_tensor", None) is not None or getattr(md, "rswa_prefix_lens", None) is not None:
+        return None
+    q_len = int(md.max_query_len)
+    if not 1 < q_len <= MAX_SPEC_QUERY_LEN:
+        return None
+    num_reqs = md.query_start_loc.shape[0] - 1
+    if md.num_actual_tokens != num_reqs * q_len:  # uniform: every request has exactly q_len tokens
+        return None
+    return q_len
+
+
+def make_attention_forward(orig_forward: Callable, split_kv_cache: Callable = _interleaved_kv_split) -> Callable:
+    """Replacement for ``forward(self, layer, query, key, value, kv_cache, attn_metadata, output,
+    output_scale=None, output_block_scale=None)`` of an attention implementation class."""
+    from .spec_attn import gqa_packed_spec_attention, supported
+
+    def forward(self, layer, query, key, value, kv_cache, attn_metadata, output,
+                output_scale=None, output_block_scale=None):
+        md = attn_metadata
+        q_len = spec_batch_q_len(md) if output_scale is None and output_block_scale is None else None
+        if q_len is not None and attn_impl_eligible(self):
+            num_reqs = md.query_start_loc.shape[0] - 1
+            key_cache, value_cache = split_kv_cache(kv_cache, self.head_size)
+            q3 = query.view(query.shape[0], self.num_heads, self.head_size)
+            if supported(q3, key_cache, q_len, self.num_kv_heads):
+                o3 = output.view(output.shape[0], self.num_heads, self.head_size)
+                gqa_packed_spec_attention(q3, key_cache, value_cache, o3, md.seq_lens, md.block_table,
+                                          num_reqs, q_len, self.num_kv_heads, self.scale)
+                return output
+        return orig_forward(self, layer, query, key, value, kv_cache, attn_metadata, output,
+                            output_scale, output_block_scale)
+
+    forward._qwen_fastpath = True
+    return forward
+
+
+VLLM_ATTENTION_CLASSES = (
+    "vllm.v1.attention.backends.flash_attn:FlashAttentionImpl",
+)
+
+
+def patch_flash_attention(impl_cls=None, split_kv_cache: Callable = _interleaved_kv_split) -> bool:
+    """Install the verification-attention path on ``impl_cls`` (default: vLLM's FlashAttention
+    implementation, as the reference patches, patches.py:10-69).  Idempotent.  ``split_kv_cache(kv_cache,
+    head_size) -> (key_cache, value_cache)`` gives the [blocks, PAGE, H_kv, D] views of the layer's cache
+    (default: the reference's interleaved layout).  Returns False when no class could be patched."""
+    classes = [impl_cls] if impl_cls is not None else []
+    if impl_cls is None:
+        for path in VLLM_ATTENTION_CLASSES:
+            try:
+                classes.append(_import_attr(path))
+            except (ImportError, AttributeError):
+                continue
+    if not classes:
+        logger.info("qwen_fastpath: vLLM attention implementation not found; split-KV attention available as "
+                    "qwen_fastpath.gqa_packed_spec_attention only")
+        return False
+    for cls in classes:
+        orig = cls.forward
+        if not getattr(orig, "_qwen_fastpath", False):
+            cls.forward = make_attention_forward(orig, split_kv_cache)
+    logger.info("qwen_fastpath: split-KV GQA-packed attention enabled for speculative-decode verification")
+    return True
 
 
 def linear_switch_enabled() -> bool:
