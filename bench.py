@@ -478,20 +478,30 @@ def run_lm_head(torch, qf, dev, args):
     for M in (1, 4):
         hs = [torch.randn(M, H, device=dev, generator=g).to(torch.bfloat16) for _ in heads]
 
-        def step(i):
-            logits = qf.int8_logits(heads[i], hs[i])
-            return qf.top_tokens(logits, num_pad, 0)
+        def step(i):  # W8A16 logits, then the pad-masked argmax over them
+            return qf.int8_top_tokens(heads[i], hs[i], 0, fused=False)
+
+        def step_fused(i):  # argmax folded into the GEMM epilogue (logits neither written nor re-read)
+            return qf.int8_top_tokens(heads[i], hs[i], 0, fused=True)
         reps = 8
-        us = time_graph(torch, lambda: [step(i) for _ in range(reps) for i in range(len(heads))], reps * len(heads))
-        gemm = algo_bytes(M, V, H)
-        b = gemm + 2 * M * V + 8 * M  # the argmax reads the logits and writes M ids
-        rows[M] = {"us_per_draft_step": round(us, 2), "GB_s": round(b / us / 1e3, 1),
-                   "pct_peak": round(100 * b / us / 1e3 / PEAK_GBS, 1), "algorithmic_bytes": b}
-        log(f"  lm_head M={M}: {us:7.2f} us  {b / us / 1e3:7.0f} GB/s  {100 * b / us / 1e3 / PEAK_GBS:5.1f}%")
+        launches = reps * len(heads)
+        us, us2 = float("inf"), float("inf")
+        for _ in range(3):  # interleaved, the best of three each: the first graph timed after set-up runs slower
+            us = min(us, time_graph(torch, lambda: [step(i) for _ in range(reps) for i in range(len(heads))], launches))
+            us2 = min(us2, time_graph(torch, lambda: [step_fused(i) for _ in range(reps) for i in range(len(heads))],
+                                      launches))
+        b = algo_bytes(M, V, H) - 2 * M * V + 8 * M  # compulsory: weights, scales and x read, M ids written
+        best = us2  # int8_top_tokens' default: the fused epilogue
+        rows[M] = {"us_per_draft_step": round(best, 2), "GB_s": round(b / best / 1e3, 1),
+                   "pct_peak": round(100 * b / best / 1e3 / PEAK_GBS, 1), "algorithmic_bytes": b,
+                   "us_logits_then_argmax": round(us, 2), "us_fused_epilogue": round(us2, 2)}
+        log(f"  lm_head M={M}: logits + argmax {us:7.2f} us, argmax fused into the epilogue {us2:7.2f} us;"
+            f"  fused {b / best / 1e3:6.0f} GB/s  {100 * b / best / 1e3 / PEAK_GBS:5.1f}%")
     line = {"metric": METRIC, "value": rows[1]["GB_s"], "unit": "GB/s", "n_gpus": 1, "steps": 10, "warmup": 2,
             "ms_per_step": round(rows[1]["us_per_draft_step"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "bf16", "data": "synthetic (bf16 N(0,0.02) head quantised per row to int8)",
-            "config": {"workload": "int8 draft lm_head 151936x5120 + pad-masked argmax (value = M=1 GB/s)",
+            "config": {"workload": "int8 draft lm_head 151936x5120 plus the pad-masked argmax, ids out "
+                                   "(value = M=1 GB/s of compulsory bytes)",
                        "weight_layout": "tiled"},
             "per_m": rows}
     print(json.dumps(line), flush=True)

@@ -21,6 +21,7 @@
  *   qf_w8a16_workspace_bytes <- the fp32 split-K buffer torch.zeros   plugin/qwen_fastpath/w8a16.py:78-79
  *   qf_quantize_rows_int8    <- draft-head per-row quantizer   plugin/qwen_fastpath/patches.py:139-147
  *   qf_argmax_rows_bf16      <- pad mask + argmax of draft logits   plugin/qwen_fastpath/patches.py:182-185
+ *   qf_w8a16_gemm_argmax     <- draft logits + pad mask + argmax in one launch   patches.py:160-166,178-185
  *   qf_w8a16_repack / qf_w8a16_unpack: load-time weight layout change (no reference counterpart;
  *                              the reference streams the checkpoint layout as is, w8a16.py:1-7)
  */
@@ -110,6 +111,26 @@ int qf_w8a16_gemm(const uint16_t* x, int64_t ldx,
                   const qf_w8a16_config* cfg,
                   void* workspace, size_t workspace_bytes,
                   void* stream);
+
+/* Fused draft-head argmax: the product of qf_w8a16_gemm, and
+ *   ids[m] = index_offset + argmax_{n < n_valid} bf16(y[m, n])      (int64, m < M)
+ * with NaN counting as the maximum and ties going to the lowest index: the result of
+ * qf_argmax_rows_bf16 on the stored logits, without writing and re-reading them.  y may be NULL (no
+ * logits are stored); otherwise it is written as by qf_w8a16_gemm.  Each wavefront column of the GEMM
+ * leaves one candidate per token in the workspace and a second small launch folds them.  Served when
+ * the configuration is the MFMA kernel without a K split (else QF_ERR_UNSUPPORTED: call qf_w8a16_gemm
+ * and qf_argmax_rows_bf16).  Workspace: qf_w8a16_argmax_workspace_bytes() bytes, needing no clearing
+ * (the same buffer as a split-K workspace may serve: its counter prefix is not touched); calls that may
+ * run at the same time need distinct workspaces.  1 <= n_valid <= N.
+ * Reference: the W8A16 logits and the pad-masked argmax of get_top_tokens,
+ * plugin/qwen_fastpath/patches.py:160-166,178-185, in one launch. */
+int qf_w8a16_gemm_argmax(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int layout,
+                         const float* scale, void* y, int64_t ldy, int out_dtype, int M, int N, int K,
+                         int n_valid, int64_t index_offset, int64_t* ids, const qf_w8a16_config* cfg,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of qf_w8a16_gemm_argmax (0 when the fused argmax does not serve the shape). */
+size_t qf_w8a16_argmax_workspace_bytes(int M, int N, int K, int layout, const qf_w8a16_config* cfg);
 
 /* Size in bytes of the TILED image of an [N, K] weight (N rounded up to 16). */
 size_t qf_w8a16_tiled_bytes(int N, int K);

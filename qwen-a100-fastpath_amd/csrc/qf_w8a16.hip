@@ -60,6 +60,16 @@ struct GemmArgs {
   int out_f32;
   int vec_out;     // rows of y are 8-byte (bf16) / 16-byte (fp32) aligned: vector stores allowed
   int fused_reduce;  // MFMA, split_k > 1: the last workgroup of an n-block reduces (else a second kernel)
+  // Fused argmax (MFMA, split_k == 1): ids[m] = index_offset + argmax over n < n_valid of the bf16
+  // outputs y[m, n] (NaN highest, then value, then the lowest index); y may be null.  Each wavefront
+  // column writes its candidate per token as one (value bits | index << 32) record to
+  // am_cand[m * am_stride + column], columns = grid.x * WN; argmax_fold_kernel folds them.
+  int argmax;
+  int n_valid;
+  int am_stride;  // records per token row: the column count rounded up to even (16-byte pairs)
+  int64_t index_offset;
+  int64_t* ids;
+  uint64_t* am_cand;
 };
 
 // ---------------------------------------------------------------------------------------------
@@ -152,6 +162,23 @@ __device__ __forceinline__ f32x4_t load_scale4(const float* scale, int N, int n)
       if (n + i < N) s[i] = scale[n + i];
   }
   return s;
+}
+
+// Candidate order of the argmax: NaN is the maximum, then the larger value, then the lower index.
+__device__ __forceinline__ bool argmax_better(float av, int ai, float bv, int bi) {
+  const bool an = av != av, bn = bv != bv;
+  if (an != bn) return an;
+  if (an) return ai < bi;
+  if (av != bv) return av > bv;
+  return ai < bi;
+}
+
+// Better of two (value, index) candidates, folded into (bv, bi).
+__device__ __forceinline__ void argmax_fold(float v, int i, float& bv, int& bi) {
+  if (argmax_better(v, i, bv, bi)) {
+    bv = v;
+    bi = i;
+  }
 }
 
 // s_waitcnt immediate (gfx9 encoding) that waits for vmcnt == 0 and leaves expcnt / lgkmcnt free.
@@ -257,6 +284,114 @@ __device__ __forceinline__ void split_range(int split, int splits, int ksteps, i
 // of an n-block to finish (a per-n-block arrival counter in the workspace) sums the split_k partials
 // in split order, applies the scale and writes y, then resets the counter to zero.
 // ---------------------------------------------------------------------------------------------
+// bf16 rounding of an fp32 value, widened back (the value a bf16 output holds)
+__device__ __forceinline__ float bf16_value(float v) { return __uint_as_float((uint32_t)bf16_rne(v) << 16); }
+
+// Fused argmax epilogue of the MFMA kernel (split_k == 1).  Each lane ranks its scaled outputs (bf16
+// values, columns < n_valid) per token, the lanes of a token fold by shuffles, and each wavefront
+// column stores one candidate record per token; argmax_fold_kernel then folds the candidates.  Plain
+// stores, no barrier and no arrival counting: the workgroup leaves at once.
+template <int NT, int WN>
+__device__ __forceinline__ void argmax_epilogue(const GemmArgs& a, const f32x4_t (&acc)[NT], bool holder, int tile0,
+                                                int ntiles, int g, int wk, int wn, int lane) {
+  float bv = -__builtin_inff();
+  int bi = 0x7fffffff;
+  if (holder) {
+    const int r = lane & 15;
+    if (a.y != nullptr) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int tile = tile0 + t;
+        const int n = tile * kTileN + 4 * g;
+        if (tile < ntiles && n < a.N)
+          store_out4(a.y, a.ldy, a.out_f32, a.vec_out, r, n, min(4, a.N - n), acc[t] * load_scale4(a.scale, a.N, n));
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int tile = tile0 + t;
+      const int n = tile * kTileN + 4 * g;
+      if (tile < ntiles && n < a.n_valid) {
+        const f32x4_t v = acc[t] * load_scale4(a.scale, a.N, n);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (n + i < a.n_valid) argmax_fold(bf16_value(v[i]), n + i, bv, bi);
+      }
+    }
+  }
+  // lanes r, r + 16, r + 32, r + 48 hold token r's candidates
+#pragma unroll
+  for (int off = 16; off <= 32; off <<= 1) {
+    const float ov = __shfl_xor(bv, off);
+    const int oi = __shfl_xor(bi, off);
+    argmax_fold(ov, oi, bv, bi);
+  }
+  // every wavefront column stores its own candidate: no barrier, the workgroup leaves at once
+  if (wk == 0 && lane < a.M)
+    a.am_cand[(int64_t)lane * a.am_stride + (int64_t)blockIdx.x * WN + wn] =
+        (uint64_t)__float_as_uint(bv) | ((uint64_t)(uint32_t)bi << 32);
+}
+
+// Second pass of the fused argmax: one 1024-thread workgroup per token folds the token's ncand
+// candidate records (contiguous, 16-byte aligned row).  Each thread issues all its 16-byte pair loads
+// of a pass before it folds any (kFoldBatch pairs, 16384 records per pass), then a fixed butterfly and
+// an LDS tree.  argmax_better is a total order, so the result is that of a sequential scan.
+constexpr int kFoldThreads = 1024;
+constexpr int kFoldBatch = 8;
+
+__global__ void __launch_bounds__(kFoldThreads) argmax_fold_kernel(const uint64_t* cand, int ncand, int stride,
+                                                                   int64_t index_offset, int64_t* ids) {
+  __shared__ float sv[kFoldThreads / kWave];
+  __shared__ int si[kFoldThreads / kWave];
+  const int r = blockIdx.x;
+  const uint64_t* row = cand + (int64_t)r * stride;
+  float bv = -__builtin_inff();
+  int bi = 0x7fffffff;
+  const int npairs = ncand / 2;  // whole pairs; an odd last record is folded below
+  for (int base = threadIdx.x; base < npairs; base += kFoldThreads * kFoldBatch) {
+    u32x4_t p[kFoldBatch];  // (value, index) of two records
+#pragma unroll
+    for (int u = 0; u < kFoldBatch; ++u) {
+      const int e = base + u * kFoldThreads;
+      if (e < npairs) p[u] = *reinterpret_cast<const u32x4_t*>(row + 2 * e);
+    }
+#pragma unroll
+    for (int u = 0; u < kFoldBatch; ++u) {
+      if (base + u * kFoldThreads < npairs) {
+        argmax_fold(__uint_as_float(p[u][0]), (int)p[u][1], bv, bi);
+        argmax_fold(__uint_as_float(p[u][2]), (int)p[u][3], bv, bi);
+      }
+    }
+  }
+  if ((ncand & 1) && threadIdx.x == 0) {
+    const uint64_t rec = row[ncand - 1];
+    argmax_fold(__uint_as_float((uint32_t)rec), (int)(uint32_t)(rec >> 32), bv, bi);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(bv, off);
+    const int oi = __shfl_xor(bi, off);
+    argmax_fold(ov, oi, bv, bi);
+  }
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    sv[threadIdx.x / kWave] = bv;
+    si[threadIdx.x / kWave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x < kWave) {
+    const int w = threadIdx.x;
+    bv = w < kFoldThreads / kWave ? sv[w] : -__builtin_inff();
+    bi = w < kFoldThreads / kWave ? si[w] : 0x7fffffff;
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off);
+      const int oi = __shfl_xor(bi, off);
+      argmax_fold(ov, oi, bv, bi);
+    }
+    if (threadIdx.x == 0) ids[r] = (int64_t)bi + index_offset;
+  }
+}
+
 template <int LAYOUT, int NT, int WN, int WK, int DEPTH, bool NTH>
 __global__ void __launch_bounds__(WN * WK * kWave) w8a16_mfma_kernel(const GemmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
@@ -386,6 +521,10 @@ __global__ void __launch_bounds__(WN * WK * kWave) w8a16_mfma_kernel(const GemmA
   // Lane (g, r) of slice 0 holds C[n = tile*16 + 4g + i][m = r], i = 0..3.
   const bool holder = wk == 0 && tile0 < ntiles && r < a.M;
   if (a.split_k == 1) {
+    if (a.argmax) {
+      argmax_epilogue<NT, WN>(a, acc, holder, tile0, ntiles, g, wk, wn, lane);
+      return;
+    }
     if (holder) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
@@ -701,23 +840,7 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* w, i
 // Row argmax over bf16 logits (torch.argmax semantics: NaN is the maximum, first index on ties).
 // One workgroup per row.
 // ---------------------------------------------------------------------------------------------
-__device__ __forceinline__ bool argmax_better(float av, int ai, float bv, int bi) {
-  const bool an = av != av, bn = bv != bv;
-  if (an != bn) return an;
-  if (an) return ai < bi;
-  if (av != bv) return av > bv;
-  return ai < bi;
-}
-
 constexpr int kArgmaxThreads = 1024;
-
-// Better of two (value, index) candidates, folded into (bv, bi).
-__device__ __forceinline__ void argmax_fold(float v, int i, float& bv, int& bi) {
-  if (argmax_better(v, i, bv, bi)) {
-    bv = v;
-    bi = i;
-  }
-}
 
 // One workgroup of 1024 threads per row.  With VEC each thread reads 8 logits per 16-byte load,
 // four loads in flight, and walks each group in index order; the row tail (n_valid % 8) and
@@ -1180,6 +1303,97 @@ int launch(KernelFn fn, dim3 grid, dim3 block, size_t smem, hipStream_t stream, 
   return QF_OK;
 }
 
+struct ArgmaxRequest {
+  int n_valid;
+  int64_t index_offset;
+  int64_t* ids;
+};
+
+// Candidates of the fused argmax: one per (workgroup, wavefront column).
+size_t argmax_candidates(const qf_w8a16_config& c, int N) {
+  return (size_t)workgroups(c, N) * (size_t)(c.waves / c.k_waves);
+}
+
+// Records per token row of the fused argmax's candidate table (even: rows stay 16-byte aligned).
+size_t argmax_stride(const qf_w8a16_config& c, int N) { return (argmax_candidates(c, N) + 1) & ~(size_t)1; }
+
+// Workspace of the fused argmax: the counter prefix (unused here), then the [M][stride] records.
+size_t argmax_workspace_for(const qf_w8a16_config& c, int M, int N) {
+  return QF_W8A16_COUNTER_BYTES + argmax_stride(c, N) * (size_t)M * sizeof(uint64_t);
+}
+
+int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int layout, const float* scale, void* y,
+             int64_t ldy, int out_dtype, int M, int N, int K, const qf_w8a16_config* cfg, void* workspace,
+             size_t workspace_bytes, void* stream, const ArgmaxRequest* am) {
+  if (x == nullptr || w == nullptr || scale == nullptr) return QF_ERR_INVALID_ARG;
+  if (M < 1 || N < 1 || K < 1) return QF_ERR_INVALID_ARG;
+  if (layout != QF_LAYOUT_ROWMAJOR && layout != QF_LAYOUT_TILED) return QF_ERR_INVALID_ARG;
+  if (out_dtype != QF_DTYPE_BF16 && out_dtype != QF_DTYPE_F32) return QF_ERR_INVALID_ARG;
+  if (ldx < K || (y != nullptr && ldy < N) || (layout == QF_LAYOUT_ROWMAJOR && ldw < K)) return QF_ERR_INVALID_ARG;
+  if (M > QF_W8A16_MAX_M || K % QF_W8A16_K_ALIGN) return QF_ERR_UNSUPPORTED;
+  if (!aligned16(x) || !aligned16(w) || !aligned16(scale) || (y != nullptr && !aligned16(y))) return QF_ERR_UNSUPPORTED;
+  if (ldx % 8 || (layout == QF_LAYOUT_ROWMAJOR && ldw % 16)) return QF_ERR_UNSUPPORTED;
+
+  qf_w8a16_config c;
+  const int rc = resolve_config(M, N, K, layout, cfg, &c);
+  if (rc != QF_OK) return rc;
+  if (am != nullptr && (c.kernel != QF_KERNEL_MFMA || c.split_k != 1)) return QF_ERR_UNSUPPORTED;
+  const size_t need = am != nullptr ? argmax_workspace_for(c, M, N) : workspace_for(c, M, N);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))) return QF_ERR_WORKSPACE;
+
+  GemmArgs a;
+  a.x = x;
+  a.w = w;
+  a.scale = scale;
+  a.y = y;
+  a.counters = reinterpret_cast<unsigned*>(workspace);
+  a.partial = need > 0 && am == nullptr
+                  ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + QF_W8A16_COUNTER_BYTES)
+                  : nullptr;
+  a.ldx = ldx;
+  a.ldw = ldw;
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.n_pad = round_up16(N);
+  a.ksteps = K / kStepK;
+  a.split_k = c.split_k;
+  a.out_f32 = out_dtype == QF_DTYPE_F32;
+  a.vec_out = (ldy % 4) == 0;
+  a.fused_reduce = c.kernel == QF_KERNEL_MFMA && c.reduce == 0;
+  a.argmax = am != nullptr;
+  a.n_valid = am != nullptr ? am->n_valid : 0;
+  a.index_offset = am != nullptr ? am->index_offset : 0;
+  a.ids = am != nullptr ? am->ids : nullptr;
+  const size_t ncand = argmax_candidates(c, N);
+  a.am_stride = (int)argmax_stride(c, N);
+  a.am_cand = am != nullptr
+                  ? reinterpret_cast<uint64_t*>(reinterpret_cast<uint8_t*>(workspace) + QF_W8A16_COUNTER_BYTES)
+                  : nullptr;
+
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(workgroups(c, N), c.split_k);
+  const dim3 block(c.waves * kWave);
+  const size_t smem = lds_bytes(c, M, a.ksteps);
+  KernelFn fn = (c.kernel == QF_KERNEL_GEMV)
+                    ? select_gemv(M, c.tiles_per_wave, c.waves, c.load_hint)
+                    : select_mfma(layout, c.tiles_per_wave, c.waves, c.k_waves, c.depth, c.load_hint);
+  if (fn == nullptr) return QF_ERR_UNSUPPORTED;
+  int st = launch(fn, grid, block, smem, s, a);
+  if (st != QF_OK) return st;
+  if (am != nullptr) {
+    hipLaunchKernelGGL(argmax_fold_kernel, dim3(M), dim3(kFoldThreads), 0, s, a.am_cand, (int)ncand, a.am_stride,
+                       a.index_offset, a.ids);
+    return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
+  }
+  if (c.split_k > 1 && (c.kernel == QF_KERNEL_GEMV || !a.fused_reduce)) {
+    const int threads = M * (a.n_pad / 4);
+    st = launch(&splitk_reduce_kernel, dim3(ceil_div(threads, 256)), dim3(256), 0, s, a);
+  }
+  return st;
+}
+
 }  // namespace qf
 
 using namespace qf;
@@ -1218,57 +1432,26 @@ size_t qf_w8a16_tiled_bytes(int N, int K) {
 int qf_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int layout, const float* scale,
                   void* y, int64_t ldy, int out_dtype, int M, int N, int K, const qf_w8a16_config* cfg,
                   void* workspace, size_t workspace_bytes, void* stream) {
-  if (x == nullptr || w == nullptr || scale == nullptr || y == nullptr) return QF_ERR_INVALID_ARG;
-  if (M < 1 || N < 1 || K < 1) return QF_ERR_INVALID_ARG;
-  if (layout != QF_LAYOUT_ROWMAJOR && layout != QF_LAYOUT_TILED) return QF_ERR_INVALID_ARG;
-  if (out_dtype != QF_DTYPE_BF16 && out_dtype != QF_DTYPE_F32) return QF_ERR_INVALID_ARG;
-  if (ldx < K || ldy < N || (layout == QF_LAYOUT_ROWMAJOR && ldw < K)) return QF_ERR_INVALID_ARG;
-  if (M > QF_W8A16_MAX_M || K % QF_W8A16_K_ALIGN) return QF_ERR_UNSUPPORTED;
-  if (!aligned16(x) || !aligned16(w) || !aligned16(scale) || !aligned16(y)) return QF_ERR_UNSUPPORTED;
-  if (ldx % 8 || (layout == QF_LAYOUT_ROWMAJOR && ldw % 16)) return QF_ERR_UNSUPPORTED;
+  if (y == nullptr) return QF_ERR_INVALID_ARG;
+  return run_gemm(x, ldx, w, ldw, layout, scale, y, ldy, out_dtype, M, N, K, cfg, workspace, workspace_bytes, stream,
+                  nullptr);
+}
 
+size_t qf_w8a16_argmax_workspace_bytes(int M, int N, int K, int layout, const qf_w8a16_config* cfg) {
   qf_w8a16_config c;
-  const int rc = resolve_config(M, N, K, layout, cfg, &c);
-  if (rc != QF_OK) return rc;
-  const size_t need = workspace_for(c, M, N);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))) return QF_ERR_WORKSPACE;
+  if (resolve_config(M, N, K, layout, cfg, &c) != QF_OK) return 0;
+  if (c.kernel != QF_KERNEL_MFMA || c.split_k != 1) return 0;
+  return argmax_workspace_for(c, M, N);
+}
 
-  GemmArgs a;
-  a.x = x;
-  a.w = w;
-  a.scale = scale;
-  a.y = y;
-  a.counters = reinterpret_cast<unsigned*>(workspace);
-  a.partial = need > 0 ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + QF_W8A16_COUNTER_BYTES)
-                       : nullptr;
-  a.ldx = ldx;
-  a.ldw = ldw;
-  a.ldy = ldy;
-  a.M = M;
-  a.N = N;
-  a.K = K;
-  a.n_pad = round_up16(N);
-  a.ksteps = K / kStepK;
-  a.split_k = c.split_k;
-  a.out_f32 = out_dtype == QF_DTYPE_F32;
-  a.vec_out = (ldy % 4) == 0;
-  a.fused_reduce = c.kernel == QF_KERNEL_MFMA && c.reduce == 0;
-
-  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid(workgroups(c, N), c.split_k);
-  const dim3 block(c.waves * kWave);
-  const size_t smem = lds_bytes(c, M, a.ksteps);
-  KernelFn fn = (c.kernel == QF_KERNEL_GEMV)
-                    ? select_gemv(M, c.tiles_per_wave, c.waves, c.load_hint)
-                    : select_mfma(layout, c.tiles_per_wave, c.waves, c.k_waves, c.depth, c.load_hint);
-  if (fn == nullptr) return QF_ERR_UNSUPPORTED;
-  int st = launch(fn, grid, block, smem, s, a);
-  if (st != QF_OK) return st;
-  if (c.split_k > 1 && (c.kernel == QF_KERNEL_GEMV || !a.fused_reduce)) {
-    const int threads = M * (a.n_pad / 4);
-    st = launch(&splitk_reduce_kernel, dim3(ceil_div(threads, 256)), dim3(256), 0, s, a);
-  }
-  return st;
+int qf_w8a16_gemm_argmax(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int layout, const float* scale,
+                         void* y, int64_t ldy, int out_dtype, int M, int N, int K, int n_valid, int64_t index_offset,
+                         int64_t* ids, const qf_w8a16_config* cfg, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  if (ids == nullptr || n_valid < 1 || n_valid > N) return QF_ERR_INVALID_ARG;
+  ArgmaxRequest am{n_valid, index_offset, ids};
+  return run_gemm(x, ldx, w, ldw, layout, scale, y, ldy, out_dtype, M, N, K, cfg, workspace, workspace_bytes, stream,
+                  &am);
 }
 
 int qf_w8a16_repack(const int8_t* w_rowmajor, int64_t ldw, int8_t* w_tiled, int N, int K, void* stream) {

@@ -44,6 +44,8 @@ EXPORTS = (
     "qf_w8a16_dequant_bf16",
     "qf_quantize_rows_int8",
     "qf_argmax_rows_bf16",
+    "qf_w8a16_gemm_argmax",
+    "qf_w8a16_argmax_workspace_bytes",
     "qf_read_probe",
 )
 
@@ -120,6 +122,11 @@ def load() -> ctypes.CDLL:
     L.qf_quantize_rows_int8.restype = i32
     L.qf_argmax_rows_bf16.argtypes = [p, i64, i32, i32, i32, i64, p, p]
     L.qf_argmax_rows_bf16.restype = i32
+    L.qf_w8a16_gemm_argmax.argtypes = [p, i64, p, i64, i32, p, p, i64, i32, i32, i32, i32, i32, i64, p,
+                                       ctypes.POINTER(Config), p, sz, p]
+    L.qf_w8a16_gemm_argmax.restype = i32
+    L.qf_w8a16_argmax_workspace_bytes.argtypes = [i32, i32, i32, i32, ctypes.POINTER(Config)]
+    L.qf_w8a16_argmax_workspace_bytes.restype = sz
     L.qf_read_probe.argtypes = [p, sz, p, i32, p]
     L.qf_read_probe.restype = i32
     v = L.qf_abi_version()

@@ -178,6 +178,43 @@ def w8a16_mm(x: torch.Tensor, w_t: torch.Tensor, w_scale: torch.Tensor, cfg, out
     return torch.ops.qwen_fastpath.w8a16_mm(x, w_t, w_scale, int(layout), out_dtype, [int(v) for v in cfg])
 
 
+def w8a16_mm_argmax(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, n_valid: int, index_offset: int = 0,
+                    cfg=None, layout: int = ROWMAJOR, with_logits: bool = False):
+    """The draft head's argmax fused into the GEMM (the logits of w8a16_mm, then
+    index_offset + argmax over the first n_valid columns of the bf16 logits, NaN highest, first index on
+    ties: patches.py:160-166,178-185).  Returns the int64 ids [M] -- and the bf16 logits [M, N] when
+    with_logits -- or None when the fused path does not serve this configuration (the caller then uses
+    w8a16_mm and top_tokens)."""
+    lib = L.load()
+    if x.dim() != 2 or x.dtype != torch.bfloat16 or w_scale.dtype != torch.float32:
+        raise TypeError("x must be 2-D bf16 and w_scale fp32")
+    M, K = x.shape
+    N = w_scale.numel()
+    if not 1 <= n_valid <= N:
+        raise ValueError(f"n_valid must be in [1, {N}], got {n_valid}")
+    ldw = _weight_geometry(w, N, K, layout)
+    c = _config_struct(AUTO if cfg is None else cfg)
+    ws_bytes = int(lib.qf_w8a16_argmax_workspace_bytes(M, N, K, layout, ctypes.byref(c)))
+    if ws_bytes == 0:
+        return None
+    if x.stride(1) != 1 or x.data_ptr() % 16 or (M > 1 and x.stride(0) % 8):
+        x = x.contiguous()
+    ldx = x.stride(0) if M > 1 else K
+    s = w_scale.reshape(-1)
+    if not s.is_contiguous() or s.data_ptr() % 16:
+        s = s.clone(memory_format=torch.contiguous_format)
+    ids = torch.empty((M,), dtype=torch.int64, device=x.device)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device) if with_logits else None
+    ws = _workspace(x.device, ws_bytes)
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    rc = lib.qf_w8a16_gemm_argmax(x.data_ptr(), ldx, w.data_ptr(), ldw, layout, s.data_ptr(),
+                                  y.data_ptr() if y is not None else None, N, L.DTYPE_BF16, M, N, K, int(n_valid),
+                                  int(index_offset), ids.data_ptr(), ctypes.byref(c), ws.data_ptr(), ws.numel(),
+                                  stream)
+    L.check(rc, f"qf_w8a16_gemm_argmax(M={M}, N={N}, K={K}, layout={layout})")
+    return (ids, y) if with_logits else ids
+
+
 # ------------------------------------------------------------------------------------------------
 # weight layout
 # ------------------------------------------------------------------------------------------------

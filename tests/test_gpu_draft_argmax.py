@@ -1,0 +1,116 @@
+"""The draft head's argmax fused into the W8A16 kernel (qf_w8a16_gemm_argmax): the ids must equal the
+pad-masked argmax of the bf16 logits the plain kernel writes (plugin/qwen_fastpath/patches.py:178-185),
+and the oracle's argmax of those logits, bit for bit -- with planted ties (first index wins), a NaN
+row (NaN is the maximum), a winner planted in the pad columns (ignored), workgroup counts below and
+above one group of 64 with a ragged last group, repeated calls and graph replay."""
+import numpy as np
+import pytest
+import torch
+
+import qwen_fastpath as qf
+from qwen_fastpath import patches as P
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def _head(N, K, seed, plant=True):
+    g = torch.Generator(device=DEV)
+    g.manual_seed(seed)
+    w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=DEV, generator=g)
+    s = (torch.rand(N, device=DEV, generator=g) * 0.002 + 1e-4).float()
+    if plant:
+        w[7] = 127                     # a strong row ...
+        w[N // 2 + 3] = 127            # ... and an identical later row: the tie goes to row 7
+        s[N // 2 + 3] = s[7]
+        w[N - 2] = 127                 # a winner inside the pad columns (ignored when num_pad >= 2)
+        s[N - 2] = 1.0
+    return w, s
+
+
+def _ref_ids(y_bits, n_valid, offset, oracle):
+    return oracle.argmax_rows(y_bits, n_valid, offset)
+
+
+@pytest.mark.parametrize("layout", [qf.TILED, qf.ROWMAJOR])
+@pytest.mark.parametrize("M", [1, 2, 4, 7, 8, 12])
+@pytest.mark.parametrize("N,K", [(151936, 5120), (5000, 1024), (1000, 256)])
+def test_fused_ids_equal_unfused(oracle, layout, M, N, K):
+    w, s = _head(N, K, seed=N + M)
+    wt = w.t()
+    wl = qf.to_tiled(wt) if layout == qf.TILED else wt
+    g = torch.Generator(device=DEV)
+    g.manual_seed(M)
+    x = torch.rand(M, K, device=DEV, generator=g).to(torch.bfloat16)  # positive: row 7 is a clear maximum
+    x[M - 1] = torch.randn(K, device=DEV, generator=g).to(torch.bfloat16)  # a random row too
+    num_pad, offset = 64, 1234
+    y = qf.w8a16_mm(x, wl, s, None, torch.bfloat16, layout)
+    torch.cuda.synchronize()
+    ref = qf.top_tokens(y, num_pad, offset).cpu().numpy()
+    y_bits = y.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(ref, _ref_ids(y_bits, N - num_pad, offset, oracle))
+    for rep in range(2):  # the arrival counters are back at zero for the next call
+        res = qf.w8a16_mm_argmax(x, wl, s, N - num_pad, offset, None, layout, with_logits=True)
+        if res is None:  # configurations without the fused epilogue (GEMV, split K)
+            assert qf.w8a16_mm_argmax(x, wl, s, N - num_pad, offset, None, layout) is None
+            return
+        ids, y2 = res
+        torch.cuda.synchronize()
+        assert np.array_equal(ids.cpu().numpy(), ref), (rep, ids.cpu().numpy(), ref)
+        assert torch.equal(y2.view(torch.int16), y.view(torch.int16))
+        ids_only = qf.w8a16_mm_argmax(x, wl, s, N - num_pad, offset, None, layout)
+        assert np.array_equal(ids_only.cpu().numpy(), ref)
+
+
+def test_nan_row_and_all_pad_winner(oracle):
+    N, K, M = 3000, 512, 3
+    w, s = _head(N, K, seed=5, plant=False)
+    s[11] = float("nan")               # every logit of column 11 is NaN: NaN is the maximum
+    wl = qf.to_tiled(w.t())
+    x = torch.randn(M, K, device=DEV).to(torch.bfloat16)
+    ids = qf.w8a16_mm_argmax(x, wl, s, N, 0, None, qf.TILED)
+    assert ids is not None
+    assert ids.cpu().tolist() == [11] * M
+    ids = qf.w8a16_mm_argmax(x, wl, s, 11, 0, None, qf.TILED)   # NaN column excluded by n_valid
+    y = qf.w8a16_mm(x, wl, s, None, torch.bfloat16, qf.TILED)
+    ref = qf.top_tokens(y, N - 11, 0)
+    assert torch.equal(ids, ref)
+
+
+def test_graph_replay():
+    N, K, M = 151936, 5120, 1
+    w, s = _head(N, K, seed=3)
+    wl = qf.to_tiled(w.t())
+    x = torch.randn(M, K, device=DEV).to(torch.bfloat16)
+    eager = qf.w8a16_mm_argmax(x, wl, s, N - 64, 7, None, qf.TILED)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        qf.w8a16_mm_argmax(x, wl, s, N - 64, 7, None, qf.TILED)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = qf.w8a16_mm_argmax(x, wl, s, N - 64, 7, None, qf.TILED)
+    for i in range(3):
+        out.fill_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+
+
+def test_int8_top_tokens_matches_two_step(oracle):
+    V, H = 151936, 5120
+    wf = (torch.randn(V, H, device=DEV) * 0.02).to(torch.bfloat16)
+    head = P.make_int8_head(wf, num_pad=64)
+    del wf
+    for M in (1, 4):
+        hs = torch.randn(M, H, device=DEV).to(torch.bfloat16)
+        ids = P.int8_top_tokens(head, hs, 100)
+        dflt = P.int8_top_tokens(head, hs, 100, fused=False)
+        two = P.top_tokens(P.int8_logits(head, hs), 64, 100)
+        torch.cuda.synchronize()
+        assert torch.equal(ids, two) and torch.equal(dflt, two)
