@@ -17,7 +17,8 @@
  *      one tile, and the split's slice of the cached prefix [0, seq_len - q_len) is streamed once for
  *      all of them; the last active split also takes this step's q_len in-flight positions, masked
  *      causally per row; each split writes its normalised partial output and base-2 log-sum-exp;
- *   2. per (token, head): the row's partials are merged by log-sum-exp.
+ *   2. per (token, head, 64 d values): the row's partials are merged by log-sum-exp (a split that
+ *      holds no position has written log-sum-exp -inf for its rows, so every split is read).
  *
  * Layouts (strides in elements, the last dimension contiguous):
  *   query      bf16 [>= num_reqs * q_len, H, D]

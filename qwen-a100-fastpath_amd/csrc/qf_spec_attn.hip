@@ -19,11 +19,12 @@
 //     online softmax needs only two cross-lane steps per row, and the lane's 4 probabilities are
 //     already its B fragment of the next product.
 //   * O^T = V^T . P^T on v_mfma_f32_16x16x16_bf16 over the tile's 16 positions and the wavefront's
-//     half of the head dimension; V^T fragments are gathered from the LDS rows.
+//     half of the head dimension; each V^T fragment is one transposing LDS read (ds_read_b64_tr_b16)
+//     of the row-major V rows.
 //   * The two key tiles keep separate softmax states (the two wavefronts of a d half compute the same
 //     scores), merged once per split through LDS; wavefronts never exchange state inside the loop.
-//   combine kernel, one 256-thread workgroup per (token, head): the row's split partials are merged by
-//   log-sum-exp in thread groups, then the groups through LDS.
+//   combine kernel, one 256-thread workgroup per (token, head, 64 d values): the row's split partials
+//   are merged by log-sum-exp in thread groups, then the groups through LDS.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -95,6 +96,38 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
+// 32-bit LDS address of a pointer into the workgroup's LDS
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Transposing LDS read (gfx950 ds_read_b64_tr_b16).  Within each group of 16 lanes, lane i receives
+// word i % 4 of the 8 bytes addressed by lane 4 j + i / 4, for j = 0..3.  Issued as inline assembly
+// because the compiler treats the builtin's read as depending on every direct-to-LDS copy still in
+// flight and waits for all of them (vmcnt(0)) before it; here the copies a read depends on have
+// been waited for explicitly before the stage barrier.  The result is valid only after
+// wait_lds_all.
+__device__ __forceinline__ u32x2_t ds_read_tr16_b64(uint32_t addr) {
+  u32x2_t v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+// Waits for every outstanding LDS read of the wavefront; the N fragments are tied to the wait, so no
+// use of them is scheduled before it.
+template <int N>
+__device__ __forceinline__ void wait_lds_all(u32x2_t (&v)[N]) {
+  static_assert(N == 2 || N == 4 || N == 8, "fragment count");
+  if constexpr (N == 2) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]));
+  } else if constexpr (N == 4) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
+  } else {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
+  }
+}
+
 __device__ __forceinline__ float wave_max_q(float v) {  // over the 4 lanes l, l^16, l^32, l^48
   v = fmaxf(v, __shfl_xor(v, 16));
   return fmaxf(v, __shfl_xor(v, 32));
@@ -162,7 +195,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const int last_split = n_active > 0 ? n_active - 1 : 0;
   const int start = split * chunk;
   const int end = split == last_split ? seq : min(start + chunk, prefix);
-  if (split > last_split || start >= end) return;  // uniform: the whole workgroup leaves
+  if (split > last_split || start >= end) {
+    // no position here: the split's rows get log-sum-exp -inf, so the combine kernel can read every
+    // split without knowing the sequence length (uniform: the whole workgroup leaves)
+    const int64_t part = ((int64_t)blockIdx.y * a.splits + split) * a.R;
+    for (int r = threadIdx.x; r < a.R; r += kThreads) a.lse_part[part + r] = -__builtin_inff();
+    return;
+  }
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -200,6 +239,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     poff[j] = piece * 16;
     koff[j] = (uint32_t)(t * a.sk_t * 2) + poff[j];
     voff[j] = (uint32_t)(t * a.sv_t * 2) + poff[j];
+  }
+
+  // byte offsets (within a stage's V rows) of this lane's transposing reads, one per d tile
+  uint32_t vt_off[Gm::kDTiles];
+  {
+    const int n = kh * 16 + 4 * (lane >> 4) + ((lane >> 2) & 3);
+    const int q4 = lane & 3;
+#pragma unroll
+    for (int dt = 0; dt < Gm::kDTiles; ++dt) {
+      const int d = (dh * Gm::kDTiles + dt) * 16 + 4 * q4;
+      vt_off[dt] = (uint32_t)(n * Gm::kRowBytes + (((d >> 3) ^ Gm::swz(n)) << 4) + (d & 7) * 2);
+    }
   }
 
   // online softmax state: m_ref is the row's exponent reference, moved only when a score exceeds it
@@ -352,22 +403,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
         pf[rt] = __builtin_bit_cast(s16x4_t, u32x2_t{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3])});
       }
 
-      // O^T += V^T P^T over this wavefront's d half and key tile (k slot 4 qg + i = position 4 qg + i)
+      // O^T += V^T P^T over this wavefront's d half and key tile (k slot 4 qg + i = position 4 qg + i).
+      // The V^T fragment of a d tile comes from one transposing LDS read: lane 16 g + 4 j + q points at
+      // the 8 bytes of row 4 g + j holding d values d0 + 4 q .. d0 + 4 q + 3, and the read hands lane
+      // 16 g + i the values V[4 g + j][d0 + i], j = 0..3.
+      u32x2_t vf[Gm::kDTiles];
+      const uint32_t vs_lds = lds_addr(vs);
+#pragma unroll
+      for (int dt = 0; dt < Gm::kDTiles; ++dt) vf[dt] = ds_read_tr16_b64(vs_lds + vt_off[dt]);
+      wait_lds_all<Gm::kDTiles>(vf);
 #pragma unroll
       for (int dt = 0; dt < Gm::kDTiles; ++dt) {
-        const int d = (dh * Gm::kDTiles + dt) * 16 + l16;
-        const int dpiece = d >> 3;
-        const int dbyte = (d & 7) * 2;
-        uint32_t h[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int n = kh * 16 + qg * 4 + i;
-          h[i] = *reinterpret_cast<const uint16_t*>(vs + n * Gm::kRowBytes + ((dpiece ^ Gm::swz(n)) << 4) + dbyte);
-        }
-        const s16x4_t vf = __builtin_bit_cast(s16x4_t, u32x2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)});
+        const s16x4_t a_frag = __builtin_bit_cast(s16x4_t, vf[dt]);
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
-          o_acc[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pf[rt], o_acc[rt][dt], 0, 0, 0);
+          o_acc[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a_frag, pf[rt], o_acc[rt][dt], 0, 0, 0);
       }
     }
     wait_vmcnt<0>();
@@ -421,17 +471,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   }
 }
 
-// One (token, head) row per workgroup: the row's split partials merged by log-sum-exp (the merge of
-// the reference's _suffix_combine_kernel, spec_attn.py:119-131).
+// One workgroup per (token, head, 64-wide slice of d): the row's split partials merged by log-sum-exp
+// (the merge of the reference's _suffix_combine_kernel, spec_attn.py:119-131).  Every split has
+// written its rows' log-sum-exp (-inf where it saw nothing), so all loads issue at once, with no
+// dependence on the sequence length; 16 groups of 16 threads merge every 16th split, then LDS merges
+// the groups.
+constexpr int kCombSlice = 64;  // d values per combine workgroup
+
 template <int D>
 __global__ __launch_bounds__(kThreads) void spec_combine_kernel(AttnArgs a) {
-  constexpr int NQ = D / 4;          // threads per group, 4 d values each
+  constexpr int NQ = kCombSlice / 4;  // threads per group, 4 d values each
   constexpr int NGRP = kThreads / NQ;
-  constexpr int kBatch = 16;         // parts a thread loads before merging them
+  constexpr int kBatch = 4;           // parts a thread loads before merging them
   __shared__ float sm_m[NGRP], sm_l[NGRP];
-  __shared__ __align__(16) float sm_acc[NGRP][D];
+  __shared__ __align__(16) float sm_acc[NGRP][kCombSlice];
 
   const int row = blockIdx.x;
+  const int d0 = blockIdx.y * kCombSlice;
   const int tok = row / a.H;
   const int h = row - tok * a.H;
   const int b = tok / a.Q;
@@ -441,33 +497,26 @@ __global__ __launch_bounds__(kThreads) void spec_combine_kernel(AttnArgs a) {
   const int grp = threadIdx.x / NQ;
   const int dq = threadIdx.x - grp * NQ;
 
-  const int seq = a.seq_lens[b];
-  const int prefix = seq - a.Q > 0 ? seq - a.Q : 0;
-  const int chunk = split_chunk(prefix, a.splits, a.min_chunk);
-  const int n_active = prefix > 0 ? (prefix + chunk - 1) / chunk : 0;
-  // the in-flight positions ride with the last active split (split 0 when the prefix is empty)
-  const int n_list = n_active > 0 ? n_active : (seq > 0 ? 1 : 0);
-
   float m = -__builtin_inff(), l = 0.f;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   const int64_t part0 = ((int64_t)(b * a.HKV + hkv) * a.splits) * a.R + r;
   // group grp merges the parts grp, grp + NGRP, ...
-  for (int base = grp; base < n_list; base += NGRP * kBatch) {
+  for (int base = grp; base < a.splits; base += NGRP * kBatch) {
     float e[kBatch];
     f32x4_t o[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int i = base + u * NGRP;
       e[u] = -__builtin_inff();
-      if (i < n_list) {
+      if (i < a.splits) {
         const int64_t idx = part0 + (int64_t)i * a.R;
         e[u] = a.lse_part[idx];
-        o[u] = *reinterpret_cast<const f32x4_t*>(a.o_part + idx * D + dq * 4);
+        o[u] = *reinterpret_cast<const f32x4_t*>(a.o_part + idx * D + d0 + dq * 4);
       }
     }
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      if (e[u] == -__builtin_inff()) continue;  // an absent part, or a row that saw no position
+      if (e[u] == -__builtin_inff()) continue;  // a split with no position, or a row that saw none
       const float mn = fmaxf(m, e[u]);
       const float c_old = fast_exp2(m - mn);
       const float w = fast_exp2(e[u] - mn);
@@ -498,7 +547,7 @@ __global__ __launch_bounds__(kThreads) void spec_combine_kernel(AttnArgs a) {
     }
   }
   const float inv = lt > 0.f ? 1.f / lt : 0.f;  // a row that sees no position is written as zeros
-  *reinterpret_cast<u32x2_t*>(a.out + (int64_t)tok * a.so_t + (int64_t)h * a.so_h + dq * 4) =
+  *reinterpret_cast<u32x2_t*>(a.out + (int64_t)tok * a.so_t + (int64_t)h * a.so_h + d0 + dq * 4) =
       u32x2_t{pack_bf16(at[0] * inv, at[1] * inv), pack_bf16(at[2] * inv, at[3] * inv)};
 }
 
@@ -635,7 +684,7 @@ int qf_spec_attention(const uint16_t* query, int64_t q_stride_tok, int64_t q_str
   if (pre == nullptr) return QF_ERR_UNSUPPORTED;
   int st = launch(pre, dim3(num_splits, num_reqs * num_kv_heads), lds, s, a);
   if (st != QF_OK) return st;
-  return launch(comb, dim3(num_reqs * q_len * num_heads), 0, s, a);
+  return launch(comb, dim3(num_reqs * q_len * num_heads, head_size / kCombSlice), 0, s, a);
 }
 
 }  // extern "C"

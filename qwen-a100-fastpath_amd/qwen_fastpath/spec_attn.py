@@ -6,7 +6,8 @@
 ``out``.  Query qi of request b attends cached positions [0, seq_lens[b] - Q + qi]; this step's K/V
 must already be in the cache.  The work runs in libqf_spec_attn.so (hand-written HIP for gfx950):
 one launch streams each kv head's cached prefix once for the Q*G query rows sharing it, split across
-workgroups, and a second attends the in-flight positions and merges by log-sum-exp.  Both grids are
+workgroups (the last split also attends this step's in-flight positions, causally per row), and a
+second merges the split partials by log-sum-exp.  Both grids are
 fixed for a batch shape and nothing is read back to the host, so the call can be captured in a HIP
 graph (its split workspace comes from torch's caching allocator, as the reference's does).
 """
@@ -18,10 +19,26 @@ from . import _attn_lib as AL
 
 LOG2E = 1.4426950408889634
 
-# Defaults of the reference's call (spec_attn.py:136).  block_n / num_warps / num_stages /
-# combine_warps are Triton launch knobs there; the HIP kernels have fixed shapes and ignore them.
-DEFAULT_NUM_SPLITS = 64
+# Defaults of the reference's call (spec_attn.py:136), except num_splits: the reference fixes 64 (for
+# an A100's 108 SMs); here None picks one prefix workgroup per compute unit, CUs // (num_reqs *
+# num_kv_heads) splits (64 for one request with 4 kv heads on MI355X's 256 CUs).  A prefix workgroup
+# holds a whole CU (128 KiB of LDS, one wavefront per SIMD), so a grid larger than the CU count runs
+# in two rounds: at 2 requests and 38K context, 32 splits take 64.7 us and 64 take 71.7 us.
+# block_n / num_warps / num_stages / combine_warps are Triton launch knobs there; the HIP kernels
+# have fixed shapes and ignore them.
+DEFAULT_NUM_SPLITS = None
 DEFAULT_MIN_CHUNK = 128
+
+_cu_count: dict = {}
+
+
+def auto_num_splits(device: torch.device, num_reqs: int, num_kv_heads: int) -> int:
+    """Prefix splits that give one workgroup per compute unit of `device` (at least 1)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    n = _cu_count.get(idx)
+    if n is None:
+        n = _cu_count[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return max(1, n // max(1, int(num_reqs) * int(num_kv_heads)))
 
 
 def _check_bf16_rows(t: torch.Tensor, name: str):
@@ -48,7 +65,8 @@ def gqa_packed_spec_attention(query, key_cache, value_cache, out, seq_lens, bloc
                               scale, num_splits=DEFAULT_NUM_SPLITS, min_chunk=DEFAULT_MIN_CHUNK, block_n=32,
                               num_warps=4, num_stages=2, combine_warps=2):
     """query/out [>= num_reqs*Q, H, D] bf16; key_cache/value_cache [num_blocks, PAGE, H_kv, D] bf16 (strided
-    views are fine); seq_lens int32 [num_reqs]; block_table int32 [num_reqs, max_blocks].  Returns out."""
+    views are fine); seq_lens int32 [num_reqs]; block_table int32 [num_reqs, max_blocks].  num_splits None:
+    one prefix workgroup per compute unit.  Returns out."""
     del block_n, num_warps, num_stages, combine_warps
     for t, n in ((query, "query"), (key_cache, "key_cache"), (value_cache, "value_cache"), (out, "out")):
         _check_bf16_rows(t, n)
@@ -65,6 +83,8 @@ def gqa_packed_spec_attention(query, key_cache, value_cache, out, seq_lens, bloc
     if query.shape[0] < B * Q or out.shape[0] < B * Q or seq_lens.numel() < B or block_table.shape[0] < B:
         raise ValueError("batch tensors are smaller than num_reqs * Q")
     page = key_cache.shape[1]
+    if num_splits is None:
+        num_splits = auto_num_splits(query.device, B, num_kv_heads)
     L = AL.load()
     ws_bytes = AL.workspace_bytes(B, Q, H, num_kv_heads, D, num_splits)
     if ws_bytes == 0:
