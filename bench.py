@@ -157,7 +157,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--workload", choices=["layer", "stack64", "msweep", "lm_head", "prefill", "spec_attn"],
+    ap.add_argument("--workload", choices=["layer", "stack64", "msweep", "lm_head", "prefill", "spec_attn", "tp8"],
                     default="layer")
     ap.add_argument("--layers", type=int, default=4, help="distinct layers rotated through (layer workload)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -224,6 +224,9 @@ def main():
         return
     if args.workload == "spec_attn":
         run_spec_attn(torch, qf, dev, args)
+        return
+    if args.workload == "tp8":
+        run_tp8(torch, qf, dev, args)
         return
 
     M = M_TOKENS
@@ -460,6 +463,54 @@ def run_prefill(torch, qf, dev, args):
             "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded int8 weights, fp32 scales, bf16 activations)",
             "config": {"workload": "gate_up 34816x5120 prefill widths on TILED weights (value = M=2048 TFLOP/s)"},
             "per_m": rows}
+    print(json.dumps(line), flush=True)
+
+
+# One tensor-parallel rank's share of the layer at TP = 8: qkv and gate_up split N (column-parallel), o_proj
+# and down split K (row-parallel; the all-reduce that would follow them is not part of this measurement).
+TP8_GEMMS = {"qkv": (1280, 5120), "o_proj": (5120, 1024), "gate_up": (4352, 5120), "down": (5120, 2176)}
+
+
+def run_tp8(torch, qf, dev, args):
+    """The layer's four GEMMs at M=5 on one TP=8 rank's shapes, TILED weights, 16 layers rotated (726 MB)."""
+    layout = qf.TILED if args.layout == "tiled" else qf.ROWMAJOR
+    M, R = M_TOKENS, 16
+    g = torch.Generator(device=dev)
+    g.manual_seed(17)
+    layers = []
+    for _ in range(R):
+        sets = {}
+        for name, (N, K) in TP8_GEMMS.items():
+            w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g).t()
+            sets[name] = (qf.to_tiled(w) if layout == qf.TILED else w,
+                          (torch.randn(N, device=dev, generator=g).abs() * 0.002 + 1e-4).float(),
+                          torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16))
+            del w
+        layers.append(sets)
+
+    def gemm(sets, name):
+        w, s_, x = sets[name]
+        return qf.w8a16_mm(x, w, s_, None, torch.bfloat16, layout)
+
+    rows = {}
+    for name, (N, K) in TP8_GEMMS.items():
+        us = time_graph(torch, lambda n=name: [gemm(L_, n) for _ in range(8) for L_ in layers], 8 * R)
+        b = algo_bytes(M, N, K)
+        rows[name] = {"N": N, "K": K, "us": round(us, 2), "GB_s": round(b / us / 1e3, 1),
+                      "pct_peak": round(100 * b / us / 1e3 / PEAK_GBS, 1),
+                      "config": list(qf.resolve_config(M, N, K, layout))}
+        log(f"  tp8 {name:8s} N={N:5d} K={K:5d}: {us:6.2f} us  {b / us / 1e3:6.0f} GB/s  {100 * b / us / 1e3 / PEAK_GBS:5.1f}%")
+    us_layer = time_graph(torch, lambda: [gemm(L_, n) for _ in range(4) for L_ in layers for n in TP8_GEMMS], 4 * R)
+    b_layer = sum(algo_bytes(M, N, K) for N, K in TP8_GEMMS.values())
+    log(f"  tp8 layer step (4 GEMMs): {us_layer:6.2f} us  {b_layer / us_layer / 1e3:6.0f} GB/s  "
+        f"{100 * b_layer / us_layer / 1e3 / PEAK_GBS:5.1f}%")
+    line = {"metric": METRIC, "value": round(b_layer / us_layer / 1e3, 1), "unit": "GB/s", "n_gpus": 1, "steps": 10,
+            "warmup": 2, "ms_per_step": round(us_layer / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded int8 weights, fp32 scales, bf16 activations)",
+            "config": {"workload": "one TP=8 rank's layer GEMMs at M=5 (qkv 1280x5120, o_proj 5120x1024, "
+                                   "gate_up 4352x5120, down 5120x2176), 16 layers rotated; no all-reduce",
+                       "weight_layout": args.layout},
+            "per_gemm": rows}
     print(json.dumps(line), flush=True)
 
 

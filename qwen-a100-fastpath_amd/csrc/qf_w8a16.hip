@@ -1262,6 +1262,17 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
       if (validate_config(M, N, K, layout, tc) == QF_OK) *c = tc;
     }
   }
+  // Few workgroups (narrow N, such as one tensor-parallel rank's shard): 4-wavefront workgroups run
+  // twice as many, each stream being latency-bound at this size, and 8 steps in flight once a
+  // wavefront has 16 or more (TP = 8 shards at M = 5: o_proj 5120x1024 4.0 us against 5.0, down
+  // 5120x2176 5.1 us against 6.6, qkv 1280x5120 6.4 us against 6.9; gate_up 4352x5120, 136
+  // workgroups of 8 wavefronts, stays: 7.5 us against 8.2).
+  if (c->waves == 8 && (int64_t)workgroups(*c, N) * c->split_k < 128) {
+    qf_w8a16_config tc = *c;
+    tc.waves = 4;
+    if (ksteps / tc.split_k / tc.k_waves >= 16) tc.depth = 8;
+    if (validate_config(M, N, K, layout, tc) == QF_OK) *c = tc;
+  }
   // The fused reduction needs one arrival counter per workgroup column.
   if (c->split_k > 1 && (size_t)workgroups(*c, N) * 4 > QF_W8A16_COUNTER_BYTES) c->reduce = 1;
   return validate_config(M, N, K, layout, *c) == QF_OK;
