@@ -141,3 +141,18 @@ def test_unsupported_shapes_raise():
     out = torch.empty_like(q)
     with pytest.raises(QFError):  # 3 * 32 packed rows > 64
         qf.gqa_packed_spec_attention(q.repeat(1, 8, 1), kc, vc, out.repeat(1, 8, 1), sl, bt, 1, 3, 2, 0.125)
+
+
+def test_default_split_count_is_one_workgroup_per_cu():
+    import torch
+    from qwen_fastpath import spec_attn as SA
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    assert SA.auto_num_splits(dev, 1, 4) == max(1, cus // 4)
+    assert SA.auto_num_splits(dev, 2, 4) == max(1, cus // 8)
+    assert SA.auto_num_splits(dev, cus, 8) == 1
+    inp = A.gen_spec_inputs(7000, 3, 2, seed=31)
+    auto = _run(inp)
+    explicit = _run(inp, num_splits=max(1, cus // (2 * inp.HKV)))
+    assert np.array_equal(auto.view(np.uint32), explicit.view(np.uint32))
+    _check(inp, auto, "default splits")
