@@ -129,6 +129,21 @@ def test_layer_shapes_m5_full_size(oracle, name):
     assert rel <= oracle.REL_MAX_TOL and rel <= 1e-5
 
 
+# One tensor-parallel rank's shards at TP = 8: qkv and gate_up split N, o_proj and down split K.
+TP8 = {"qkv": (1280, 5120), "o_proj": (5120, 1024), "gate_up": (4352, 5120), "down": (5120, 2176)}
+
+
+@pytest.mark.parametrize("name", list(TP8))
+def test_tp8_rank_shapes_tiled(oracle, name):
+    """The auto shapes for few workgroups (4-wavefront workgroups, DEPTH 8 on longer k ranges) on TILED weights."""
+    N, K = TP8[name]
+    inp = oracle.gen_inputs(5, N, K, seed=8)
+    x, w, s = dev_inputs(inp, DEV)
+    cfg = qf.resolve_config(5, N, K, qf.TILED)
+    y = run(x, qf.to_tiled(w), s, layout=qf.TILED)
+    check(oracle, inp, bf16_bits(y), label=f"tp8 {name} M=5 tiled cfg={tuple(cfg)}")
+
+
 def test_single_linear_m1(oracle):
     inp = oracle.gen_inputs(1, 5120, 5120, seed=0)
     x, w, s = dev_inputs(inp, DEV)
