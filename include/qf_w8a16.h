@@ -63,7 +63,9 @@ typedef enum qf_dtype { QF_DTYPE_BF16 = 0, QF_DTYPE_F32 = 1 } qf_dtype;
 typedef enum qf_kernel {
   QF_KERNEL_AUTO = 0,  /* pick by shape and M */
   QF_KERNEL_GEMV = 1,  /* wavefront-reduction GEMV, M <= 4, row-major layout only */
-  QF_KERNEL_MFMA = 2   /* v_mfma_f32_16x16x32_bf16 tiles, M <= 16, both layouts */
+  QF_KERNEL_MFMA = 2,  /* v_mfma_f32_16x16x32_bf16 tiles, M <= 16, both layouts */
+  QF_KERNEL_MFMA_XRING = 3  /* the same tiles with x staged in (depth + 1)-step chunks through a
+                               two-slot LDS ring instead of whole; k_waves must be 1 */
 } qf_kernel;
 
 /* Launch configuration.  A zero field means "choose automatically". */

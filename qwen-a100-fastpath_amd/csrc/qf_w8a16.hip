@@ -392,7 +392,7 @@ __global__ void __launch_bounds__(kFoldThreads) argmax_fold_kernel(const uint64_
   }
 }
 
-template <int LAYOUT, int NT, int WN, int WK, int DEPTH, bool NTH>
+template <int LAYOUT, int NT, int WN, int WK, int DEPTH, bool NTH, bool XRING>
 __global__ void __launch_bounds__(WN * WK * kWave) w8a16_mfma_kernel(const GemmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ int last_arrival;
@@ -434,18 +434,19 @@ __global__ void __launch_bounds__(WN * WK * kWave) w8a16_mfma_kernel(const GemmA
     }
   }
 
-  // Prologue: the x slice of the workgroup (all WK k-slices) is requested first, then the first
-  // DEPTH steps of weights; writing x to LDS waits only for the x requests (vmcnt retires in issue
-  // order), so the weight requests stay in flight across the barrier.
   // Every weight load in this kernel is unconditional: step indices past the slice are clamped to its
   // last step (an in-bounds re-read of a line just fetched) and their math is skipped.  Keeping
   // branches away from the loads lets the compiler keep DEPTH steps of loads in flight.
   // The ring has DEPTH + 1 slots: at step s the load for step s + DEPTH goes into the slot freed at
-  // step s - 1, so it can be issued before step s's fragment is consumed.
-  const int pitch = x_pitch(wg_steps);
-  XStage<WAVES * kWave> xst(a, s_begin, wg_steps);
+  // step s - 1, so it can be issued before step s's fragment is consumed.  In both x staging modes
+  // the x requests go out first, then the first DEPTH steps of weights; writing x to LDS waits only
+  // for the x requests (vmcnt retires in issue order), so the weight requests stay in flight across
+  // the barriers.
   constexpr int RING = DEPTH + 1;
   u32x4_t buf[RING][NT];
+  f32x4_t acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
   auto prologue = [&]() {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
@@ -454,50 +455,103 @@ __global__ void __launch_bounds__(WN * WK * kWave) w8a16_mfma_kernel(const GemmA
       for (int t = 0; t < NT; ++t) buf[d][t] = load16<NTH>(wp[t] + sd * step_bytes);
     }
   };
-  if (xst.single_batch()) {  // uniform
-    xst.load_batch(a, 0);
+  // One k-step: request the weights DEPTH steps ahead into the slot freed by the previous step, then
+  // (for steps of the slice) dequantise ring slot d and multiply by the x fragments at xp.
+  auto step = [&](int s, int d, const uint8_t* xp) {
+    const int sn = min(s + DEPTH, nsteps - 1);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) buf[(d + DEPTH) % RING][t] = load16<NTH>(wp[t] + (int64_t)sn * step_bytes);
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch issue ahead of this step's math
+    if (s < nsteps) {                   // uniform: steps past the slice only keep loads in flight
+      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(xp);
+      const bf16x8_t xb0 = __builtin_bit_cast(bf16x8_t, p[0]);
+      const bf16x8_t xb1 = __builtin_bit_cast(bf16x8_t, p[1]);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        bf16x8_t w0, w1;
+        dequant16(buf[d][t], w0, w1);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, xb0, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, xb1, acc[t], 0, 0, 0);
+      }
+    }
+  };
+  // Lane (g, r) reads x[r][k + 16g .. +15] of each step.  Lanes of token rows r >= M read row M - 1
+  // instead: MFMA column r only feeds output column r, which is never stored.
+  const int xr = min(r, a.M - 1);
+
+  if constexpr (!XRING) {
+    // The workgroup's whole x slice (all WK k-slices) is staged once, before the first step.
+    const int pitch = x_pitch(wg_steps);
+    XStage<WAVES * kWave> xst(a, s_begin, wg_steps);
+    if (xst.single_batch()) {  // uniform
+      xst.load_batch(a, 0);
+      __builtin_amdgcn_sched_barrier(0);  // the x requests go out before the weight requests
+      prologue();
+      __builtin_amdgcn_sched_barrier(0);
+      xst.store_batch(smem, 0);
+    } else {
+      xst.copy_all(a, smem);
+      prologue();
+    }
+    lds_barrier();  // the weight requests issued above stay in flight across it
+    const uint8_t* xs = smem + xr * pitch + (k_lo * kStepK + 16 * g) * 2;
+    constexpr int xs_stride = kStepK * 2 * WK;
+    for (int base = 0; base < nsteps; base += RING) {
+#pragma unroll
+      for (int d = 0; d < RING; ++d) step(base + d, d, xs + (size_t)(base + d) * xs_stride);
+    }
+  } else {
+    // x through a two-slot LDS ring (k_waves == 1, so a wavefront's steps are the workgroup's): chunk
+    // c holds steps [c RING, (c + 1) RING) of every token row, and block c of the loop computes them.
+    // Each thread requests its pieces of chunk c + 1 into registers at the start of block c and
+    // writes them to the other slot at the start of block c + 1, before the barrier that opens it;
+    // the slot is free because every wavefront passed that barrier after finishing block c - 1.
+    // Only a RING-step chunk is staged before the first step, instead of the whole slice.
+    static_assert(WK == 1, "the x ring serves one k-slice per workgroup");
+    constexpr int THREADS = WAVES * kWave;
+    constexpr int CP = RING * 8;                               // 16-byte pieces per token row of a chunk
+    constexpr int XP = (QF_W8A16_MAX_M * CP + THREADS - 1) / THREADS;  // pieces per thread, at most
+    constexpr int SWM = CP % 16 == 0 ? 7 : 3;                  // the row swizzle stays inside the row
+    const int cpieces = a.M * CP;
+    const int slot_bytes = cpieces * 16;
+    // Every wavefront runs every block, including one whose tiles lie past N (nsteps == 1): the
+    // block barriers must match across the workgroup, and its threads stage their share of x.
+    const int nchunks = (k_count + RING - 1) / RING;
+    const int64_t kmax = (int64_t)s_end * kStepK - 8;          // last 8-element piece of the range
+    u32x4_t xv[XP];
+    // Piece q of a chunk lies at LDS byte 16 q and holds row m = q / CP, piece (q % CP) ^ sw(m) of
+    // the row's steps: the XOR moves the rows' fragment reads onto different banks, as the +32-byte
+    // row pitch of the whole-slice layout does.  Pieces past the chunk are clamped to its last piece.
+    auto load_chunk = [&](int c) {
+#pragma unroll
+      for (int j = 0; j < XP; ++j) {
+        const int q = min(j * THREADS + (int)threadIdx.x, cpieces - 1);
+        const int m = q / CP;
+        const int jx = (q - m * CP) ^ ((m & SWM) << 1);
+        const int64_t k = min((int64_t)(s_begin + c * RING) * kStepK + jx * 8, kmax);
+        xv[j] = *reinterpret_cast<const u32x4_t*>(a.x + (int64_t)m * a.ldx + k);
+      }
+    };
+    auto store_chunk = [&](int c) {
+      uint8_t* slot = smem + (c & 1) * slot_bytes;
+#pragma unroll
+      for (int j = 0; j < XP; ++j)
+        *reinterpret_cast<u32x4_t*>(slot + min(j * THREADS + (int)threadIdx.x, cpieces - 1) * 16) = xv[j];
+    };
+    load_chunk(0);
     __builtin_amdgcn_sched_barrier(0);  // the x requests go out before the weight requests
     prologue();
     __builtin_amdgcn_sched_barrier(0);
-    xst.store_batch(smem, 0);
-  } else {
-    xst.copy_all(a, smem);
-    prologue();
-  }
-  lds_barrier();  // the weight requests issued above stay in flight across it
-
-  f32x4_t acc[NT];
+    store_chunk(0);
+    const int xsw = (xr & SWM) << 1;
+    for (int c = 0; c < nchunks; ++c) {
+      if (c > 0) store_chunk(c);
+      lds_barrier();  // the weight requests stay in flight across it
+      if (c + 1 < nchunks) load_chunk(c + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      const uint8_t* xrow = smem + (c & 1) * slot_bytes + xr * (CP * 16);
 #pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-
-  {
-    // Lane (g, r) reads x[r][k + 16g .. +15] of each step.  Lanes of token rows r >= M read row M - 1
-    // instead: MFMA column r only feeds output column r, which is never stored.
-    const int xr = min(r, a.M - 1);
-    const uint8_t* xs = smem + xr * pitch + (k_lo * kStepK + 16 * g) * 2;
-    constexpr int xs_stride = kStepK * 2 * WK;
-
-    for (int base = 0; base < nsteps; base += RING) {
-#pragma unroll
-      for (int d = 0; d < RING; ++d) {
-        const int s = base + d;
-        const int sn = min(s + DEPTH, nsteps - 1);
-#pragma unroll
-        for (int t = 0; t < NT; ++t) buf[(d + DEPTH) % RING][t] = load16<NTH>(wp[t] + (int64_t)sn * step_bytes);
-        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch issue ahead of this step's math
-        if (s < nsteps) {                   // uniform: steps past the slice only keep loads in flight
-          const u32x4_t* p = reinterpret_cast<const u32x4_t*>(xs + (size_t)s * xs_stride);
-          const bf16x8_t xb0 = __builtin_bit_cast(bf16x8_t, p[0]);
-          const bf16x8_t xb1 = __builtin_bit_cast(bf16x8_t, p[1]);
-#pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            bf16x8_t w0, w1;
-            dequant16(buf[d][t], w0, w1);
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, xb0, acc[t], 0, 0, 0);
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, xb1, acc[t], 0, 0, 0);
-          }
-        }
-      }
+      for (int d = 0; d < RING; ++d) step(c * RING + d, d, xrow + (((d * 8 + 2 * g) ^ xsw) << 4));
     }
   }
 
@@ -1038,36 +1092,46 @@ __global__ void __launch_bounds__(256) read_probe_kernel(const u32x4_t* buf, int
 // ---------------------------------------------------------------------------------------------
 using KernelFn = void (*)(GemmArgs);
 
-// MFMA instantiations: layout x NT {1, 2} x (WN, WK) x DEPTH {4, 8} x load hint.
-template <int L, int NT, int WN, int WK>
+// MFMA instantiations: layout x NT {1, 2} x (WN, WK) x DEPTH {4, 8} x load hint, whole-slice x
+// staging; the x-ring staging for the k_waves == 1 shapes.
+template <int L, int NT, int WN, int WK, bool XR>
 KernelFn mfma_fn(int depth, int hint) {
-  if (depth == 4) return hint ? &w8a16_mfma_kernel<L, NT, WN, WK, 4, true> : &w8a16_mfma_kernel<L, NT, WN, WK, 4, false>;
-  if (depth == 8) return hint ? &w8a16_mfma_kernel<L, NT, WN, WK, 8, true> : &w8a16_mfma_kernel<L, NT, WN, WK, 8, false>;
+  if (depth == 4)
+    return hint ? &w8a16_mfma_kernel<L, NT, WN, WK, 4, true, XR> : &w8a16_mfma_kernel<L, NT, WN, WK, 4, false, XR>;
+  if (depth == 8)
+    return hint ? &w8a16_mfma_kernel<L, NT, WN, WK, 8, true, XR> : &w8a16_mfma_kernel<L, NT, WN, WK, 8, false, XR>;
   return nullptr;
 }
 
 template <int L, int NT>
-KernelFn mfma_by_shape(int wn, int wk, int depth, int hint) {
+KernelFn mfma_by_shape(int wn, int wk, int depth, int hint, bool xring) {
+  if (xring) {
+    if (wn == 4 && wk == 1) return mfma_fn<L, NT, 4, 1, true>(depth, hint);
+    if (wn == 8 && wk == 1) return mfma_fn<L, NT, 8, 1, true>(depth, hint);
+    return nullptr;
+  }
 #define QF_WNWK(A, B) \
-  if (wn == A && wk == B) return mfma_fn<L, NT, A, B>(depth, hint);
+  if (wn == A && wk == B) return mfma_fn<L, NT, A, B, false>(depth, hint);
   QF_WNWK(4, 1) QF_WNWK(8, 1) QF_WNWK(2, 2) QF_WNWK(4, 2) QF_WNWK(8, 2)
   QF_WNWK(1, 4) QF_WNWK(2, 4) QF_WNWK(4, 4) QF_WNWK(1, 8) QF_WNWK(2, 8)
 #undef QF_WNWK
   return nullptr;
 }
 
-KernelFn select_mfma(int layout, int nt, int waves, int k_waves, int depth, int hint) {
+KernelFn select_mfma(int layout, int nt, int waves, int k_waves, int depth, int hint, bool xring) {
   if (k_waves < 1 || waves % k_waves) return nullptr;
   const int wn = waves / k_waves;
   if (layout == QF_LAYOUT_ROWMAJOR) {
-    if (nt == 1) return mfma_by_shape<QF_LAYOUT_ROWMAJOR, 1>(wn, k_waves, depth, hint);
-    if (nt == 2) return mfma_by_shape<QF_LAYOUT_ROWMAJOR, 2>(wn, k_waves, depth, hint);
+    if (nt == 1) return mfma_by_shape<QF_LAYOUT_ROWMAJOR, 1>(wn, k_waves, depth, hint, xring);
+    if (nt == 2) return mfma_by_shape<QF_LAYOUT_ROWMAJOR, 2>(wn, k_waves, depth, hint, xring);
   } else {
-    if (nt == 1) return mfma_by_shape<QF_LAYOUT_TILED, 1>(wn, k_waves, depth, hint);
-    if (nt == 2) return mfma_by_shape<QF_LAYOUT_TILED, 2>(wn, k_waves, depth, hint);
+    if (nt == 1) return mfma_by_shape<QF_LAYOUT_TILED, 1>(wn, k_waves, depth, hint, xring);
+    if (nt == 2) return mfma_by_shape<QF_LAYOUT_TILED, 2>(wn, k_waves, depth, hint, xring);
   }
   return nullptr;
 }
+
+inline bool is_mfma(int kernel) { return kernel == QF_KERNEL_MFMA || kernel == QF_KERNEL_MFMA_XRING; }
 
 template <int MM, int RPW>
 KernelFn gemv_fn(int hint) {
@@ -1103,7 +1167,8 @@ inline int round_up16(int n) { return (n + 15) / 16 * 16; }
 size_t lds_bytes(const qf_w8a16_config& c, int M, int ksteps) {
   const int steps = ceil_div(ksteps, c.split_k);
   if (c.kernel == QF_KERNEL_GEMV) return (size_t)M * steps * kStepK * 2;
-  const size_t xs = (size_t)M * x_pitch(steps);
+  const size_t xs = c.kernel == QF_KERNEL_MFMA_XRING ? (size_t)2 * M * (c.depth + 1) * kStepK * 2  // two chunks
+                                                     : (size_t)M * x_pitch(steps);
   const size_t red = c.k_waves > 1 ? (size_t)c.waves * c.tiles_per_wave * kWave * sizeof(f32x4_t) : 0;
   return xs > red ? xs : red;
 }
@@ -1124,18 +1189,19 @@ size_t workspace_for(const qf_w8a16_config& c, int M, int N) {
 // Checks a complete configuration against the instantiated kernels and the LDS budget.
 int validate_config(int M, int N, int K, int layout, const qf_w8a16_config& c) {
   const int ksteps = K / kStepK;
-  if (c.kernel != QF_KERNEL_GEMV && c.kernel != QF_KERNEL_MFMA) return QF_ERR_INVALID_ARG;
+  if (c.kernel != QF_KERNEL_GEMV && !is_mfma(c.kernel)) return QF_ERR_INVALID_ARG;
   if (c.split_k < 1 || c.split_k > ksteps || c.waves < 1 || c.k_waves < 1 || c.tiles_per_wave < 1)
     return QF_ERR_INVALID_ARG;
   if (c.kernel == QF_KERNEL_GEMV && (M > 4 || layout != QF_LAYOUT_ROWMAJOR || c.k_waves != 1))
     return QF_ERR_UNSUPPORTED;
   if (ksteps / c.split_k < c.k_waves) return QF_ERR_UNSUPPORTED;  // every k-slice needs a step
-  if (c.kernel == QF_KERNEL_MFMA && c.split_k > 1 && c.reduce == 0 &&
+  if (c.kernel == QF_KERNEL_MFMA_XRING && c.k_waves != 1) return QF_ERR_UNSUPPORTED;
+  if (is_mfma(c.kernel) && c.split_k > 1 && c.reduce == 0 &&
       (size_t)workgroups(c, N) * 4 > QF_W8A16_COUNTER_BYTES)
     return QF_ERR_UNSUPPORTED;  // one arrival counter per workgroup column
   if (lds_bytes(c, M, ksteps) > kMaxLds) return QF_ERR_UNSUPPORTED;
-  if (c.kernel == QF_KERNEL_MFMA &&
-      select_mfma(layout, c.tiles_per_wave, c.waves, c.k_waves, c.depth, c.load_hint) == nullptr)
+  if (is_mfma(c.kernel) && select_mfma(layout, c.tiles_per_wave, c.waves, c.k_waves, c.depth, c.load_hint,
+                                       c.kernel == QF_KERNEL_MFMA_XRING) == nullptr)
     return QF_ERR_UNSUPPORTED;
   if (c.kernel == QF_KERNEL_GEMV && select_gemv(M, c.tiles_per_wave, c.waves, c.load_hint) == nullptr)
     return QF_ERR_UNSUPPORTED;
@@ -1193,6 +1259,14 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
     // M = 13 K is split so that the slice stays near 56 KiB (M = 16: 39.7 us against 54 us).
     c->tiles_per_wave = 2;
     c->k_waves = 1;
+    if (M <= 14) {
+      // x through the two-slot ring, unsplit: only a 5-step chunk is staged before the first step
+      // (gate_up M = 8 34.1 us, 12 34.6 us, 14 35.0 us against 35.3, 36.2 and 36.5 us staging the
+      // whole slice; at M = 16 the split whole-slice shape stays ahead, 39.5 us against 39.9 us).
+      c->kernel = QF_KERNEL_MFMA_XRING;
+      c->split_k = 1;
+      return validate_config(M, N, K, layout, *c) == QF_OK;
+    }
     c->split_k = M >= 13 ? ceil_div((int)((int64_t)M * K * 2), 56 * 1024) : 1;
     if (c->split_k > ksteps) c->split_k = ksteps;
     while (lds_bytes(*c, M, ksteps) > kMaxLds && c->split_k < ksteps) ++c->split_k;
@@ -1242,6 +1316,9 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
       c->waves = 4;  // row-major o_proj M = 16: 14.3 us against 15.3 us
       c->k_waves = 1;
     }
+    // one k-slice per workgroup on TILED weights: x through the two-slot ring (M = 12: qkv 14.0 us,
+    // down 20.3 us against 14.3 and 21.3 us; M = 16: 14.3 and 21.0 us against 14.7 and 21.5 us)
+    if (layout == QF_LAYOUT_TILED && c->k_waves == 1) c->kernel = QF_KERNEL_MFMA_XRING;
     c->reduce = 1;
     while (lds_bytes(*c, M, ksteps) > kMaxLds && c->split_k < ksteps) ++c->split_k;
     return validate_config(M, N, K, layout, *c) == QF_OK;
@@ -1348,7 +1425,7 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
   qf_w8a16_config c;
   const int rc = resolve_config(M, N, K, layout, cfg, &c);
   if (rc != QF_OK) return rc;
-  if (am != nullptr && (c.kernel != QF_KERNEL_MFMA || c.split_k != 1)) return QF_ERR_UNSUPPORTED;
+  if (am != nullptr && (!is_mfma(c.kernel) || c.split_k != 1)) return QF_ERR_UNSUPPORTED;
   const size_t need = am != nullptr ? argmax_workspace_for(c, M, N) : workspace_for(c, M, N);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))) return QF_ERR_WORKSPACE;
 
@@ -1372,7 +1449,7 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
   a.split_k = c.split_k;
   a.out_f32 = out_dtype == QF_DTYPE_F32;
   a.vec_out = (ldy % 4) == 0;
-  a.fused_reduce = c.kernel == QF_KERNEL_MFMA && c.reduce == 0;
+  a.fused_reduce = is_mfma(c.kernel) && c.reduce == 0;
   a.argmax = am != nullptr;
   a.n_valid = am != nullptr ? am->n_valid : 0;
   a.index_offset = am != nullptr ? am->index_offset : 0;
@@ -1389,7 +1466,8 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
   const size_t smem = lds_bytes(c, M, a.ksteps);
   KernelFn fn = (c.kernel == QF_KERNEL_GEMV)
                     ? select_gemv(M, c.tiles_per_wave, c.waves, c.load_hint)
-                    : select_mfma(layout, c.tiles_per_wave, c.waves, c.k_waves, c.depth, c.load_hint);
+                    : select_mfma(layout, c.tiles_per_wave, c.waves, c.k_waves, c.depth, c.load_hint,
+                                  c.kernel == QF_KERNEL_MFMA_XRING);
   if (fn == nullptr) return QF_ERR_UNSUPPORTED;
   int st = launch(fn, grid, block, smem, s, a);
   if (st != QF_OK) return st;
@@ -1451,7 +1529,7 @@ int qf_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, 
 size_t qf_w8a16_argmax_workspace_bytes(int M, int N, int K, int layout, const qf_w8a16_config* cfg) {
   qf_w8a16_config c;
   if (resolve_config(M, N, K, layout, cfg, &c) != QF_OK) return 0;
-  if (c.kernel != QF_KERNEL_MFMA || c.split_k != 1) return 0;
+  if (!is_mfma(c.kernel) || c.split_k != 1) return 0;
   return argmax_workspace_for(c, M, N);
 }
 

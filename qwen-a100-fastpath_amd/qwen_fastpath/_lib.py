@@ -27,6 +27,7 @@ DTYPE_F32 = 1
 KERNEL_AUTO = 0
 KERNEL_GEMV = 1
 KERNEL_MFMA = 2
+KERNEL_MFMA_XRING = 3
 
 MAX_M = 16
 K_ALIGN = 64

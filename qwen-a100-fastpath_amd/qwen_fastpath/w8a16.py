@@ -28,8 +28,9 @@ TILED = L.LAYOUT_TILED
 
 class W8A16Config(NamedTuple):
     """Launch configuration; zero fields are chosen by the library for the call's M (see
-    qf_w8a16_pick_config).  kernel: 0 auto, 1 gemv (M <= 4), 2 mfma.  waves = wavefronts per
-    workgroup, of which k_waves split K inside the workgroup (MFMA); reduce (MFMA, split_k > 1):
+    qf_w8a16_pick_config).  kernel: 0 auto, 1 gemv (M <= 4), 2 mfma, 3 mfma with x staged in
+    chunks through a two-slot LDS ring (k_waves 1).  waves = wavefronts per workgroup, of which
+    k_waves split K inside the workgroup (MFMA); reduce (MFMA, split_k > 1):
     0 = the last workgroup of each n-block sums the splits, 1 = a second kernel does."""
 
     kernel: int = 0

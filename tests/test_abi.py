@@ -49,7 +49,7 @@ def test_pick_config_supported_and_lds_bounded(M):
     for (N, K) in ((10240, 5120), (5120, 8192), (34816, 5120), (5120, 17408), (151936, 5120), (100, 64)):
         c = L.pick_config(M, N, K)
         assert c is not None
-        assert c.kernel in (L.KERNEL_GEMV, L.KERNEL_MFMA)
+        assert c.kernel in (L.KERNEL_GEMV, L.KERNEL_MFMA, L.KERNEL_MFMA_XRING)
         ksteps = K // 64
         assert 1 <= c.split_k <= ksteps
         steps = -(-ksteps // c.split_k)

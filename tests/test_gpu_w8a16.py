@@ -68,6 +68,42 @@ def test_mfma_configs(oracle, nt, wn, wk, depth, hint):
         check(oracle, inp, outs[(sk, qf.ROWMAJOR)], label=f"mfma nt={nt} wn={wn} wk={wk} d={depth} h={hint} sk={sk}")
 
 
+XRING_CFGS = [(nt, wn, d, h) for nt in (1, 2) for wn in (4, 8) for d in (4, 8) for h in (0, 1)]
+
+
+@pytest.mark.parametrize("nt,wn,depth,hint", XRING_CFGS)
+def test_mfma_xring_configs(oracle, nt, wn, depth, hint):
+    """x staged through the two-slot LDS ring: the oracle's tolerance, and bit for bit the result of the
+    whole-slice kernel with the same shape (same products, same order), at M = 1, 5 and 16."""
+    for M in (1, 5, 16):
+        N, K = 1040, 5120
+        inp = oracle.gen_inputs(M, N, K, seed=M * 100 + nt * 10 + wn + depth + hint)
+        x, w, s = dev_inputs(inp, DEV)
+        wt = qf.to_tiled(w)
+        for sk in (1, 3):
+            ring = qf.W8A16Config(L.KERNEL_MFMA_XRING, sk, nt, wn, depth, hint, 1)
+            staged = qf.W8A16Config(L.KERNEL_MFMA, sk, nt, wn, depth, hint, 1)
+            for layout, ww in ((qf.ROWMAJOR, w), (qf.TILED, wt)):
+                y = bf16_bits(run(x, ww, s, ring, layout))
+                check(oracle, inp, y, label=f"xring M={M} nt={nt} wn={wn} d={depth} h={hint} sk={sk} layout={layout}")
+                try:
+                    y2 = bf16_bits(run(x, ww, s, staged, layout))
+                except L.QFError:  # the whole slice does not fit in LDS
+                    continue
+                assert np.array_equal(y, y2), (M, sk, layout)
+
+
+def test_xring_unsplit_where_the_whole_slice_does_not_fit(oracle):
+    """M = 16 over K = 17408 unsplit: the whole x slice (557 KiB) exceeds LDS, the ring needs 20 KiB."""
+    M, N, K = 16, 512, 17408
+    inp = oracle.gen_inputs(M, N, K, seed=99)
+    x, w, s = dev_inputs(inp, DEV)
+    with pytest.raises(L.QFError):
+        run(x, w, s, qf.W8A16Config(L.KERNEL_MFMA, 1, 2, 8, 4, 1, 1), qf.ROWMAJOR)
+    y = bf16_bits(run(x, qf.to_tiled(w), s, qf.W8A16Config(L.KERNEL_MFMA_XRING, 1, 2, 8, 4, 1, 1), qf.TILED))
+    check(oracle, inp, y, label="xring M=16 K=17408 unsplit")
+
+
 def test_fused_split_k_counters_return_to_zero(oracle):
     """Every split-K call leaves the arrival counters at the front of the workspace at zero, so the
     persistent workspace serves the next call: repeated calls give identical, correct results."""
