@@ -659,7 +659,7 @@ def run_spec_attn(torch, qf, dev, args):
             "ms_per_step": round(head["us"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "bf16", "data": "synthetic (N(0,1) bf16 queries and KV cache, shuffled pages)",
             "config": {"workload": "one full-attention layer, H=24 H_kv=4 D=256, 800-position pages; value = "
-                                   "ctx 38000, Q=3, 1 request", "num_splits": "auto: CUs / (requests x kv heads) (64 at 1 request)", "min_chunk": 128},
+                                   "ctx 38000, Q=3, 1 request", "num_splits": "auto: CUs / (requests x kv heads) (64 at 1 request)", "min_chunk": 64},
             # achieved: KV bytes / duration of the whole layer call (prefix + combine kernels, HIP events
             # on the launch stream); traffic: the prefix kernel's FETCH_SIZE + WRITE_SIZE bytes per launch
             "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": PEAK_GBS, "unit": "GB/s",

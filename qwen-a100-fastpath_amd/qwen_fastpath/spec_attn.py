@@ -19,15 +19,18 @@ from . import _attn_lib as AL
 
 LOG2E = 1.4426950408889634
 
-# Defaults of the reference's call (spec_attn.py:136), except num_splits: the reference fixes 64 (for
-# an A100's 108 SMs); here None picks one prefix workgroup per compute unit, CUs // (num_reqs *
-# num_kv_heads) splits (64 for one request with 4 kv heads on MI355X's 256 CUs).  A prefix workgroup
-# holds a whole CU (128 KiB of LDS, one wavefront per SIMD), so a grid larger than the CU count runs
-# in two rounds: at 2 requests and 38K context, 32 splits take 64.7 us and 64 take 71.7 us.
+# Defaults of the reference's call (spec_attn.py:136), except two sizes:
+# * num_splits: the reference fixes 64 (for an A100's 108 SMs); here None picks one prefix workgroup
+#   per compute unit, CUs // (num_reqs * num_kv_heads) splits (64 for one request with 4 kv heads on
+#   MI355X's 256 CUs).  A prefix workgroup holds a whole CU (128 KiB of LDS, one wavefront per SIMD),
+#   so a grid larger than the CU count runs in two rounds: at 2 requests and 38K context, 32 splits
+#   take 64.7 us and 64 take 71.7 us.
+# * min_chunk: 64 positions instead of 128, so that short contexts spread over more workgroups (one
+#   request: 1K context 12.4 us against 14.3 us, 2K 13.1 against 14.7 us; no change from 8K on).
 # block_n / num_warps / num_stages / combine_warps are Triton launch knobs there; the HIP kernels
 # have fixed shapes and ignore them.
 DEFAULT_NUM_SPLITS = None
-DEFAULT_MIN_CHUNK = 128
+DEFAULT_MIN_CHUNK = 64
 
 _cu_count: dict = {}
 
