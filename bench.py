@@ -463,7 +463,30 @@ def run_prefill(torch, qf, dev, args):
             "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded int8 weights, fp32 scales, bf16 activations)",
             "config": {"workload": "gate_up 34816x5120 prefill widths on TILED weights (value = M=2048 TFLOP/s)"},
             "per_m": rows}
+    if not args.no_cpu:
+        line["cpu_baseline"] = prefill_cpu_baseline()
     print(json.dumps(line), flush=True)
+
+
+def prefill_cpu_baseline(M: int = 2048, N: int = 2048, K: int = 5120):
+    """The oracle's fp32-dequant restatement of the reference CPU path (bench/test_w8a16.py:15) at a
+    prefill width, on an N-channel slice of gate_up, best of 3, in TFLOP/s."""
+    from oracle import oracle as O
+    cores = max(1, min(len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1), 16))
+    try:
+        from threadpoolctl import threadpool_limits
+        threadpool_limits(limits=cores)
+    except Exception:  # noqa: BLE001 - threadpoolctl optional
+        pass
+    inp = O.gen_inputs(M, N, K, seed=6)
+    best = float("inf")
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.fp32_dequant_linear(inp.x, inp.w, inp.s)
+        best = min(best, time.perf_counter() - t0)
+    return {"value": round(2.0 * M * N * K / best / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"M={M} over a {N}-channel slice of gate_up (K={K}), fp32 dequant linear, best of 3 over "
+                      f"{cores} threads: {best * 1e3:.1f} ms"}
 
 
 # One tensor-parallel rank's share of the layer at TP = 8: qkv and gate_up split N (column-parallel), o_proj
@@ -514,6 +537,31 @@ def run_tp8(torch, qf, dev, args):
     print(json.dumps(line), flush=True)
 
 
+def lm_head_cpu_baseline(M: int = 1, rows: int = 16384, H: int = 5120):
+    """The reference's draft-head path on the host (patches.py:160-166,178-185 in the oracle's fp32-dequant
+    form): logits = x . (w * s)^T in fp32, rounded to bf16, the pad columns masked, argmax.  Timed on a
+    vocabulary slice of `rows` rows, best of 3, as GB/s of the slice's compulsory bytes."""
+    import numpy as np
+    from oracle import oracle as O
+    cores = max(1, min(len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1), 16))
+    try:
+        from threadpoolctl import threadpool_limits
+        threadpool_limits(limits=cores)
+    except Exception:  # noqa: BLE001 - threadpoolctl optional
+        pass
+    inp = O.gen_inputs(M, rows, H, seed=5)
+    best = float("inf")
+    for _ in range(3):
+        t0 = time.perf_counter()
+        logits = O.fp32_dequant_linear(inp.x, inp.w, inp.s)
+        O.argmax_rows(O.bf16_from_f64(logits.astype(np.float64)), rows - 64, 0)
+        best = min(best, time.perf_counter() - t0)
+    b = rows * H + 4 * rows + 2 * M * H + 8 * M
+    return {"value": round(b / best / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"M={M}, a {rows}-row slice of the 151936x5120 head ({b / 1e6:.1f} MB), fp32 dequant linear + "
+                      f"bf16 rounding + pad mask + argmax, best of 3 over {cores} threads: {best * 1e3:.1f} ms"}
+
+
 def run_lm_head(torch, qf, dev, args):
     """Int8 MTP draft head: V=151936, H=5120, at M = 1 and 4.  One step = W8A16 logits for M hidden rows
     plus the pad-masked argmax (64 pad columns, vocab offset 0); weights rotate over 2 copies (1.56 GB)."""
@@ -555,6 +603,8 @@ def run_lm_head(torch, qf, dev, args):
                                    "(value = M=1 GB/s of compulsory bytes)",
                        "weight_layout": "tiled"},
             "per_m": rows}
+    if not args.no_cpu:
+        line["cpu_baseline"] = lm_head_cpu_baseline(1)
     print(json.dumps(line), flush=True)
 
 
