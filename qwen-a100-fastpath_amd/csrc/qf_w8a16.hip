@@ -1253,25 +1253,17 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
   // stay contiguous however many tiles a wavefront holds (row-major gate_up at M = 8: 63 us with this
   // shape against 42 us without)
   if (M >= 8 && layout == QF_LAYOUT_TILED && wide_n) {
-    // Wide M and N: the staged x slice grows with M, so a workgroup covers more weight rows per
-    // staged byte -- 8 tile groups of 2 tiles, each wavefront over the whole K range of its split
-    // (gate_up: M = 8 35.0 us, M = 12 36.5 us against 44 and 48 us with the M = 5 shape); from
-    // M = 13 K is split so that the slice stays near 56 KiB (M = 16: 39.7 us against 54 us).
+    // Wide M and N: a workgroup covers more weight rows per x byte -- 8 tile groups of 2 tiles, each
+    // wavefront over the whole K range (gate_up: M = 8 35.0 us, M = 12 36.5 us against 44 and 48 us
+    // with the M = 5 shape) -- and x goes through the two-slot ring with K unsplit: only a 5-step
+    // chunk is staged before the first step, and LDS holds two chunks instead of the whole slice
+    // (interleaved A/B against staging the whole slice: M = 8 34.1 us against 35.3, M = 12 34.6
+    // against 36.2, and, where the slice needed a 3-way K split to fit, M = 13 35.1 against 38.2 and
+    // M = 16 35.4 against 39.3 us).
     c->tiles_per_wave = 2;
     c->k_waves = 1;
-    if (M <= 14) {
-      // x through the two-slot ring, unsplit: only a 5-step chunk is staged before the first step
-      // (gate_up M = 8 34.1 us, 12 34.6 us, 14 35.0 us against 35.3, 36.2 and 36.5 us staging the
-      // whole slice; at M = 16 the split whole-slice shape stays ahead, 39.5 us against 39.9 us).
-      c->kernel = QF_KERNEL_MFMA_XRING;
-      c->split_k = 1;
-      return validate_config(M, N, K, layout, *c) == QF_OK;
-    }
-    c->split_k = M >= 13 ? ceil_div((int)((int64_t)M * K * 2), 56 * 1024) : 1;
-    if (c->split_k > ksteps) c->split_k = ksteps;
-    while (lds_bytes(*c, M, ksteps) > kMaxLds && c->split_k < ksteps) ++c->split_k;
-    if (c->split_k > 1) c->reduce = 1;
-    if ((size_t)workgroups(*c, N) * 4 > QF_W8A16_COUNTER_BYTES) c->reduce = 1;
+    c->kernel = QF_KERNEL_MFMA_XRING;
+    c->split_k = 1;
     return validate_config(M, N, K, layout, *c) == QF_OK;
   }
   if (layout == QF_LAYOUT_ROWMAJOR && (wide_n || M < 12)) {
@@ -1316,9 +1308,21 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
       c->waves = 4;  // row-major o_proj M = 16: 14.3 us against 15.3 us
       c->k_waves = 1;
     }
-    // one k-slice per workgroup on TILED weights: x through the two-slot ring (M = 12: qkv 14.0 us,
-    // down 20.3 us against 14.3 and 21.3 us; M = 16: 14.3 and 21.0 us against 14.7 and 21.5 us)
-    if (layout == QF_LAYOUT_TILED && c->k_waves == 1) c->kernel = QF_KERNEL_MFMA_XRING;
+    if (layout == QF_LAYOUT_TILED) {
+      // x through the two-slot ring, one k-slice per workgroup (interleaved A/B, M = 12 / 16):
+      // o_proj-like shapes (2 k-slices above) as 4 wavefronts with 8 steps in flight, 12.4 / 12.7 us
+      // against 13.3 / 13.5 us; short splits (qkv, 27 steps) with 8 steps in flight, 14.0 / 14.4 us
+      // against 14.3 / 14.8 us; down (45 steps a split) at DEPTH 4, 20.5 / 20.8 us, level with the
+      // alternatives and ahead of the whole slice (21.3 / 21.5 us).
+      c->kernel = QF_KERNEL_MFMA_XRING;
+      if (c->k_waves == 2) {
+        c->waves = 4;
+        c->k_waves = 1;
+        c->depth = 8;
+      } else if (ksteps / c->split_k < 32) {
+        c->depth = 8;
+      }
+    }
     c->reduce = 1;
     while (lds_bytes(*c, M, ksteps) > kMaxLds && c->split_k < ksteps) ++c->split_k;
     return validate_config(M, N, K, layout, *c) == QF_OK;
