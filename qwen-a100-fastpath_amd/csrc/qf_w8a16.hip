@@ -890,6 +890,62 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* w, i
   }
 }
 
+// The same quantiser for 16-byte-aligned rows with H % 8 == 0 and H <= 8 * kQuantThreads * kQuantChunks:
+// each thread keeps its 16-byte pieces (8 values) of the row in registers, so the row is read once
+// with 16-byte loads and written with 8-byte stores; the per-value arithmetic is the one above, so
+// the results are bit-identical.
+constexpr int kQuantThreads = 128;
+constexpr int kQuantChunks = 8;
+
+__global__ void __launch_bounds__(kQuantThreads) quantize_rows_vec_kernel(const uint16_t* w, int64_t ldw, int8_t* q,
+                                                                          float* s_out, int H) {
+  __shared__ float red[kQuantThreads / kWave];
+  const int64_t v = blockIdx.x;
+  const u32x4_t* row = reinterpret_cast<const u32x4_t*>(w + v * ldw);
+  const int nch = H / 8;
+  u32x4_t x[kQuantChunks];
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < kQuantChunks; ++j) {
+    const int c = j * kQuantThreads + (int)threadIdx.x;
+    x[j] = c < nch ? row[c] : u32x4_t{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int j = 0; j < kQuantChunks; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(x[j][i] << 16)), fabsf(__uint_as_float(x[j][i] & 0xffff0000u))));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = amax;
+  __syncthreads();
+  amax = red[0];
+#pragma unroll
+  for (int i = 1; i < kQuantThreads / kWave; ++i) amax = fmaxf(amax, red[i]);
+  const float inv127 = 1.0f / 127.0f;  // constant-folded: the fp32 reciprocal of 127
+  const float s = fmaxf(amax, 1e-8f) * inv127;
+  if (threadIdx.x == 0) s_out[v] = s;
+  u32x2_t* qrow = reinterpret_cast<u32x2_t*>(q + v * (int64_t)H);
+  auto quant = [&](float xv) {
+    const float t = fminf(fmaxf(rintf(__fdiv_rn(xv, s)), -127.f), 127.f);
+    return (uint32_t)(uint8_t)(int8_t)(int)t;
+  };
+#pragma unroll
+  for (int j = 0; j < kQuantChunks; ++j) {
+    const int c = j * kQuantThreads + (int)threadIdx.x;
+    if (c < nch) {
+      uint32_t b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t lo = x[j][2 * i], hi = x[j][2 * i + 1];
+        b[i] = quant(__uint_as_float(lo << 16)) | (quant(__uint_as_float(lo & 0xffff0000u)) << 8) |
+               (quant(__uint_as_float(hi << 16)) << 16) | (quant(__uint_as_float(hi & 0xffff0000u)) << 24);
+      }
+      qrow[c] = u32x2_t{b[0], b[1]};
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // Row argmax over bf16 logits (torch.argmax semantics: NaN is the maximum, first index on ties).
 // One workgroup per row.
@@ -1592,8 +1648,13 @@ int qf_w8a16_dequant_bf16(const int8_t* w, int64_t ldw, int layout, int N, int K
 
 int qf_quantize_rows_int8(const uint16_t* w, int64_t ldw, int8_t* q, float* s, int V, int H, void* stream) {
   if (w == nullptr || q == nullptr || s == nullptr || V < 1 || H < 1 || ldw < H) return QF_ERR_INVALID_ARG;
-  hipLaunchKernelGGL(quantize_rows_kernel, dim3(V), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), w, ldw,
-                     q, s, H);
+  if (aligned16(w) && ldw % 8 == 0 && H % 8 == 0 && H <= 8 * kQuantThreads * kQuantChunks && (uintptr_t)q % 8 == 0) {
+    hipLaunchKernelGGL(quantize_rows_vec_kernel, dim3(V), dim3(kQuantThreads), 0, reinterpret_cast<hipStream_t>(stream),
+                       w, ldw, q, s, H);
+  } else {
+    hipLaunchKernelGGL(quantize_rows_kernel, dim3(V), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), w, ldw,
+                       q, s, H);
+  }
   return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
 }
 

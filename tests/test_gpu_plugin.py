@@ -111,6 +111,24 @@ def test_quantize_lm_head_bit_exact(oracle):
     assert np.array_equal(w8.cpu().numpy(), q_ref)
 
 
+@pytest.mark.parametrize("H", [8, 5120, 8192, 5124, 8200])
+def test_quantizer_kernels_bit_exact(oracle, H):
+    """Both quantiser kernels: the single-pass vector one (16-byte-aligned rows, H % 8 == 0, H <= 8192) and
+    the general one (H = 5124, 8200), with zero rows, huge and tiny magnitudes and values at exact ties."""
+    V = 257
+    rng = np.random.default_rng(H)
+    wf = rng.standard_normal((V, H)) * np.exp2(rng.integers(-20, 20, (V, 1)))
+    wf[3] = 0.0
+    wf[5, :] = 2.5                # amax 127: scale ~1, so 2.5 / s sits on (or next to) a half step
+    wf[5, 0] = 127.0
+    wb = oracle.bf16_from_f64(wf)
+    q_ref, s_ref = oracle.quantize_rows(wb)
+    w8, sc = qf.quantize_lm_head(to_dev_bf16(wb, DEV))
+    torch.cuda.synchronize()
+    assert np.array_equal(sc.cpu().numpy(), s_ref)
+    assert np.array_equal(w8.cpu().numpy(), q_ref)
+
+
 def test_draft_head_logits_and_argmax(oracle):
     """int8 draft logits through the W8A16 kernel (patches.py:157-166) and the pad-masked argmax
     (patches.py:182-185), against the oracle.  A row whose top-2 exact logits are within 2 bf16 ulp
