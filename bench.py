@@ -438,27 +438,37 @@ def run_msweep(torch, qf, dev, args):
 
 
 def run_prefill(torch, qf, dev, args):
-    """gate_up (N=34816, K=5120) at prefill widths M = 64, 256, 1024, 2048 on TILED weights: the
-    chunked exact bf16 widening + library bf16 GEMM path, against 16-row slices of the decode kernel."""
+    """gate_up (N=34816, K=5120) at prefill widths M = 64 ... 2048 on TILED weights, two weight sets
+    rotated (356 MB, past the 256 MB last-level cache): the wide-M kernel (one launch, weights read
+    once per 64-row token group) and the widened-weights path (exact bf16 widening, hipBLASLt bf16
+    GEMM with fp32 output, one scale/cast pass); the dispatcher takes the wide kernel up to
+    TILED_WIDE_MAX_M rows.  Both timed interleaved, best of 2 medians."""
+    from qwen_fastpath.patches import TILED_WIDE_MAX_M
     N, K = GEMMS["gate_up"]
     g = torch.Generator(device=dev)
     g.manual_seed(13)
-    w = qf.to_tiled(torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g).t())
-    s = (torch.randn(N, device=dev, generator=g).abs() * 0.002 + 1e-4).float()
+    sets = []
+    for _ in range(2):
+        w = qf.to_tiled(torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g).t())
+        sets.append((w, (torch.randn(N, device=dev, generator=g).abs() * 0.002 + 1e-4).float()))
     rows = {}
-    for M in (64, 256, 1024, 2048):
+    for M in (64, 256, 512, 1024, 2048):
         x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
-        us = time_graph(torch, lambda: qf.w8a16_mm_prefill(x, w, s, torch.bfloat16, qf.TILED), 1, reps=5)
+        paths = {"wide": lambda i: qf.w8a16_mm(x, sets[i][0], sets[i][1], None, torch.bfloat16, qf.TILED),
+                 "widened": lambda i: qf.w8a16_mm_prefill(x, sets[i][0], sets[i][1], torch.bfloat16, qf.TILED)}
+        t = {}
+        for _ in range(2):
+            for k, f in paths.items():
+                us = time_graph(torch, lambda: [f(i) for _ in range(2) for i in range(2)], 4, reps=5)
+                t[k] = min(t.get(k, float("inf")), us)
+        path = "wide" if M <= TILED_WIDE_MAX_M else "widened"
+        us = t[path]
         tflops = 2.0 * M * N * K / us / 1e6
-        entry = {"us": round(us, 1), "TFLOP_s": round(tflops, 1), "pct_bf16_mfma_peak": round(100 * tflops / 2500.0, 1)}
-        if M <= 256:
-            us_sl = time_graph(torch, lambda: [qf.w8a16_mm(x[i:i + 16], w, s, None, torch.bfloat16, qf.TILED)
-                                               for i in range(0, M, 16)], 1, reps=5)
-            entry["us_16row_slices"] = round(us_sl, 1)
-        rows[M] = entry
-        log(f"  prefill gate_up M={M:5d}: {us:9.1f} us  {tflops:7.1f} TFLOP/s"
-            + (f"  (16-row slices {entry['us_16row_slices']:.1f} us)" if "us_16row_slices" in entry else ""))
-    line = {"metric": METRIC, "value": rows[2048]["TFLOP_s"], "unit": "TFLOP/s", "n_gpus": 1, "steps": 5, "warmup": 2,
+        rows[M] = {"us": round(us, 1), "TFLOP_s": round(tflops, 1), "pct_bf16_mfma_peak": round(100 * tflops / 2500.0, 1),
+                   "path": path, "us_wide_kernel": round(t["wide"], 1), "us_widened_gemm": round(t["widened"], 1)}
+        log(f"  prefill gate_up M={M:5d}: {us:8.1f} us  {tflops:7.1f} TFLOP/s  ({path}; wide kernel "
+            f"{t['wide']:.1f} us, widened + library GEMM {t['widened']:.1f} us)")
+    line = {"metric": METRIC, "value": rows[2048]["TFLOP_s"], "unit": "TFLOP/s", "n_gpus": 1, "steps": 4, "warmup": 1,
             "ms_per_step": round(rows[2048]["us"] / 1e3, 4), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded int8 weights, fp32 scales, bf16 activations)",
             "config": {"workload": "gate_up 34816x5120 prefill widths on TILED weights (value = M=2048 TFLOP/s)"},

@@ -1,7 +1,7 @@
 /*
  * qf_w8a16.h — C ABI of the MI355X (gfx950) W8A16 decode GEMM.
  *
- *   y[m, n] = bf16_rne( scale[n] * sum_k x[m, k] * w[n, k] )      m < M <= 16
+ *   y[m, n] = bf16_rne( scale[n] * sum_k x[m, k] * w[n, k] )      m < M
  *
  * x is bf16 [M, K] (row stride ldx elements, unit column stride), w is int8 [N, K] row-major
  * (the W8A8 checkpoint layout; the [K, N] column-major view vLLM keeps for CUTLASS is the same
@@ -37,7 +37,8 @@ extern "C" {
 
 #define QF_W8A16_ABI_VERSION 1
 
-/* Largest M handled (the reference's SMALL_M, plugin/qwen_fastpath/w8a16.py:12). */
+/* Largest M of the decode kernels (the reference's SMALL_M, plugin/qwen_fastpath/w8a16.py:12), and of
+ * every call on row-major weights.  On TILED weights QF_KERNEL_MFMA_WIDE serves any M. */
 #define QF_W8A16_MAX_M 16
 /* K must be a multiple of this (the reference's smallest BLOCK_K, w8a16.py:63-68). */
 #define QF_W8A16_K_ALIGN 64
@@ -64,8 +65,11 @@ typedef enum qf_kernel {
   QF_KERNEL_AUTO = 0,  /* pick by shape and M */
   QF_KERNEL_GEMV = 1,  /* wavefront-reduction GEMV, M <= 4, row-major layout only */
   QF_KERNEL_MFMA = 2,  /* v_mfma_f32_16x16x32_bf16 tiles, M <= 16, both layouts */
-  QF_KERNEL_MFMA_XRING = 3  /* the same tiles with x staged in (depth + 1)-step chunks through a
+  QF_KERNEL_MFMA_XRING = 3, /* the same tiles with x staged in (depth + 1)-step chunks through a
                                two-slot LDS ring instead of whole; k_waves must be 1 */
+  QF_KERNEL_MFMA_WIDE = 4   /* TILED layout, any M (picked for M > 16): each weight fragment feeds
+                               up to four 16-token tiles; groups of up to 64 token rows run in one
+                               launch; k_waves and split_k must be 1 */
 } qf_kernel;
 
 /* Launch configuration.  A zero field means "choose automatically". */
@@ -88,8 +92,10 @@ int qf_abi_version(void);
 const char* qf_status_string(int status);
 
 /* Fill *cfg with the configuration used for (M, N, K, layout).  Returns QF_ERR_UNSUPPORTED when the
- * shape is not served (M outside 1..16, N < 1, K % 64 != 0, unknown layout), mirroring
- * pick_config() returning None.  Host-only; touches no device. */
+ * shape is not served (M < 1, M > 16 on row-major weights, N < 1, K % 64 != 0, unknown layout),
+ * mirroring pick_config() returning None.  M > 16 on TILED weights gets QF_KERNEL_MFMA_WIDE (the
+ * reference sends M > 16 to its W8A8 fallback, plugin/qwen_fastpath/patches.py:99-100, which cannot
+ * read the TILED image).  Host-only; touches no device. */
 int qf_w8a16_pick_config(int M, int N, int K, int layout, qf_w8a16_config* cfg);
 
 /* Bytes of device workspace qf_w8a16_gemm needs for this call (0 when split_k == 1): arrival
@@ -149,11 +155,21 @@ int qf_w8a16_unpack(const int8_t* w_tiled, int8_t* w_rowmajor, int64_t ldw,
 /* Exact int8 -> bf16 copy of weight rows [n0, n0 + rows) of an [N, K] weight in either layout (TILED:
  * the image made by qf_w8a16_repack) into the row-major bf16 matrix out (row stride ldo elements,
  * ldo % 8 == 0, 16-byte aligned).  No scale is applied.  It feeds a library bf16 GEMM (fp32
- * accumulation, scale after the K reduction) for M beyond QF_W8A16_MAX_M on weights kept in the
- * TILED layout, which no W8A8 library kernel can read.  No reference counterpart: the reference
- * routes M > 16 to CUTLASS W8A8 on the checkpoint layout (plugin/qwen_fastpath/patches.py:99-100). */
+ * accumulation, scale after the K reduction) for M beyond the wide-M kernel's range on weights kept
+ * in the TILED layout, which no W8A8 library kernel can read.  No reference counterpart: the
+ * reference routes M > 16 to CUTLASS W8A8 on the checkpoint layout
+ * (plugin/qwen_fastpath/patches.py:99-100). */
 int qf_w8a16_dequant_bf16(const int8_t* w, int64_t ldw, int layout, int N, int K,
                           int n0, int rows, uint16_t* out, int64_t ldo, void* stream);
+
+/* y[m, n] = bf16_rne(acc[m, n] * scale[n]) for m < M, n < N: the epilogue of that library GEMM, whose
+ * fp32 output acc [M, N] (row stride lda >= N elements) is scaled after the K reduction and rounded,
+ * in one pass; y is bf16 [M, N] with row stride ldy >= N.  16-byte vector accesses when acc, scale
+ * and y are 16-byte aligned, lda % 4 == 0 and ldy % 8 == 0, element by element otherwise.  Every
+ * non-NaN result equals torch's (acc * scale).to(bfloat16) bit for bit; NaN stays NaN.  No
+ * reference counterpart (the M > 16 path above). */
+int qf_scale_cast_bf16(const float* acc, int64_t lda, const float* scale, int M, int N,
+                       uint16_t* y, int64_t ldy, void* stream);
 
 /* Per-row symmetric int8 quantisation of a bf16 [V, H] matrix (row stride ldw elements):
  *   s[v] = max(max_h |w[v,h]|, 1e-8) / 127   (fp32, IEEE division)

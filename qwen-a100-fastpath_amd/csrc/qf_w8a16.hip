@@ -70,6 +70,10 @@ struct GemmArgs {
   int64_t index_offset;
   int64_t* ids;
   uint64_t* am_cand;
+  // Wide-M kernel: token groups per n-block and rows per group (a multiple of 16; the last group
+  // takes the rest, at least one row).
+  int groups;
+  int group_rows;
 };
 
 // ---------------------------------------------------------------------------------------------
@@ -658,6 +662,192 @@ __global__ void __launch_bounds__(WN * WK * kWave) w8a16_mfma_kernel(const GemmA
 }
 
 // ---------------------------------------------------------------------------------------------
+// Wide-M MFMA kernel, TILED layout: M > 16 (prefill chunks, long verification batches).
+//
+// A workgroup owns WN * NT 16-row weight tiles over the whole K range (one wavefront per NT tiles,
+// as in the decode kernel) and one group of up to MT * 16 token rows.  Each weight fragment is
+// dequantised once per step and multiplied by the x fragments of all MT token tiles, so a group's
+// weights cross the memory system once instead of once per 16 tokens.  x reaches LDS through the
+// decode kernel's two-slot ring (chunks of DEPTH + 1 steps), sized for the group's rows.
+//
+// M above one group runs a.groups groups of a.group_rows rows (the last one shorter) in the same
+// launch, and a.split_k > 1 splits K across workgroups (fp32 partial sums, reduced by
+// splitk_reduce_kernel).  The grid is one-dimensional over (split, n-block, group).  The hardware
+// hands workgroup i to XCD i % kXcds; the placement below gives the groups of one (split, n-block)
+// consecutive workgroups of one XCD, so they run together and all but the first find the block's
+// weights in that XCD's L2.
+// ---------------------------------------------------------------------------------------------
+constexpr int kXcds = 8;  // accelerator complexes of an MI355X
+
+template <int NT, int MT, int WN, int DEPTH>
+__global__ void __launch_bounds__(WN * kWave) w8a16_wide_kernel(const GemmArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  constexpr int THREADS = WN * kWave;
+  constexpr int RING = DEPTH + 1;
+  constexpr int CP = RING * 8;                               // 16-byte pieces per token row of a chunk
+  constexpr int XP = (MT * 16 * CP + THREADS - 1) / THREADS;  // pieces per thread, at most
+  constexpr int SWM = CP % 16 == 0 ? 7 : 3;                  // the row swizzle stays inside the row
+  constexpr int64_t step_bytes = kTileN * kStepK;            // one KiB block of a tile per step
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wn = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int g = lane >> 4;
+  const int r = lane & 15;
+
+  // Workgroup -> linear index l -> (split, n-block, token group), the group fastest.  Workgroups i,
+  // i + kXcds, i + 2 kXcds ... share an XCD and take consecutive l.
+  const int ntiles = a.n_pad / kTileN;
+  const int nblocks = (ntiles + WN * NT - 1) / (WN * NT);
+  int l = blockIdx.x;
+  if (a.groups > 1) {
+    const int total = gridDim.x;
+    const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+    const int per = total / kXcds, rem = total % kXcds;
+    l = xcd < rem ? xcd * (per + 1) + j : rem * (per + 1) + (xcd - rem) * per + j;
+  }
+  const int grp = l % a.groups;
+  const int nb = (l / a.groups) % nblocks;
+  const int split = l / a.groups / nblocks;
+  int s_begin, s_end;
+  split_range(split, a.split_k, a.ksteps, s_begin, s_end);
+  const int m0 = grp * a.group_rows;
+  const int mg = min(a.group_rows, a.M - m0);  // >= 1: the host sizes the groups so
+  const uint16_t* xg = a.x + (int64_t)m0 * a.ldx;
+
+  const int tile0 = (nb * WN + wn) * NT;
+  const int k_count = s_end - s_begin;  // >= 1: split_k <= ksteps
+  // A wavefront whose tiles lie past N runs one clamped step (see w8a16_mfma_kernel) but every block
+  // of the x ring, whose barriers the whole workgroup must meet.
+  const int nsteps = tile0 < ntiles ? k_count : 1;
+  const int8_t* wp[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int tile = min(tile0 + t, ntiles - 1);
+    wp[t] = a.w + (((int64_t)tile * a.ksteps + s_begin) * kWave + lane) * 16;
+  }
+
+  u32x4_t buf[RING][NT];
+  f32x4_t acc[NT][MT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+
+  // Lane (g, r) of token tile mt reads row min(16 mt + r, mg - 1) of the group: rows past the group
+  // repeat its last row and their MFMA columns are never stored.
+  int xoff[MT], xsw[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int xm = min(mt * 16 + r, mg - 1);
+    xoff[mt] = xm * (CP * 16);
+    xsw[mt] = (xm & SWM) << 1;
+  }
+
+  const int cpieces = mg * CP;
+  const int slot_bytes = cpieces * 16;
+  const int nchunks = (k_count + RING - 1) / RING;
+  const int64_t kmax = (int64_t)s_end * kStepK - 8;  // last 8-element piece of the range
+  u32x4_t xv[XP];
+  auto load_chunk = [&](int c) {
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+      const int q = min(j * THREADS + (int)threadIdx.x, cpieces - 1);
+      const int m = q / CP;
+      const int jx = (q - m * CP) ^ ((m & SWM) << 1);
+      const int64_t k = min((int64_t)(s_begin + c * RING) * kStepK + jx * 8, kmax);
+      xv[j] = *reinterpret_cast<const u32x4_t*>(xg + (int64_t)m * a.ldx + k);
+    }
+  };
+  auto store_chunk = [&](int c) {
+    uint8_t* slot = smem + (c & 1) * slot_bytes;
+#pragma unroll
+    for (int j = 0; j < XP; ++j)
+      *reinterpret_cast<u32x4_t*>(slot + min(j * THREADS + (int)threadIdx.x, cpieces - 1) * 16) = xv[j];
+  };
+
+  load_chunk(0);
+  __builtin_amdgcn_sched_barrier(0);  // the x requests go out before the weight requests
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) {
+    const int sd = min(d, nsteps - 1);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) buf[d][t] = load16<true>(wp[t] + sd * step_bytes);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  store_chunk(0);
+  for (int c = 0; c < nchunks; ++c) {
+    if (c > 0) store_chunk(c);
+    lds_barrier();  // the weight requests stay in flight across it
+    if (c + 1 < nchunks) load_chunk(c + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t* slot = smem + (c & 1) * slot_bytes;
+#pragma unroll
+    for (int d = 0; d < RING; ++d) {
+      const int s = c * RING + d;
+      const int sn = min(s + DEPTH, nsteps - 1);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) buf[(d + DEPTH) % RING][t] = load16<true>(wp[t] + (int64_t)sn * step_bytes);
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch issue ahead of this step's math
+      if (s < nsteps) {                   // uniform
+        bf16x8_t w0[NT], w1[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) dequant16(buf[d][t], w0[t], w1[t]);
+        bf16x8_t xb0[MT], xb1[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const u32x4_t* p = reinterpret_cast<const u32x4_t*>(slot + xoff[mt] + (((d * 8 + 2 * g) ^ xsw[mt]) << 4));
+          xb0[mt] = __builtin_bit_cast(bf16x8_t, p[0]);
+          xb1[mt] = __builtin_bit_cast(bf16x8_t, p[1]);
+        }
+        // First halves of every (tile, token tile) pair, then the second halves: no MFMA waits on
+        // the one just before it.
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+            acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0[t], xb0[mt], acc[t][mt], 0, 0, 0);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+            acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1[t], xb1[mt], acc[t][mt], 0, 0, 0);
+      }
+    }
+  }
+
+  // Lane (g, r) holds C[n = tile*16 + 4g + i][m = 16 mt + r] of the group, i = 0..3.
+  if (tile0 >= ntiles) return;
+  if (a.split_k > 1) {  // partial sums [split][M][n_pad], summed and scaled by splitk_reduce_kernel
+    float* part = a.partial + (int64_t)split * a.M * a.n_pad;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int tile = tile0 + t;
+      if (tile < ntiles) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int m = mt * 16 + r;
+          if (m < mg)
+            *reinterpret_cast<f32x4_t*>(part + (int64_t)(m0 + m) * a.n_pad + tile * kTileN + 4 * g) = acc[t][mt];
+        }
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int tile = tile0 + t;
+    const int n = tile * kTileN + 4 * g;
+    if (tile < ntiles && n < a.N) {
+      const f32x4_t sc = load_scale4(a.scale, a.N, n);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = mt * 16 + r;
+        if (m < mg) store_out4(a.y, a.ldy, a.out_f32, a.vec_out, m0 + m, n, min(4, a.N - n), acc[t][mt] * sc);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // GEMV kernel (wavefront reduction), row-major layout, M = MM <= 4.
 //
 // Workgroup = WAVES wavefronts; wavefront w owns RPW consecutive rows; blockIdx.y is the K split.
@@ -831,32 +1021,71 @@ __global__ void __launch_bounds__(256) repack_kernel(const int8_t* src, int8_t* 
 
 // ---------------------------------------------------------------------------------------------
 // Exact int8 -> bf16 copy of weight rows [n0, n0 + rows) into a row-major bf16 matrix (row stride
-// ldo), from either layout: the operand of a library bf16 GEMM for M beyond the decode widths.  One
-// thread per 16 weights: a 16-byte gathered read (for TILED, one lane's chunk of a 1 KiB tile) and
-// a 32-byte coalesced write.  The scale is not applied (it follows the K reduction).
+// ldo), from either layout: the operand of a library bf16 GEMM for M beyond the wide-M kernel's
+// range.  The scale is not applied (it follows the K reduction).
+//
+// Row-major: one thread per 16 weights of a row, a 16-byte read and a 32-byte write, both
+// contiguous across the wavefront.
 // ---------------------------------------------------------------------------------------------
-template <int LAYOUT>
-__global__ void __launch_bounds__(256) dequant_bf16_kernel(const int8_t* w, int64_t ldw, int ksteps, int n0,
+__global__ void __launch_bounds__(256) dequant_rows_kernel(const int8_t* w, int64_t ldw, int ksteps, int n0,
                                                            int64_t pieces, uint16_t* out, int64_t ldo) {
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (q >= pieces) return;
   const int kp = ksteps * 4;  // 16-weight pieces per row
   const int64_t r = q / kp;   // output row
   const int c = (int)(q - r * kp);
-  const int64_t n = n0 + r;
-  const int8_t* src;
-  if constexpr (LAYOUT == QF_LAYOUT_ROWMAJOR) {
-    src = w + n * ldw + c * 16;
-  } else {
-    const int64_t tile = n / kTileN;
-    const int lane = (c & 3) * 16 + (int)(n % kTileN);
-    src = w + ((tile * ksteps + (c >> 2)) * kWave + lane) * 16;
-  }
   bf16x8_t a0, a1;
-  dequant16(*reinterpret_cast<const u32x4_t*>(src), a0, a1);
+  dequant16(*reinterpret_cast<const u32x4_t*>(w + (n0 + r) * ldw + c * 16), a0, a1);
   u32x4_t* dst = reinterpret_cast<u32x4_t*>(out + r * ldo + c * 16);
   dst[0] = __builtin_bit_cast(u32x4_t, a0);
   dst[1] = __builtin_bit_cast(u32x4_t, a1);
+}
+
+// TILED: a workgroup reads 4 consecutive KiB of the image, k-steps 4 kg .. 4 kg + 3 of one 16-row
+// tile (thread t: step 4 kg + t / 64, lane t % 64 = row t % 16, k piece t / 16 % 4), and writes 512
+// contiguous bytes of each of the tile's rows.  Reading the image in order, instead of gathering
+// each output row's pieces from 16 lanes apart, doubles the copy rate (the whole gate_up image,
+// 34816 x 5120: 107 us against 222 us).
+__global__ void __launch_bounds__(256) dequant_tiled_kernel(const int8_t* w, int ksteps, int n0, int rows,
+                                                            int kgroups, uint16_t* out, int64_t ldo) {
+  const int tile = n0 / kTileN + (int)(blockIdx.x / kgroups);
+  const int kg = (int)(blockIdx.x % kgroups);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int ks = kg * 4 + (int)(threadIdx.x / kWave);
+  const int n = tile * kTileN + (lane & 15);
+  if (ks >= ksteps || n < n0 || n >= n0 + rows) return;
+  bf16x8_t a0, a1;
+  dequant16(*reinterpret_cast<const u32x4_t*>(w + (((int64_t)tile * ksteps + ks) * kWave + lane) * 16), a0, a1);
+  u32x4_t* dst = reinterpret_cast<u32x4_t*>(out + (int64_t)(n - n0) * ldo + (ks * 4 + (lane >> 4)) * 16);
+  dst[0] = __builtin_bit_cast(u32x4_t, a0);
+  dst[1] = __builtin_bit_cast(u32x4_t, a1);
+}
+
+// y[m, n] = bf16_rne(acc[m, n] * scale[n]): the epilogue of the library GEMM on widened weights (its
+// fp32 output, scaled after the K reduction).  One thread per 8 outputs of a row: two 16-byte reads
+// of acc and of the scale, one 16-byte write; `vec` is false when a pointer or a row stride breaks
+// that alignment, and then every element is handled on its own.
+__global__ void __launch_bounds__(256) scale_cast_kernel(const float* acc, int64_t lda, const float* scale, int M,
+                                                         int N, int cpr, uint16_t* y, int64_t ldy, int vec) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= (int64_t)M * cpr) return;
+  const int m = (int)(q / cpr);
+  const int n = (int)(q - (int64_t)m * cpr) * 8;
+  const float* a = acc + m * lda + n;
+  uint16_t* o = y + m * ldy + n;
+  if (vec && n + 8 <= N) {
+    const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(a), a1 = *reinterpret_cast<const f32x4_t*>(a + 4);
+    const f32x4_t s0 = *reinterpret_cast<const f32x4_t*>(scale + n);
+    const f32x4_t s1 = *reinterpret_cast<const f32x4_t*>(scale + n + 4);
+    u32x4_t v;
+    v.x = pack_bf16_rne(a0.x * s0.x, a0.y * s0.y);
+    v.y = pack_bf16_rne(a0.z * s0.z, a0.w * s0.w);
+    v.z = pack_bf16_rne(a1.x * s1.x, a1.y * s1.y);
+    v.w = pack_bf16_rne(a1.z * s1.z, a1.w * s1.w);
+    *reinterpret_cast<u32x4_t*>(o) = v;
+  } else {
+    for (int i = 0; i < 8 && n + i < N; ++i) o[i] = bf16_rne(a[i] * scale[n + i]);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1189,6 +1418,42 @@ KernelFn select_mfma(int layout, int nt, int waves, int k_waves, int depth, int 
 
 inline bool is_mfma(int kernel) { return kernel == QF_KERNEL_MFMA || kernel == QF_KERNEL_MFMA_XRING; }
 
+// Wide-M instantiations: NT {1, 2} x MT {1..4} x WN {4, 8} x DEPTH {4, 8} (non-temporal weight loads).
+template <int NT, int MT>
+KernelFn wide_by_shape(int wn, int depth) {
+  if (wn == 4 && depth == 4) return &w8a16_wide_kernel<NT, MT, 4, 4>;
+  if (wn == 4 && depth == 8) return &w8a16_wide_kernel<NT, MT, 4, 8>;
+  if (wn == 8 && depth == 4) return &w8a16_wide_kernel<NT, MT, 8, 4>;
+  if (wn == 8 && depth == 8) return &w8a16_wide_kernel<NT, MT, 8, 8>;
+  return nullptr;
+}
+
+template <int NT>
+KernelFn wide_by_mt(int mt, int wn, int depth) {
+  switch (mt) {
+    case 1: return wide_by_shape<NT, 1>(wn, depth);
+    case 2: return wide_by_shape<NT, 2>(wn, depth);
+    case 3: return wide_by_shape<NT, 3>(wn, depth);
+    case 4: return wide_by_shape<NT, 4>(wn, depth);
+    default: return nullptr;
+  }
+}
+
+KernelFn select_wide(int nt, int mt, int waves, int depth) {
+  if (nt == 1) return wide_by_mt<1>(mt, waves, depth);
+  if (nt == 2) return wide_by_mt<2>(mt, waves, depth);
+  return nullptr;
+}
+
+// Token groups of the wide-M kernel: as few groups as 64-row groups allow, rows spread evenly and
+// rounded up to whole 16-row tiles; the count is then recomputed so that every group has a row.
+constexpr int kWideGroupRows = 64;
+void wide_groups(int M, int& groups, int& group_rows) {
+  const int g0 = (M + kWideGroupRows - 1) / kWideGroupRows;
+  group_rows = ((M + g0 - 1) / g0 + 15) / 16 * 16;
+  groups = (M + group_rows - 1) / group_rows;
+}
+
 template <int MM, int RPW>
 KernelFn gemv_fn(int hint) {
   return hint ? &w8a16_gemv_kernel<MM, RPW, 4, true> : &w8a16_gemv_kernel<MM, RPW, 4, false>;
@@ -1223,6 +1488,11 @@ inline int round_up16(int n) { return (n + 15) / 16 * 16; }
 size_t lds_bytes(const qf_w8a16_config& c, int M, int ksteps) {
   const int steps = ceil_div(ksteps, c.split_k);
   if (c.kernel == QF_KERNEL_GEMV) return (size_t)M * steps * kStepK * 2;
+  if (c.kernel == QF_KERNEL_MFMA_WIDE) {
+    int groups, rows;
+    wide_groups(M, groups, rows);
+    return (size_t)2 * rows * (c.depth + 1) * kStepK * 2;  // two chunks of the group's rows
+  }
   const size_t xs = c.kernel == QF_KERNEL_MFMA_XRING ? (size_t)2 * M * (c.depth + 1) * kStepK * 2  // two chunks
                                                      : (size_t)M * x_pitch(steps);
   const size_t red = c.k_waves > 1 ? (size_t)c.waves * c.tiles_per_wave * kWave * sizeof(f32x4_t) : 0;
@@ -1245,9 +1515,19 @@ size_t workspace_for(const qf_w8a16_config& c, int M, int N) {
 // Checks a complete configuration against the instantiated kernels and the LDS budget.
 int validate_config(int M, int N, int K, int layout, const qf_w8a16_config& c) {
   const int ksteps = K / kStepK;
-  if (c.kernel != QF_KERNEL_GEMV && !is_mfma(c.kernel)) return QF_ERR_INVALID_ARG;
+  if (c.kernel != QF_KERNEL_GEMV && !is_mfma(c.kernel) && c.kernel != QF_KERNEL_MFMA_WIDE) return QF_ERR_INVALID_ARG;
   if (c.split_k < 1 || c.split_k > ksteps || c.waves < 1 || c.k_waves < 1 || c.tiles_per_wave < 1)
     return QF_ERR_INVALID_ARG;
+  if (c.kernel == QF_KERNEL_MFMA_WIDE) {
+    // TILED weights, any M, the whole K range per workgroup.
+    if (layout != QF_LAYOUT_TILED || c.k_waves != 1) return QF_ERR_UNSUPPORTED;
+    int groups, rows;
+    wide_groups(M, groups, rows);
+    if ((int64_t)workgroups(c, N) * groups * c.split_k > 0x7fffffff) return QF_ERR_UNSUPPORTED;
+    if (select_wide(c.tiles_per_wave, rows / 16, c.waves, c.depth) == nullptr) return QF_ERR_UNSUPPORTED;
+    return lds_bytes(c, M, ksteps) > kMaxLds ? QF_ERR_UNSUPPORTED : QF_OK;
+  }
+  if (M > QF_W8A16_MAX_M) return QF_ERR_UNSUPPORTED;
   if (c.kernel == QF_KERNEL_GEMV && (M > 4 || layout != QF_LAYOUT_ROWMAJOR || c.k_waves != 1))
     return QF_ERR_UNSUPPORTED;
   if (ksteps / c.split_k < c.k_waves) return QF_ERR_UNSUPPORTED;  // every k-slice needs a step
@@ -1280,8 +1560,36 @@ constexpr TunedShape kTuned[] = {
 };
 
 bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
-  if (M < 1 || M > QF_W8A16_MAX_M || N < 1 || K < QF_W8A16_K_ALIGN || K % QF_W8A16_K_ALIGN) return false;
+  if (M < 1 || N < 1 || K < QF_W8A16_K_ALIGN || K % QF_W8A16_K_ALIGN) return false;
   if (layout != QF_LAYOUT_ROWMAJOR && layout != QF_LAYOUT_TILED) return false;
+  if (M > QF_W8A16_MAX_M) {
+    // Beyond the decode widths only TILED weights are served, by the wide-M kernel (64-row token
+    // groups; measured on the dense 27B-class layer at M = 17 .. 256 against 32- and 16-row groups,
+    // which lose everywhere): 2 tiles per wavefront, 4 steps in flight, 8 wavefronts per workgroup,
+    // or 4 once 8-wavefront workgroups number 256 or more (gate_up M = 128: 88.0 us against 98.4);
+    // K is split across workgroups until they number 128, at most 8 ways and 16 steps a split
+    // (M = 17: o_proj 16.4 us unsplit 31.8, down 23.5 against 62.6, qkv 16.5 against 21.0).
+    if (layout != QF_LAYOUT_TILED) return false;
+    *c = qf_w8a16_config{};
+    c->kernel = QF_KERNEL_MFMA_WIDE;
+    c->k_waves = 1;
+    c->load_hint = 1;
+    c->reduce = 1;
+    c->tiles_per_wave = 2;
+    c->waves = 8;
+    c->depth = 4;
+    int groups, rows;
+    wide_groups(M, groups, rows);
+    int64_t wgs = (int64_t)workgroups(*c, N) * groups;
+    if (wgs >= 256) {
+      c->waves = 4;
+      wgs = (int64_t)workgroups(*c, N) * groups;
+    }
+    const int ksteps = K / kStepK;
+    c->split_k = 1;
+    while (wgs * c->split_k < 128 && c->split_k < 8 && ksteps / (c->split_k + 1) >= 16) ++c->split_k;
+    return validate_config(M, N, K, layout, *c) == QF_OK;
+  }
   *c = qf_w8a16_config{};
   c->kernel = QF_KERNEL_MFMA;
   c->tiles_per_wave = 1;
@@ -1424,7 +1732,7 @@ int resolve_config(int M, int N, int K, int layout, const qf_w8a16_config* in, q
   if (c.k_waves == 0) c.k_waves = 1;
   if (c.tiles_per_wave == 0) c.tiles_per_wave = (c.kernel == QF_KERNEL_GEMV) ? 4 : 1;
   if (c.depth == 0) c.depth = 8;
-  if (c.split_k == 0) c.split_k = out->split_k;
+  if (c.split_k == 0) c.split_k = c.kernel == QF_KERNEL_MFMA_WIDE ? 1 : out->split_k;
   const int rc = validate_config(M, N, K, layout, c);
   if (rc != QF_OK) return rc;
   *out = c;
@@ -1478,7 +1786,7 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
   if (layout != QF_LAYOUT_ROWMAJOR && layout != QF_LAYOUT_TILED) return QF_ERR_INVALID_ARG;
   if (out_dtype != QF_DTYPE_BF16 && out_dtype != QF_DTYPE_F32) return QF_ERR_INVALID_ARG;
   if (ldx < K || (y != nullptr && ldy < N) || (layout == QF_LAYOUT_ROWMAJOR && ldw < K)) return QF_ERR_INVALID_ARG;
-  if (M > QF_W8A16_MAX_M || K % QF_W8A16_K_ALIGN) return QF_ERR_UNSUPPORTED;
+  if ((M > QF_W8A16_MAX_M && layout != QF_LAYOUT_TILED) || K % QF_W8A16_K_ALIGN) return QF_ERR_UNSUPPORTED;
   if (!aligned16(x) || !aligned16(w) || !aligned16(scale) || (y != nullptr && !aligned16(y))) return QF_ERR_UNSUPPORTED;
   if (ldx % 8 || (layout == QF_LAYOUT_ROWMAJOR && ldw % 16)) return QF_ERR_UNSUPPORTED;
 
@@ -1519,13 +1827,19 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
   a.am_cand = am != nullptr
                   ? reinterpret_cast<uint64_t*>(reinterpret_cast<uint8_t*>(workspace) + QF_W8A16_COUNTER_BYTES)
                   : nullptr;
+  a.groups = 1;
+  a.group_rows = M;
+  if (c.kernel == QF_KERNEL_MFMA_WIDE) wide_groups(M, a.groups, a.group_rows);
 
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid(workgroups(c, N), c.split_k);
+  const dim3 grid = c.kernel == QF_KERNEL_MFMA_WIDE ? dim3(workgroups(c, N) * a.groups * c.split_k)
+                                                    : dim3(workgroups(c, N), c.split_k);
   const dim3 block(c.waves * kWave);
   const size_t smem = lds_bytes(c, M, a.ksteps);
   KernelFn fn = (c.kernel == QF_KERNEL_GEMV)
                     ? select_gemv(M, c.tiles_per_wave, c.waves, c.load_hint)
+                : (c.kernel == QF_KERNEL_MFMA_WIDE)
+                    ? select_wide(c.tiles_per_wave, a.group_rows / 16, c.waves, c.depth)
                     : select_mfma(layout, c.tiles_per_wave, c.waves, c.k_waves, c.depth, c.load_hint,
                                   c.kernel == QF_KERNEL_MFMA_XRING);
   if (fn == nullptr) return QF_ERR_UNSUPPORTED;
@@ -1536,7 +1850,7 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
                        a.index_offset, a.ids);
     return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
   }
-  if (c.split_k > 1 && (c.kernel == QF_KERNEL_GEMV || !a.fused_reduce)) {
+  if (c.split_k > 1 && !a.fused_reduce) {
     const int threads = M * (a.n_pad / 4);
     st = launch(&splitk_reduce_kernel, dim3(ceil_div(threads, 256)), dim3(256), 0, s, a);
   }
@@ -1634,15 +1948,29 @@ int qf_w8a16_dequant_bf16(const int8_t* w, int64_t ldw, int layout, int N, int K
   if (K % QF_W8A16_K_ALIGN || ldo % 8 || !aligned16(w) || !aligned16(out)) return QF_ERR_UNSUPPORTED;
   if (layout == QF_LAYOUT_ROWMAJOR && ldw % 16) return QF_ERR_UNSUPPORTED;
   const int ksteps = K / kStepK;
-  const int64_t pieces = (int64_t)rows * ksteps * 4;
-  const int64_t blocks = (pieces + 255) / 256;
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (layout == QF_LAYOUT_ROWMAJOR)
-    hipLaunchKernelGGL(dequant_bf16_kernel<QF_LAYOUT_ROWMAJOR>, dim3((unsigned)blocks), dim3(256), 0, s, w, ldw, ksteps,
+  if (layout == QF_LAYOUT_ROWMAJOR) {
+    const int64_t pieces = (int64_t)rows * ksteps * 4;
+    hipLaunchKernelGGL(dequant_rows_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s, w, ldw, ksteps,
                        n0, pieces, out, ldo);
-  else
-    hipLaunchKernelGGL(dequant_bf16_kernel<QF_LAYOUT_TILED>, dim3((unsigned)blocks), dim3(256), 0, s, w, ldw, ksteps, n0,
-                       pieces, out, ldo);
+  } else {
+    const int kgroups = ceil_div(ksteps, 4);
+    const int64_t tiles = (int64_t)(n0 + rows + kTileN - 1) / kTileN - n0 / kTileN;
+    hipLaunchKernelGGL(dequant_tiled_kernel, dim3((unsigned)(tiles * kgroups)), dim3(256), 0, s, w, ksteps, n0, rows,
+                       kgroups, out, ldo);
+  }
+  return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
+}
+
+int qf_scale_cast_bf16(const float* acc, int64_t lda, const float* scale, int M, int N, uint16_t* y, int64_t ldy,
+                       void* stream) {
+  if (acc == nullptr || scale == nullptr || y == nullptr || M < 1 || N < 1 || lda < N || ldy < N)
+    return QF_ERR_INVALID_ARG;
+  const int cpr = ceil_div(N, 8);
+  const int64_t threads = (int64_t)M * cpr;
+  const int vec = aligned16(acc) && aligned16(scale) && aligned16(y) && lda % 4 == 0 && ldy % 8 == 0;
+  hipLaunchKernelGGL(scale_cast_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), acc, lda, scale, M, N, cpr, y, ldy, vec);
   return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
 }
 

@@ -28,6 +28,7 @@ KERNEL_AUTO = 0
 KERNEL_GEMV = 1
 KERNEL_MFMA = 2
 KERNEL_MFMA_XRING = 3
+KERNEL_MFMA_WIDE = 4
 
 MAX_M = 16
 K_ALIGN = 64
@@ -43,6 +44,7 @@ EXPORTS = (
     "qf_w8a16_repack",
     "qf_w8a16_unpack",
     "qf_w8a16_dequant_bf16",
+    "qf_scale_cast_bf16",
     "qf_quantize_rows_int8",
     "qf_argmax_rows_bf16",
     "qf_w8a16_gemm_argmax",
@@ -119,6 +121,8 @@ def load() -> ctypes.CDLL:
     L.qf_w8a16_unpack.restype = i32
     L.qf_w8a16_dequant_bf16.argtypes = [p, i64, i32, i32, i32, i32, i32, p, i64, p]
     L.qf_w8a16_dequant_bf16.restype = i32
+    L.qf_scale_cast_bf16.argtypes = [p, i64, p, i32, i32, p, i64, p]
+    L.qf_scale_cast_bf16.restype = i32
     L.qf_quantize_rows_int8.argtypes = [p, i64, p, p, i32, i32, p]
     L.qf_quantize_rows_int8.restype = i32
     L.qf_argmax_rows_bf16.argtypes = [p, i64, i32, i32, i32, i64, p, p]

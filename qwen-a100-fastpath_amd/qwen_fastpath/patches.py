@@ -189,20 +189,20 @@ def w8a8_reference(x2: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, bias:
 
 
 _fallback_impl: Optional[Callable] = None
-TILED_SLICE_MAX_M = 192
+TILED_WIDE_MAX_M = 768
 
 
 def _fallback(x2, w_q, w_s, bias, out_dtype, layout):
     if layout == TILED:
-        # No W8A8 library kernel reads the permuted image.  Up to TILED_SLICE_MAX_M rows the decode
-        # kernel runs over 16-row slices (each re-reads the weights); above, the weights are widened
-        # to bf16 chunk by chunk for a library bf16 GEMM (fp32 accumulation, scale after the K
-        # reduction), whose fixed cost is one full widening pass (gate_up: 168 / 622 us for slices
-        # at M = 64 / 256 against 366 / 504 us).
-        if x2.shape[0] <= TILED_SLICE_MAX_M:
-            ys = [w8a16_mm(x2[i:i + SMALL_M], w_q, w_s.reshape(-1), None, out_dtype, layout)
-                  for i in range(0, x2.shape[0], SMALL_M)]
-            y = torch.cat(ys, dim=0)
+        # No W8A8 library kernel reads the permuted image.  Up to TILED_WIDE_MAX_M rows the wide-M
+        # kernel runs (one launch, each weight fragment feeding up to 64 token rows); above, the
+        # weights are widened to bf16 for a library bf16 GEMM (fp32 accumulation, scale after the K
+        # reduction), whose MFMA tiles win once the product is that large.  Measured on the dense
+        # 27B-class layer: at M = 512 the wide kernel takes 268 / 93 / 74 / 149 us for gate_up /
+        # qkv / o_proj / down against 341 / 96 / 89 / 211 us widened, at M = 1024 498 / 158 / 143 /
+        # 279 us against 478 / 136 / 116 / 277 us.
+        if x2.shape[0] <= TILED_WIDE_MAX_M:
+            y = w8a16_mm(x2, w_q, w_s.reshape(-1), None, out_dtype, layout)
         else:
             y = w8a16_mm_prefill(x2.contiguous(), w_q, w_s, out_dtype, TILED)
         return y if bias is None else y + bias
@@ -339,8 +339,8 @@ def patch_int8_linear(kernel_cls=None, tiled: Optional[bool] = None) -> bool:
     """Install the W8A16 decode path on ``kernel_cls`` (default: vLLM's int8 scaled-mm kernel
     classes).  Idempotent (patches.py:80-82).  Returns False when no class could be patched.
     With ``tiled`` (default: QWEN_FAST_LINEAR_LAYOUT=tiled) the weights are also repacked into the
-    TILED image after loading; M > 16 calls on such layers run the W8A16 kernel over 16-row slices
-    up to TILED_SLICE_MAX_M rows, and a bf16 library GEMM over exactly widened weights above."""
+    TILED image after loading; M > 16 calls on such layers run the wide-M W8A16 kernel up to
+    TILED_WIDE_MAX_M rows, and a bf16 library GEMM over exactly widened weights above."""
     tiled = tiled_layout_requested() if tiled is None else bool(tiled)
     classes = [kernel_cls] if kernel_cls is not None else []
     if kernel_cls is None:

@@ -29,7 +29,8 @@ TILED = L.LAYOUT_TILED
 class W8A16Config(NamedTuple):
     """Launch configuration; zero fields are chosen by the library for the call's M (see
     qf_w8a16_pick_config).  kernel: 0 auto, 1 gemv (M <= 4), 2 mfma, 3 mfma with x staged in
-    chunks through a two-slot LDS ring (k_waves 1).  waves = wavefronts per workgroup, of which
+    chunks through a two-slot LDS ring (k_waves 1), 4 the wide-M mfma kernel (TILED weights, any M;
+    k_waves and split_k 1).  waves = wavefronts per workgroup, of which
     k_waves split K inside the workgroup (MFMA); reduce (MFMA, split_k > 1):
     0 = the last workgroup of each n-block sums the splits, 1 = a second kernel does."""
 
@@ -249,7 +250,12 @@ def from_tiled(w_tiled: torch.Tensor, N: int, K: int) -> torch.Tensor:
 # M beyond the decode widths (prefill) on weights this library laid out
 # ------------------------------------------------------------------------------------------------
 
+# Output channels widened per library GEMM of w8a16_mm_prefill: the whole weight up to
+# PREFILL_WHOLE_MAX_N channels, PREFILL_CHUNK_ROWS at a time above (hipBLASLt's own tiling picks:
+# qkv 10240 x 5120 at M = 1024 takes 136 us in one GEMM against 159 us in 8192 + 2048, while
+# gate_up 34816 x 5120 takes 478 us in 8192-row chunks against 529 us whole).
 PREFILL_CHUNK_ROWS = 8192
+PREFILL_WHOLE_MAX_N = 12288
 
 
 def dequant_bf16(w: torch.Tensor, N: int, K: int, layout: int = ROWMAJOR, n0: int = 0, rows: int | None = None,
@@ -268,24 +274,49 @@ def dequant_bf16(w: torch.Tensor, N: int, K: int, layout: int = ROWMAJOR, n0: in
     return out
 
 
+def scale_cast_bf16(acc: torch.Tensor, w_scale: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out[m, n] = bf16(acc[m, n] * w_scale[n]) in one pass (qf_scale_cast_bf16): acc fp32 [M, N] and
+    out bf16 [M, N], both with unit column stride; bit-identical to (acc * w_scale).to(torch.bfloat16)."""
+    M, N = acc.shape
+    if acc.dtype != torch.float32 or out.dtype != torch.bfloat16 or w_scale.dtype != torch.float32:
+        raise TypeError("acc and w_scale must be fp32, out bf16")
+    if tuple(out.shape) != (M, N) or w_scale.numel() != N or acc.stride(1) != 1 or out.stride(1) != 1:
+        raise ValueError("acc [M, N], out [M, N] with unit column strides and w_scale [N] expected")
+    s = w_scale.reshape(-1)
+    if not s.is_contiguous():
+        s = s.contiguous()
+    stream = torch.cuda.current_stream(acc.device).cuda_stream
+    L.check(L.load().qf_scale_cast_bf16(acc.data_ptr(), acc.stride(0) if M > 1 else N, s.data_ptr(), M, N,
+                                        out.data_ptr(), out.stride(0) if M > 1 else N, stream),
+            "qf_scale_cast_bf16")
+    return out
+
+
 def w8a16_mm_prefill(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, out_dtype: torch.dtype,
-                     layout: int = TILED, chunk_rows: int = PREFILL_CHUNK_ROWS) -> torch.Tensor:
+                     layout: int = TILED, chunk_rows: int | None = None) -> torch.Tensor:
     """y[M, N] = (x @ W^T) * w_scale for any M, the same product as w8a16_mm: the int8 weights are
-    widened to bf16 exactly, chunk_rows output channels at a time, multiplied by a library bf16 GEMM
+    widened to bf16 exactly, chunk_rows output channels at a time (default: all of them up to
+    PREFILL_WHOLE_MAX_N, else PREFILL_CHUNK_ROWS), multiplied by a library bf16 GEMM
     with fp32 accumulation (hipBLASLt through torch.mm), and scaled after the K reduction, then
-    rounded to out_dtype.  This serves M > 16 on weights kept in the TILED layout; the reference sends
-    M > 16 to CUTLASS W8A8 on the checkpoint layout (plugin/qwen_fastpath/patches.py:99-100)."""
+    rounded to out_dtype (bf16: one qf_scale_cast_bf16 pass per chunk).  This serves M above the
+    wide-M kernel's range on weights kept in the TILED layout; the reference sends M > 16 to CUTLASS
+    W8A8 on the checkpoint layout (plugin/qwen_fastpath/patches.py:99-100)."""
     if x.dim() != 2 or x.dtype != torch.bfloat16:
         raise TypeError("x must be a 2-D bf16 tensor")
     M, K = x.shape
     N = w_scale.numel()
-    s = w_scale.reshape(-1).float()
+    s = w_scale.reshape(-1).float().contiguous()
     y = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    if chunk_rows is None:
+        chunk_rows = N if N <= PREFILL_WHOLE_MAX_N else PREFILL_CHUNK_ROWS
     rows = min(chunk_rows, N)
     wb = torch.empty((rows, K), dtype=torch.bfloat16, device=x.device)
     for n0 in range(0, N, rows):
         r = min(rows, N - n0)
         dequant_bf16(w, N, K, layout, n0, r, wb)
         y32 = torch.mm(x, wb[:r].t(), out_dtype=torch.float32)
-        y[:, n0:n0 + r] = (y32 * s[n0:n0 + r]).to(out_dtype)
+        if out_dtype == torch.bfloat16:
+            scale_cast_bf16(y32, s[n0:n0 + r], y[:, n0:n0 + r])
+        else:
+            y[:, n0:n0 + r] = (y32 * s[n0:n0 + r]).to(out_dtype)
     return y

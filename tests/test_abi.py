@@ -185,3 +185,52 @@ def test_attention_rejects_before_launch():
     assert _attn_call(lib, splits=0) == L.ERR_INVALID_ARG
     assert _attn_call(lib, min_chunk=0) == L.ERR_INVALID_ARG
     assert _attn_call(lib, ws_bytes=1024) == L.ERR_WORKSPACE
+
+
+def _wide_groups(M):
+    """Token grouping of the wide-M kernel: the fewest 64-row groups, rows spread evenly in whole
+    16-row tiles, then the count that leaves no group empty."""
+    g0 = -(-M // 64)
+    rows = -(-(-(-M // g0)) // 16) * 16
+    return -(-M // rows), rows
+
+
+def test_wide_groups_cover_every_row():
+    for M in range(1, 5000):
+        groups, rows = _wide_groups(M)
+        assert rows % 16 == 0 and 16 <= rows <= 64
+        assert (groups - 1) * rows < M <= groups * rows, M  # every group holds at least one row
+
+
+def test_pick_config_wide_m_on_tiled_weights():
+    """M > 16 is served on TILED weights only, by the wide-M kernel (kind 4, one k-slice, K split at most 8 ways),
+    for every N and K; row-major weights stay unsupported above 16 rows."""
+    Ks = [64 * k for k in (1, 2, 3, 7, 80, 128, 272, 512)]
+    Ns = [1, 15, 16, 17, 1000, 5120, 34816, 151936]
+    for M in (17, 31, 32, 48, 63, 64, 65, 100, 129, 192, 256, 1000, 4096):
+        for K in Ks:
+            for N in Ns:
+                assert L.pick_config(M, N, K, 0) is None
+                c = L.pick_config(M, N, K, 1)
+                assert c is not None, (M, N, K)
+                assert c.kernel == L.KERNEL_MFMA_WIDE and c.k_waves == 1 and 1 <= c.split_k <= 8
+                assert c.split_k == 1 or K // 64 // c.split_k >= 16
+                n_pad = -(-N // 16) * 16
+                assert L.workspace_bytes(M, N, K, 1, c) == (0 if c.split_k == 1 else
+                                                            65536 + c.split_k * M * n_pad * 4)
+    # explicit wide configurations outside the instantiated (tiles {1, 2}, waves {4, 8}, depth {4, 8})
+    # or with k-slices are refused before any launch; a K split needs the workspace
+    fake = 1 << 20
+    for bad in ((L.KERNEL_MFMA_WIDE, 1, 4, 8, 4, 1, 1, 0), (L.KERNEL_MFMA_WIDE, 1, 2, 16, 4, 1, 1, 0),
+                (L.KERNEL_MFMA_WIDE, 1, 2, 8, 4, 1, 2, 0),
+                (L.KERNEL_MFMA_WIDE, 1, 2, 8, 6, 1, 1, 0)):
+        c = L.Config.from_seq(bad)
+        assert _gemm(x=fake, w=fake, s=fake, y=fake, layout=1, M=40, K=1024, ldx=1024, ldw=1024,
+                     cfg=c) == L.ERR_UNSUPPORTED, bad
+    c = L.Config.from_seq((L.KERNEL_MFMA_WIDE, 4, 2, 8, 4, 1, 1, 1))
+    assert L.workspace_bytes(40, 1000, 1024, 1, c) == 65536 + 4 * 40 * 1008 * 4
+    assert _gemm(x=fake, w=fake, s=fake, y=fake, layout=1, M=40, K=1024, ldx=1024, ldw=1024,
+                 cfg=c) == L.ERR_WORKSPACE
+    c = L.Config.from_seq((L.KERNEL_MFMA_WIDE, 1, 2, 8, 4, 1, 1, 0))
+    assert _gemm(x=fake, w=fake, s=fake, y=fake, layout=0, M=40, cfg=c) == L.ERR_UNSUPPORTED  # row-major
+    assert _gemm(x=fake, w=fake, s=fake, y=fake, layout=0, M=40) == L.ERR_UNSUPPORTED
