@@ -686,7 +686,14 @@ __global__ void __launch_bounds__(WN * kWave) w8a16_wide_kernel(const GemmArgs a
   constexpr int RING = DEPTH + 1;
   constexpr int CP = RING * 8;                               // 16-byte pieces per token row of a chunk
   constexpr int XP = (MT * 16 * CP + THREADS - 1) / THREADS;  // pieces per thread, at most
-  constexpr int SWM = CP % 16 == 0 ? 7 : 3;                  // the row swizzle stays inside the row
+  // Chunk rows of 8-wavefront workgroups (one per CU) are padded by 16 bytes and read at plain
+  // offsets.  4-wavefront workgroups keep the rows unpadded, so that a 64-row ring of DEPTH 4 fills
+  // exactly half of a CU's LDS and two workgroups share a CU, and move piece j of row m to position
+  // j ^ ((m & SWM) << 1) instead (measured: the padded rows gain 1-7% on 8 wavefronts; on 4 they
+  // cost the second workgroup, 20% at gate_up M = 512).
+  constexpr bool PAD = WN == 8;
+  constexpr int SWM = PAD ? 0 : (CP % 16 == 0 ? 7 : 3);     // the row swizzle stays inside the row
+  constexpr int ROW = (CP + (PAD ? 1 : 0)) * 16;
   constexpr int64_t step_bytes = kTileN * kStepK;            // one KiB block of a tile per step
   const int lane = threadIdx.x & (kWave - 1);
   const int wn = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -738,12 +745,12 @@ __global__ void __launch_bounds__(WN * kWave) w8a16_wide_kernel(const GemmArgs a
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int xm = min(mt * 16 + r, mg - 1);
-    xoff[mt] = xm * (CP * 16);
+    xoff[mt] = xm * ROW;
     xsw[mt] = (xm & SWM) << 1;
   }
 
   const int cpieces = mg * CP;
-  const int slot_bytes = cpieces * 16;
+  const int slot_bytes = mg * ROW;  // LDS bytes of one ring slot
   const int nchunks = (k_count + RING - 1) / RING;
   const int64_t kmax = (int64_t)s_end * kStepK - 8;  // last 8-element piece of the range
   u32x4_t xv[XP];
@@ -752,7 +759,7 @@ __global__ void __launch_bounds__(WN * kWave) w8a16_wide_kernel(const GemmArgs a
     for (int j = 0; j < XP; ++j) {
       const int q = min(j * THREADS + (int)threadIdx.x, cpieces - 1);
       const int m = q / CP;
-      const int jx = (q - m * CP) ^ ((m & SWM) << 1);
+      const int jx = (q - m * CP) ^ ((m & SWM) << 1);  // the x piece that LDS position q holds
       const int64_t k = min((int64_t)(s_begin + c * RING) * kStepK + jx * 8, kmax);
       xv[j] = *reinterpret_cast<const u32x4_t*>(xg + (int64_t)m * a.ldx + k);
     }
@@ -760,8 +767,10 @@ __global__ void __launch_bounds__(WN * kWave) w8a16_wide_kernel(const GemmArgs a
   auto store_chunk = [&](int c) {
     uint8_t* slot = smem + (c & 1) * slot_bytes;
 #pragma unroll
-    for (int j = 0; j < XP; ++j)
-      *reinterpret_cast<u32x4_t*>(slot + min(j * THREADS + (int)threadIdx.x, cpieces - 1) * 16) = xv[j];
+    for (int j = 0; j < XP; ++j) {
+      const int q = min(j * THREADS + (int)threadIdx.x, cpieces - 1);
+      *reinterpret_cast<u32x4_t*>(slot + q * 16 + (PAD ? q / CP * 16 : 0)) = xv[j];
+    }
   };
 
   load_chunk(0);
@@ -1491,7 +1500,8 @@ size_t lds_bytes(const qf_w8a16_config& c, int M, int ksteps) {
   if (c.kernel == QF_KERNEL_MFMA_WIDE) {
     int groups, rows;
     wide_groups(M, groups, rows);
-    return (size_t)2 * rows * (c.depth + 1) * kStepK * 2;  // two chunks of the group's rows
+    // two chunks of the group's rows, rows padded by 16 bytes in 8-wavefront workgroups
+    return (size_t)2 * rows * ((c.depth + 1) * kStepK * 2 + (c.waves == 8 ? 16 : 0));
   }
   const size_t xs = c.kernel == QF_KERNEL_MFMA_XRING ? (size_t)2 * M * (c.depth + 1) * kStepK * 2  // two chunks
                                                      : (size_t)M * x_pitch(steps);
