@@ -69,7 +69,9 @@ typedef enum qf_kernel {
                                two-slot LDS ring instead of whole; k_waves must be 1 */
   QF_KERNEL_MFMA_WIDE = 4   /* TILED layout, any M (picked for M > 16): each weight fragment feeds
                                up to four 16-token tiles; groups of up to 64 token rows run in one
-                               launch; k_waves and split_k must be 1 */
+                               launch; k_waves must be 1, split_k > 1 needs the workspace;
+                               tiles_per_wave 1 or 2 with 4 or 8 waves at depth 4 or 8, or 4 tiles
+                               with 4 waves at depth 2 */
 } qf_kernel;
 
 /* Launch configuration.  A zero field means "choose automatically". */

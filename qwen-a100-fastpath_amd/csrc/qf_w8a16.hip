@@ -1427,7 +1427,8 @@ KernelFn select_mfma(int layout, int nt, int waves, int k_waves, int depth, int 
 
 inline bool is_mfma(int kernel) { return kernel == QF_KERNEL_MFMA || kernel == QF_KERNEL_MFMA_XRING; }
 
-// Wide-M instantiations: NT {1, 2} x MT {1..4} x WN {4, 8} x DEPTH {4, 8} (non-temporal weight loads).
+// Wide-M instantiations: NT {1, 2} x MT {1..4} x WN {4, 8} x DEPTH {4, 8}, and NT 4 x MT {1..4} with 4
+// wavefronts and DEPTH 2 (non-temporal weight loads).
 template <int NT, int MT>
 KernelFn wide_by_shape(int wn, int depth) {
   if (wn == 4 && depth == 4) return &w8a16_wide_kernel<NT, MT, 4, 4>;
@@ -1451,6 +1452,15 @@ KernelFn wide_by_mt(int mt, int wn, int depth) {
 KernelFn select_wide(int nt, int mt, int waves, int depth) {
   if (nt == 1) return wide_by_mt<1>(mt, waves, depth);
   if (nt == 2) return wide_by_mt<2>(mt, waves, depth);
+  if (nt == 4 && waves == 4 && depth == 2) {
+    switch (mt) {
+      case 1: return &w8a16_wide_kernel<4, 1, 4, 2>;
+      case 2: return &w8a16_wide_kernel<4, 2, 4, 2>;
+      case 3: return &w8a16_wide_kernel<4, 3, 4, 2>;
+      case 4: return &w8a16_wide_kernel<4, 4, 4, 2>;
+      default: return nullptr;
+    }
+  }
   return nullptr;
 }
 
@@ -1574,22 +1584,30 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
   if (layout != QF_LAYOUT_ROWMAJOR && layout != QF_LAYOUT_TILED) return false;
   if (M > QF_W8A16_MAX_M) {
     // Beyond the decode widths only TILED weights are served, by the wide-M kernel (64-row token
-    // groups; measured on the dense 27B-class layer at M = 17 .. 256 against 32- and 16-row groups,
-    // which lose everywhere): 2 tiles per wavefront, 4 steps in flight, 8 wavefronts per workgroup,
-    // or 4 once 8-wavefront workgroups number 256 or more (gate_up M = 128: 88.0 us against 98.4);
-    // K is split across workgroups until they number 128, at most 8 ways and 16 steps a split
-    // (M = 17: o_proj 16.4 us unsplit 31.8, down 23.5 against 62.6, qkv 16.5 against 21.0).
+    // groups; measured on the dense 27B-class layer at M = 17 .. 2048 against 32-, 16- and 128-row
+    // groups, which lose everywhere).  Once 4-wavefront workgroups of 4 tiles a wavefront number 256
+    // or more, they run with 2 steps in flight: each x fragment read from LDS then feeds 4 tiles
+    // (M = 1024: gate_up 403 us against 482, qkv 133 against 148, down 252 against 267).  Below
+    // that: 2 tiles per wavefront, 4 steps in flight, 8 wavefronts per workgroup, or 4 once
+    // 8-wavefront workgroups number 256 or more (gate_up M = 128: 88.0 us against 98.4); K is split
+    // across workgroups until they number 128, at most 8 ways and 16 steps a split (M = 17: o_proj
+    // 16.4 us unsplit 31.8, down 23.5 against 62.6, qkv 16.5 against 21.0).
     if (layout != QF_LAYOUT_TILED) return false;
     *c = qf_w8a16_config{};
     c->kernel = QF_KERNEL_MFMA_WIDE;
     c->k_waves = 1;
     c->load_hint = 1;
     c->reduce = 1;
+    c->split_k = 1;
+    c->tiles_per_wave = 4;
+    c->waves = 4;
+    c->depth = 2;
+    int groups, rows;
+    wide_groups(M, groups, rows);
+    if ((int64_t)workgroups(*c, N) * groups >= 256) return validate_config(M, N, K, layout, *c) == QF_OK;
     c->tiles_per_wave = 2;
     c->waves = 8;
     c->depth = 4;
-    int groups, rows;
-    wide_groups(M, groups, rows);
     int64_t wgs = (int64_t)workgroups(*c, N) * groups;
     if (wgs >= 256) {
       c->waves = 4;

@@ -189,7 +189,7 @@ def w8a8_reference(x2: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, bias:
 
 
 _fallback_impl: Optional[Callable] = None
-TILED_WIDE_MAX_M = 768
+TILED_WIDE_MAX_M = 1024
 
 
 def _fallback(x2, w_q, w_s, bias, out_dtype, layout):
@@ -198,9 +198,9 @@ def _fallback(x2, w_q, w_s, bias, out_dtype, layout):
         # kernel runs (one launch, each weight fragment feeding up to 64 token rows); above, the
         # weights are widened to bf16 for a library bf16 GEMM (fp32 accumulation, scale after the K
         # reduction), whose MFMA tiles win once the product is that large.  Measured on the dense
-        # 27B-class layer: at M = 512 the wide kernel takes 268 / 93 / 74 / 149 us for gate_up /
-        # qkv / o_proj / down against 341 / 96 / 89 / 211 us widened, at M = 1024 498 / 158 / 143 /
-        # 279 us against 478 / 136 / 116 / 277 us.
+        # 27B-class layer (gate_up / qkv / o_proj / down): at M = 1024 the wide kernel takes
+        # 403 / 133 / 123 / 252 us against 478 / 136 / 116 / 277 us widened, at M = 2048
+        # 806 / 241 / 205 / 427 us against 741 / 233 / 175 / 338 us.
         if x2.shape[0] <= TILED_WIDE_MAX_M:
             y = w8a16_mm(x2, w_q, w_s.reshape(-1), None, out_dtype, layout)
         else:

@@ -218,10 +218,12 @@ def test_pick_config_wide_m_on_tiled_weights():
                 n_pad = -(-N // 16) * 16
                 assert L.workspace_bytes(M, N, K, 1, c) == (0 if c.split_k == 1 else
                                                             65536 + c.split_k * M * n_pad * 4)
-    # explicit wide configurations outside the instantiated (tiles {1, 2}, waves {4, 8}, depth {4, 8})
-    # or with k-slices are refused before any launch; a K split needs the workspace
+    # explicit wide configurations outside the instantiated ones (tiles {1, 2} x waves {4, 8} x depth
+    # {4, 8}; 4 tiles x 4 waves at depth 2) or with k-slices are refused before any launch; a K split
+    # needs the workspace
     fake = 1 << 20
     for bad in ((L.KERNEL_MFMA_WIDE, 1, 4, 8, 4, 1, 1, 0), (L.KERNEL_MFMA_WIDE, 1, 2, 16, 4, 1, 1, 0),
+                (L.KERNEL_MFMA_WIDE, 1, 4, 4, 4, 1, 1, 0), (L.KERNEL_MFMA_WIDE, 1, 2, 4, 2, 1, 1, 0),
                 (L.KERNEL_MFMA_WIDE, 1, 2, 8, 4, 1, 2, 0),
                 (L.KERNEL_MFMA_WIDE, 1, 2, 8, 6, 1, 1, 0)):
         c = L.Config.from_seq(bad)

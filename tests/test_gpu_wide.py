@@ -59,9 +59,10 @@ def test_wide_against_oracle(oracle, M):
     assert torch.equal(bits(y), bits(slices(x, wt, s, split=split)))
 
 
-@pytest.mark.parametrize("depth", [4, 8])
-@pytest.mark.parametrize("waves", [4, 8])
-@pytest.mark.parametrize("nt", [1, 2])
+WIDE_SHAPES = [(nt, waves, depth) for nt in (1, 2) for waves in (4, 8) for depth in (4, 8)] + [(4, 4, 2)]
+
+
+@pytest.mark.parametrize("nt,waves,depth", WIDE_SHAPES)
 def test_wide_configs_bitwise(nt, waves, depth):
     """Every instantiated (tiles, wavefronts, depth) at 1..4 token tiles and 1..3 groups, a ragged N
     and a chunk count that does not divide the k-steps, bf16 and fp32 outputs."""
