@@ -6,7 +6,9 @@
 
 * ``qf_int8_linear`` -- the dispatcher op (patches.py:84-106): M <= 16 bf16 activations on an int8
   weight with stride(0) == 1 and one fp32 scale per output channel go to the HIP W8A16 kernel;
-  anything else goes to the W8A8 path the reference falls back to.
+  anything else goes to the W8A8 path the reference falls back to, except on TILED layers, whose
+  M > 16 calls run the wide-M W8A16 kernel (up to TILED_WIDE_MAX_M rows) or the widened-weights
+  library GEMM.
 * ``patch_int8_linear`` -- swaps ``apply_weights(self, layer, x, bias)`` of vLLM's int8 scaled-mm
   kernel class (patches.py:72-116); ``W8A16LinearMethod.apply(layer, x, bias)`` is the same surface
   for callers that hold the layer directly.
@@ -155,7 +157,7 @@ def draft_head_switch_enabled() -> bool:
 
 
 # ------------------------------------------------------------------------------------------------
-# W8A8 fallback (M > 16 or ineligible inputs)
+# W8A8 fallback (M > 16 or ineligible inputs on row-major layers)
 # ------------------------------------------------------------------------------------------------
 
 def _vllm_w8a8() -> Optional[Callable]:
