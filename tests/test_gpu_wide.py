@@ -105,3 +105,43 @@ def test_wide_layer_shapes_bitwise(name, N, K):
         torch.cuda.synchronize()
         print(f"{name} M={M} cfg={tuple(qf.resolve_config(M, N, K, qf.TILED))}", flush=True)
         assert torch.equal(bits(y), bits(ref)), (name, M)
+
+
+def test_wide_and_widened_paths_in_a_graph():
+    """The wide-M kernel with a K split (workspace + second-pass sum), without one, and the widened-weights
+    path (widening, library GEMM, scale/cast) captured in one graph: four replays with eager work and
+    zeroed outputs between them, each bitwise equal to the eager results."""
+    cases = []
+    for (M, N, K, seed) in ((40, 1000, 2048, 1), (300, 2000, 1024, 2)):
+        wt, s, g = random_layer(N, K, seed)
+        x = torch.randn(M, K, device=DEV, generator=g).to(torch.bfloat16)
+        cases.append((x, wt, s))
+    assert qf.resolve_config(40, 1000, 2048, qf.TILED).split_k > 1
+    assert qf.resolve_config(300, 2000, 1024, qf.TILED).split_k == 1
+
+    def work():
+        outs = [qf.w8a16_mm(x, wt, s, None, torch.bfloat16, qf.TILED) for (x, wt, s) in cases]
+        x, wt, s = cases[1]
+        outs.append(qf.w8a16_mm_prefill(x, wt, s, torch.bfloat16, qf.TILED, chunk_rows=768))
+        return outs
+
+    eager = [o.clone() for o in work()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        work()  # warm-up off the default stream (allocates the split-K workspace)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = work()
+    torch.cuda.synchronize()
+    for rep in range(4):
+        for o in outs:
+            o.fill_(0)
+        junk = torch.randn(1 << 20, device=DEV).sum()  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (o, e) in enumerate(zip(outs, eager)):
+            assert torch.equal(bits(o), bits(e)), (rep, i)
+        del junk
