@@ -1604,7 +1604,16 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
     c->depth = 2;
     int groups, rows;
     wide_groups(M, groups, rows);
-    if ((int64_t)workgroups(*c, N) * groups >= 256) return validate_config(M, N, K, layout, *c) == QF_OK;
+    const int ksteps = K / kStepK;
+    const int64_t wgs4 = (int64_t)workgroups(*c, N) * groups;
+    if (wgs4 >= 256) return validate_config(M, N, K, layout, *c) == QF_OK;
+    if (wgs4 >= 128 && wgs4 < 192 && ksteps >= 256) {
+      // Long K (K >= 16384) and 128..191 such workgroups: split K as far as 512 workgroups (two per
+      // CU slot), 4 ways and 64 steps a split at most.  down 5120 x 17408 at M = 448 / 512 (3 ways):
+      // 102 / 107 us against 138 us for the 2-tile choice below, which stays ahead from M = 640.
+      while (wgs4 * (c->split_k + 1) <= 512 && c->split_k < 4 && ksteps / (c->split_k + 1) >= 64) ++c->split_k;
+      return validate_config(M, N, K, layout, *c) == QF_OK;
+    }
     c->tiles_per_wave = 2;
     c->waves = 8;
     c->depth = 4;
@@ -1613,7 +1622,6 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
       c->waves = 4;
       wgs = (int64_t)workgroups(*c, N) * groups;
     }
-    const int ksteps = K / kStepK;
     c->split_k = 1;
     while (wgs * c->split_k < 128 && c->split_k < 8 && ksteps / (c->split_k + 1) >= 16) ++c->split_k;
     return validate_config(M, N, K, layout, *c) == QF_OK;
