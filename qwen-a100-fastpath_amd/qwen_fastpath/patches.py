@@ -173,6 +173,21 @@ def _vllm_w8a8() -> Optional[Callable]:
     return run
 
 
+def _int8_products(x_q: torch.Tensor, w_q: torch.Tensor) -> torch.Tensor:
+    """fp32(x_q @ w_q) for integer-valued x_q in [-128, 127] and int8 w_q [K, N]: the exact integer
+    sums rounded once to fp32.  On the GPU with M > 16 and K, N multiples of 8 the int8 GEMM of the
+    library (torch._int_mm, int32 accumulation: |sum| <= K * 128 * 127 < 2^31 for K < 132000) gives them;
+    otherwise an fp64 product does (sums of at most 2^53 are exact)."""
+    M, K = x_q.shape
+    N = w_q.shape[1]
+    if x_q.is_cuda and M > 16 and K % 8 == 0 and N % 8 == 0 and K < 132000:
+        try:
+            return torch._int_mm(x_q.to(torch.int8), w_q).float()
+        except RuntimeError:
+            pass
+    return (x_q.double() @ w_q.double()).float()
+
+
 def w8a8_reference(x2: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, bias: Optional[torch.Tensor],
                    out_dtype: torch.dtype) -> torch.Tensor:
     """Dynamic per-token symmetric int8 activations x int8 weights, exact integer accumulation, then
@@ -183,7 +198,7 @@ def w8a8_reference(x2: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, bias:
     s_a = xf.abs().amax(dim=-1, keepdim=True) / 127.0
     x_q = torch.where(s_a > 0, torch.round(xf / torch.where(s_a > 0, s_a, torch.ones_like(s_a))),
                       torch.zeros_like(xf)).clamp_(-128, 127)
-    acc = (x_q.double() @ w_q.double()).float()  # integer sums: exact in fp64
+    acc = _int8_products(x_q, w_q)
     y = acc * s_a * w_s.reshape(1, -1).float()
     if bias is not None:
         y = y + bias.float()

@@ -98,6 +98,25 @@ def test_ineligible_m17_uses_w8a8_fallback(oracle):
     assert 0.006 <= rel <= 0.012, rel
 
 
+@pytest.mark.parametrize("M,N,K", [(17, 5120, 6144), (64, 1000, 2048), (300, 512, 17408)])
+def test_w8a8_integer_products_library_gemm_matches_fp64(M, N, K):
+    """The W8A8 restatement's integer sums through the library int8 GEMM (int32) equal the fp64 ones bit
+    for bit after the one rounding to fp32, extremes included (-128 activations, +-127 weights)."""
+    from qwen_fastpath import patches as P
+    g = torch.Generator(device=DEV)
+    g.manual_seed(M + N)
+    x_q = torch.randint(-128, 128, (M, K), device=DEV, generator=g).float()
+    x_q[0] = -128.0
+    w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=DEV, generator=g)
+    w[0] = 127
+    got = P._int8_products(x_q, w.t())
+    ref = (x_q.double() @ w.t().double()).float()
+    direct = torch._int_mm(x_q.to(torch.int8), w.t())  # the library path itself runs for these shapes
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    assert torch.equal(direct.float(), ref)
+
+
 def test_quantize_lm_head_bit_exact(oracle):
     V, H = 3000, 5120
     rng = np.random.default_rng(5)
