@@ -22,6 +22,8 @@
  *   qf_quantize_rows_int8    <- draft-head per-row quantizer   plugin/qwen_fastpath/patches.py:139-147
  *   qf_argmax_rows_bf16      <- pad mask + argmax of draft logits   plugin/qwen_fastpath/patches.py:182-185
  *   qf_w8a16_gemm_argmax     <- draft logits + pad mask + argmax in one launch   patches.py:160-166,178-185
+ *   qf_quantize_tokens_int8  <- ops.scaled_int8_quant (dynamic, symmetric)   plugin/qwen_fastpath/patches.py:99
+ *   qf_w8a8_gemm             <- ops.cutlass_scaled_mm on the int8 weights      plugin/qwen_fastpath/patches.py:100
  *   qf_w8a16_repack / qf_w8a16_unpack: load-time weight layout change (no reference counterpart;
  *                              the reference streams the checkpoint layout as is, w8a16.py:1-7)
  */
@@ -67,11 +69,13 @@ typedef enum qf_kernel {
   QF_KERNEL_MFMA = 2,  /* v_mfma_f32_16x16x32_bf16 tiles, M <= 16, both layouts */
   QF_KERNEL_MFMA_XRING = 3, /* the same tiles with x staged in (depth + 1)-step chunks through a
                                two-slot LDS ring instead of whole; k_waves must be 1 */
-  QF_KERNEL_MFMA_WIDE = 4   /* TILED layout, any M (picked for M > 16): each weight fragment feeds
+  QF_KERNEL_MFMA_WIDE = 4,  /* TILED layout, any M (picked for M > 16): each weight fragment feeds
                                up to four 16-token tiles; groups of up to 64 token rows run in one
                                launch; k_waves must be 1, split_k > 1 needs the workspace;
                                tiles_per_wave 1 or 2 with 4 or 8 waves at depth 4 or 8, or 4 tiles
                                with 4 waves at depth 2 */
+  QF_KERNEL_MFMA_W8A8 = 5   /* qf_w8a8_gemm only: the same tiling on v_mfma_i32_16x16x64_i8 with int8
+                               activations; tiles_per_wave 2 or 4, 4 or 8 waves, depth 2 or 4 */
 } qf_kernel;
 
 /* Launch configuration.  A zero field means "choose automatically". */
@@ -172,6 +176,36 @@ int qf_w8a16_dequant_bf16(const int8_t* w, int64_t ldw, int layout, int N, int K
  * reference counterpart (the M > 16 path above). */
 int qf_scale_cast_bf16(const float* acc, int64_t lda, const float* scale, int M, int N,
                        uint16_t* y, int64_t ldy, void* stream);
+
+/* ---- W8A8 path for M > 16 on TILED weights: the reference's fallback arithmetic (dynamic per-token int8
+ * activations, int8 weights, exact integer sums, fp32 scales), plugin/qwen_fastpath/patches.py:99-100,
+ * on weights kept in the TILED image, which CUTLASS cannot read. ---- */
+
+/* Per-token symmetric int8 quantisation of bf16 x [M, K] (row stride ldx elements):
+ *   s_a[m] = max_k |x[m,k]| * fl(1/127)          (fp32; 0 for a row of zeros)
+ *   xq[m,k] = clamp(round_half_even(x[m,k] / s_a[m]), -128, 127)   (IEEE division; 0 when s_a[m] == 0)
+ * xq is int8 [M, K] with row stride ldq bytes.  Finite inputs.  K % 64 == 0, x 16-byte aligned,
+ * ldx % 8 == 0, xq 8-byte aligned and ldq % 8 == 0, else QF_ERR_UNSUPPORTED.
+ * Reference: vLLM's scaled_int8_quant(x, symmetric=True) at plugin/qwen_fastpath/patches.py:99, which
+ * divides amax by 127 where this multiplies by the fp32 reciprocal (at most one ulp apart in s_a). */
+int qf_quantize_tokens_int8(const uint16_t* x, int64_t ldx, int M, int K, int8_t* xq, int64_t ldq, float* s_a,
+                            void* stream);
+
+/* y[m, n] = out_dtype( (float(sum_k xq[m,k] * w[n,k]) * s_a[m]) * scale[n] ), the integer sums exact in
+ * int32 (K < 132000).  w is the TILED image (layout must be QF_LAYOUT_TILED, else QF_ERR_UNSUPPORTED; ldw is
+ * ignored); xq / s_a as written by qf_quantize_tokens_int8 (xq 16-byte aligned, ldq % 16 == 0); any M >= 1.
+ * cfg may be NULL (automatic); its kernel must be QF_KERNEL_MFMA_W8A8 or AUTO.  Workspace
+ * (qf_w8a8_workspace_bytes, 0 without a K split): the int32 split partials after the counter prefix, which
+ * this path does not use; calls that may run at the same time need distinct workspaces.
+ * Reference: ops.cutlass_scaled_mm(x_q, w_q, scale_a, scale_b, out_dtype, bias=None) at
+ * plugin/qwen_fastpath/patches.py:100 (the bias is added by the caller). */
+int qf_w8a8_gemm(const int8_t* xq, int64_t ldq, const float* s_a, const int8_t* w, int64_t ldw, int layout,
+                 const float* scale, void* y, int64_t ldy, int out_dtype, int M, int N, int K,
+                 const qf_w8a16_config* cfg, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Automatic configuration and workspace bytes of qf_w8a8_gemm (host only). */
+int qf_w8a8_pick_config(int M, int N, int K, int layout, qf_w8a16_config* cfg);
+size_t qf_w8a8_workspace_bytes(int M, int N, int K, int layout, const qf_w8a16_config* cfg);
 
 /* Per-row symmetric int8 quantisation of a bf16 [V, H] matrix (row stride ldw elements):
  *   s[v] = max(max_h |w[v,h]|, 1e-8) / 127   (fp32, IEEE division)

@@ -74,6 +74,9 @@ struct GemmArgs {
   // takes the rest, at least one row).
   int groups;
   int group_rows;
+  // W8A8 kernel: int8 activations [M][K] (row stride ldx bytes) and their per-token scales.
+  const int8_t* xq;
+  const float* s_tok;
 };
 
 // ---------------------------------------------------------------------------------------------
@@ -854,6 +857,236 @@ __global__ void __launch_bounds__(WN * kWave) w8a16_wide_kernel(const GemmArgs a
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------------------------
+// W8A8 path for M > 16 on TILED weights: the arithmetic of the reference's fallback for M > 16
+// (scaled_int8_quant + cutlass_scaled_mm, plugin/qwen_fastpath/patches.py:99-100).  Activations are
+// quantised per token to int8, multiplied by the int8 weights with exact int32 sums on
+// v_mfma_i32_16x16x64_i8, and scaled as (float(sum) * s_a[m]) * s_w[n].
+// ---------------------------------------------------------------------------------------------
+
+// Per-token quantiser: s_a[m] = amax_k |x[m, k]| * fl(1/127) (amax / 127.0 as torch evaluates a tensor
+// divided by a scalar on the device; vLLM's kernel divides, at most an ulp away) and
+// xq[m, k] = clamp(rint(x / s_a), -128, 127) with an IEEE division; a row of zeros gets s_a = 0 and
+// xq = 0.  Finite inputs.  One workgroup per row, 8 values a thread per 16-byte load (K % 64 == 0,
+// 16-byte-aligned rows: the GEMM's own contract).
+__global__ void __launch_bounds__(256) quantize_tokens_kernel(const uint16_t* x, int64_t ldx, int K, int8_t* xq,
+                                                              int64_t ldq, float* s_a) {
+  __shared__ float red[256 / kWave];
+  const int64_t m = blockIdx.x;
+  const u32x4_t* row = reinterpret_cast<const u32x4_t*>(x + m * ldx);
+  const int pieces = K / 8;
+  float amax = 0.f;
+  for (int c = threadIdx.x; c < pieces; c += 256) {
+    const u32x4_t v = row[c];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      amax = fmaxf(amax, fabsf(__uint_as_float(v[i] << 16)));
+      amax = fmaxf(amax, fabsf(__uint_as_float(v[i] & 0xffff0000u)));
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = amax;
+  __syncthreads();
+  amax = red[0];
+#pragma unroll
+  for (int i = 1; i < 256 / kWave; ++i) amax = fmaxf(amax, red[i]);
+  const float inv127 = 1.0f / 127.0f;  // constant-folded: the fp32 reciprocal of 127
+  const float s = amax * inv127;
+  if (threadIdx.x == 0) s_a[m] = s;
+  u32x2_t* qrow = reinterpret_cast<u32x2_t*>(xq + m * ldq);
+  for (int c = threadIdx.x; c < pieces; c += 256) {
+    const u32x4_t v = row[c];
+    uint32_t b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float f = __uint_as_float((i & 1) ? (v[i >> 1] & 0xffff0000u) : (v[i >> 1] << 16));
+      float t = s > 0.f ? rintf(__fdiv_rn(f, s)) : 0.f;
+      t = fminf(fmaxf(t, -128.f), 127.f);
+      b[i] = (uint32_t)(int)t & 0xffu;
+    }
+    u32x2_t o;
+    o.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+    o.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    qrow[c] = o;
+  }
+}
+
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
+
+// The wide-M kernel's structure (tiles, 64-row token groups, XCD placement, K split, x ring) with int8
+// activations: the TILED layout's 1 KiB block (lane (g, r): row r, k 16 g .. 16 g + 15 of a 64-k step)
+// is the A operand of v_mfma_i32_16x16x64_i8 as loaded, and the B operand is the 16 activation bytes
+// of token row r at the same k, so there is no conversion work.  The x ring rows (CP 16-byte pieces of
+// 16 activations) are padded by 16 bytes: the 16 rows of a fragment read then sit on distinct 16-byte
+// bank groups.  Sums are exact in int32 (|sum| <= K * 128 * 127 < 2^31 for K < 132000).
+template <int NT, int MT, int WN, int DEPTH>
+__global__ void __launch_bounds__(WN * kWave) w8a8_wide_kernel(const GemmArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  constexpr int THREADS = WN * kWave;
+  constexpr int RING = DEPTH + 1;
+  constexpr int CP = RING * 4;                               // 16-byte pieces per token row of a chunk
+  constexpr int XP = (MT * 16 * CP + THREADS - 1) / THREADS;  // pieces per thread, at most
+  constexpr int ROW = (CP + 1) * 16;
+  constexpr int64_t step_bytes = kTileN * kStepK;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wn = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int g = lane >> 4;
+  const int r = lane & 15;
+
+  const int ntiles = a.n_pad / kTileN;
+  const int nblocks = (ntiles + WN * NT - 1) / (WN * NT);
+  int l = blockIdx.x;
+  if (a.groups > 1) {  // the groups of one (split, n-block) on consecutive workgroups of one XCD
+    const int total = gridDim.x;
+    const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+    const int per = total / kXcds, rem = total % kXcds;
+    l = xcd < rem ? xcd * (per + 1) + j : rem * (per + 1) + (xcd - rem) * per + j;
+  }
+  const int grp = l % a.groups;
+  const int nb = (l / a.groups) % nblocks;
+  const int split = l / a.groups / nblocks;
+  int s_begin, s_end;
+  split_range(split, a.split_k, a.ksteps, s_begin, s_end);
+  const int m0 = grp * a.group_rows;
+  const int mg = min(a.group_rows, a.M - m0);  // >= 1
+  const int8_t* xg = a.xq + (int64_t)m0 * a.ldx;
+
+  const int tile0 = (nb * WN + wn) * NT;
+  const int k_count = s_end - s_begin;
+  const int nsteps = tile0 < ntiles ? k_count : 1;
+  const int8_t* wp[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int tile = min(tile0 + t, ntiles - 1);
+    wp[t] = a.w + (((int64_t)tile * a.ksteps + s_begin) * kWave + lane) * 16;
+  }
+
+  u32x4_t buf[RING][NT];
+  i32x4_t acc[NT][MT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = (i32x4_t){0, 0, 0, 0};
+  int xoff[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) xoff[mt] = min(mt * 16 + r, mg - 1) * ROW + g * 16;
+
+  const int cpieces = mg * CP;
+  const int slot_bytes = mg * ROW;
+  const int nchunks = (k_count + RING - 1) / RING;
+  const int64_t kmax = (int64_t)s_end * kStepK - 16;  // last 16-activation piece of the range
+  u32x4_t xv[XP];
+  auto load_chunk = [&](int c) {
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+      const int q = min(j * THREADS + (int)threadIdx.x, cpieces - 1);
+      const int m = q / CP;
+      const int64_t k = min((int64_t)(s_begin + c * RING) * kStepK + (q - m * CP) * 16, kmax);
+      xv[j] = *reinterpret_cast<const u32x4_t*>(xg + (int64_t)m * a.ldx + k);
+    }
+  };
+  auto store_chunk = [&](int c) {
+    uint8_t* slot = smem + (c & 1) * slot_bytes;
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+      const int q = min(j * THREADS + (int)threadIdx.x, cpieces - 1);
+      *reinterpret_cast<u32x4_t*>(slot + q * 16 + q / CP * 16) = xv[j];
+    }
+  };
+
+  load_chunk(0);
+  __builtin_amdgcn_sched_barrier(0);  // the x requests go out before the weight requests
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) {
+    const int sd = min(d, nsteps - 1);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) buf[d][t] = load16<true>(wp[t] + sd * step_bytes);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  store_chunk(0);
+  for (int c = 0; c < nchunks; ++c) {
+    if (c > 0) store_chunk(c);
+    lds_barrier();  // the weight requests stay in flight across it
+    if (c + 1 < nchunks) load_chunk(c + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t* slot = smem + (c & 1) * slot_bytes;
+#pragma unroll
+    for (int d = 0; d < RING; ++d) {
+      const int s = c * RING + d;
+      const int sn = min(s + DEPTH, nsteps - 1);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) buf[(d + DEPTH) % RING][t] = load16<true>(wp[t] + (int64_t)sn * step_bytes);
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch issue ahead of this step's math
+      if (s < nsteps) {                   // uniform
+        i32x4_t xb[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) xb[mt] = *reinterpret_cast<const i32x4_t*>(slot + xoff[mt] + d * 64);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const i32x4_t wv = __builtin_bit_cast(i32x4_t, buf[d][t]);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            acc[t][mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wv, xb[mt], acc[t][mt], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // Lane (g, r) holds C[n = tile*16 + 4g + i][m = 16 mt + r] of the group, i = 0..3.
+  if (tile0 >= ntiles) return;
+  if (a.split_k > 1) {  // exact int32 partial sums [split][M][n_pad], summed by splitk_reduce_w8a8_kernel
+    int32_t* part = reinterpret_cast<int32_t*>(a.partial) + (int64_t)split * a.M * a.n_pad;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int tile = tile0 + t;
+      if (tile < ntiles) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int m = mt * 16 + r;
+          if (m < mg)
+            *reinterpret_cast<i32x4_t*>(part + (int64_t)(m0 + m) * a.n_pad + tile * kTileN + 4 * g) = acc[t][mt];
+        }
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int tile = tile0 + t;
+    const int n = tile * kTileN + 4 * g;
+    if (tile < ntiles && n < a.N) {
+      const f32x4_t sc = load_scale4(a.scale, a.N, n);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = mt * 16 + r;
+        if (m < mg) {
+          const i32x4_t v = acc[t][mt];
+          const f32x4_t f = {(float)v.x, (float)v.y, (float)v.z, (float)v.w};
+          store_out4(a.y, a.ldy, a.out_f32, a.vec_out, m0 + m, n, min(4, a.N - n), (f * a.s_tok[m0 + m]) * sc);
+        }
+      }
+    }
+  }
+}
+
+// Sum of the W8A8 kernel's int32 split partials (exact in any order), then the scales.
+__global__ void __launch_bounds__(256) splitk_reduce_w8a8_kernel(const GemmArgs a) {
+  const int groups = a.n_pad / 4;
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= a.M * groups) return;
+  const int m = idx / groups;
+  const int n = (idx - m * groups) * 4;
+  if (n >= a.N) return;
+  const int64_t plane = (int64_t)a.M * a.n_pad;
+  const int32_t* p = reinterpret_cast<const int32_t*>(a.partial) + (int64_t)m * a.n_pad + n;
+  i32x4_t sum = *reinterpret_cast<const i32x4_t*>(p);
+  for (int j = 1; j < a.split_k; ++j) sum += *reinterpret_cast<const i32x4_t*>(p + j * plane);
+  const f32x4_t f = {(float)sum.x, (float)sum.y, (float)sum.z, (float)sum.w};
+  const f32x4_t sc = load_scale4(a.scale, a.N, n);
+  store_out4(a.y, a.ldy, a.out_f32, a.vec_out, m, n, min(4, a.N - n), (f * a.s_tok[m]) * sc);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1893,6 +2126,139 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
   return st;
 }
 
+// ---------------------------------------------------------------------------------------------
+// W8A8 GEMM on TILED weights (QF_KERNEL_MFMA_W8A8)
+// ---------------------------------------------------------------------------------------------
+
+// Instantiations: NT {2, 4} x MT {1..4} x WN {4, 8} x DEPTH {2, 4}.
+template <int NT, int MT>
+KernelFn w8a8_by_shape(int wn, int depth) {
+  if (wn == 4 && depth == 2) return &w8a8_wide_kernel<NT, MT, 4, 2>;
+  if (wn == 4 && depth == 4) return &w8a8_wide_kernel<NT, MT, 4, 4>;
+  if (wn == 8 && depth == 2) return &w8a8_wide_kernel<NT, MT, 8, 2>;
+  if (wn == 8 && depth == 4) return &w8a8_wide_kernel<NT, MT, 8, 4>;
+  return nullptr;
+}
+
+template <int NT>
+KernelFn w8a8_by_mt(int mt, int wn, int depth) {
+  switch (mt) {
+    case 1: return w8a8_by_shape<NT, 1>(wn, depth);
+    case 2: return w8a8_by_shape<NT, 2>(wn, depth);
+    case 3: return w8a8_by_shape<NT, 3>(wn, depth);
+    case 4: return w8a8_by_shape<NT, 4>(wn, depth);
+    default: return nullptr;
+  }
+}
+
+KernelFn select_w8a8(int nt, int mt, int waves, int depth) {
+  if (nt == 2) return w8a8_by_mt<2>(mt, waves, depth);
+  if (nt == 4) return w8a8_by_mt<4>(mt, waves, depth);
+  return nullptr;
+}
+
+// LDS of one workgroup: two chunks of the group's rows, (depth + 1) 64-byte steps and a 16-byte pad each.
+size_t w8a8_lds_bytes(const qf_w8a16_config& c, int M) {
+  int groups, rows;
+  wide_groups(M, groups, rows);
+  return (size_t)2 * rows * ((c.depth + 1) * kStepK + 16);
+}
+
+int validate_w8a8(int M, int N, int K, int layout, const qf_w8a16_config& c) {
+  const int ksteps = K / kStepK;
+  if (c.kernel != QF_KERNEL_MFMA_W8A8) return QF_ERR_INVALID_ARG;
+  if (c.split_k < 1 || c.split_k > ksteps || c.waves < 1 || c.k_waves < 1 || c.tiles_per_wave < 1)
+    return QF_ERR_INVALID_ARG;
+  if (layout != QF_LAYOUT_TILED || c.k_waves != 1 || K >= 132000) return QF_ERR_UNSUPPORTED;
+  int groups, rows;
+  wide_groups(M, groups, rows);
+  if ((int64_t)workgroups(c, N) * groups * c.split_k > 0x7fffffff) return QF_ERR_UNSUPPORTED;
+  if (select_w8a8(c.tiles_per_wave, rows / 16, c.waves, c.depth) == nullptr) return QF_ERR_UNSUPPORTED;
+  return w8a8_lds_bytes(c, M) > kMaxLds ? QF_ERR_UNSUPPORTED : QF_OK;
+}
+
+// Automatic W8A8 configuration (TILED weights, any M): 8 wavefronts of 2 tiles, 4 steps in flight, and
+// K split across workgroups until they number 128 (at most 8 ways and 16 steps a split).  Measured on
+// the dense 27B-class layer at M = 64 .. 2048 against 4-tile and 4-wavefront shapes at depth 2 and 4:
+// within 9% of the best shape everywhere (gate_up M = 2048: 565 us against 533 for 4 tiles, 677 for
+// 4 wavefronts of 4 tiles).
+bool auto_config_w8a8(int M, int N, int K, int layout, qf_w8a16_config* c) {
+  if (M < 1 || N < 1 || K < QF_W8A16_K_ALIGN || K % QF_W8A16_K_ALIGN || layout != QF_LAYOUT_TILED) return false;
+  *c = qf_w8a16_config{};
+  c->kernel = QF_KERNEL_MFMA_W8A8;
+  c->k_waves = 1;
+  c->load_hint = 1;
+  c->reduce = 1;
+  c->split_k = 1;
+  c->tiles_per_wave = 2;
+  c->waves = 8;
+  c->depth = 4;
+  int groups, rows;
+  wide_groups(M, groups, rows);
+  const int64_t wgs = (int64_t)workgroups(*c, N) * groups;
+  const int ksteps = K / kStepK;
+  while (wgs * c->split_k < 128 && c->split_k < 8 && ksteps / (c->split_k + 1) >= 16) ++c->split_k;
+  return validate_w8a8(M, N, K, layout, *c) == QF_OK;
+}
+
+int resolve_w8a8(int M, int N, int K, int layout, const qf_w8a16_config* in, qf_w8a16_config* out) {
+  if (!auto_config_w8a8(M, N, K, layout, out)) return QF_ERR_UNSUPPORTED;
+  if (in == nullptr || in->kernel == QF_KERNEL_AUTO) return QF_OK;
+  qf_w8a16_config c = *in;
+  if (c.waves == 0) c.waves = 4;
+  if (c.k_waves == 0) c.k_waves = 1;
+  if (c.tiles_per_wave == 0) c.tiles_per_wave = 4;
+  if (c.depth == 0) c.depth = 4;
+  if (c.split_k == 0) c.split_k = 1;
+  const int rc = validate_w8a8(M, N, K, layout, c);
+  if (rc != QF_OK) return rc;
+  *out = c;
+  return QF_OK;
+}
+
+int run_w8a8(const int8_t* xq, int64_t ldq, const float* s_a, const int8_t* w, int layout, const float* scale,
+             void* y, int64_t ldy, int out_dtype, int M, int N, int K, const qf_w8a16_config* cfg, void* workspace,
+             size_t workspace_bytes, void* stream) {
+  if (xq == nullptr || s_a == nullptr || w == nullptr || scale == nullptr || y == nullptr) return QF_ERR_INVALID_ARG;
+  if (M < 1 || N < 1 || K < 1 || ldq < K || ldy < N) return QF_ERR_INVALID_ARG;
+  if (layout != QF_LAYOUT_ROWMAJOR && layout != QF_LAYOUT_TILED) return QF_ERR_INVALID_ARG;
+  if (out_dtype != QF_DTYPE_BF16 && out_dtype != QF_DTYPE_F32) return QF_ERR_INVALID_ARG;
+  if (layout != QF_LAYOUT_TILED || K % QF_W8A16_K_ALIGN) return QF_ERR_UNSUPPORTED;
+  if (!aligned16(xq) || !aligned16(w) || !aligned16(scale) || !aligned16(y) || ldq % 16) return QF_ERR_UNSUPPORTED;
+  qf_w8a16_config c;
+  const int rc = resolve_w8a8(M, N, K, layout, cfg, &c);
+  if (rc != QF_OK) return rc;
+  const size_t need = workspace_for(c, M, N);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))) return QF_ERR_WORKSPACE;
+
+  GemmArgs a{};
+  a.xq = xq;
+  a.s_tok = s_a;
+  a.w = w;
+  a.scale = scale;
+  a.y = y;
+  a.partial = need > 0 ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + QF_W8A16_COUNTER_BYTES)
+                       : nullptr;
+  a.ldx = ldq;
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.n_pad = round_up16(N);
+  a.ksteps = K / kStepK;
+  a.split_k = c.split_k;
+  a.out_f32 = out_dtype == QF_DTYPE_F32;
+  a.vec_out = (ldy % 4) == 0;
+  wide_groups(M, a.groups, a.group_rows);
+  KernelFn fn = select_w8a8(c.tiles_per_wave, a.group_rows / 16, c.waves, c.depth);
+  if (fn == nullptr) return QF_ERR_UNSUPPORTED;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int st = launch(fn, dim3(workgroups(c, N) * a.groups * c.split_k), dim3(c.waves * kWave), w8a8_lds_bytes(c, M), s,
+                  a);
+  if (st != QF_OK || c.split_k == 1) return st;
+  return launch(&splitk_reduce_w8a8_kernel, dim3(ceil_div(M * (a.n_pad / 4), 256)), dim3(256), 0, s, a);
+}
+
 }  // namespace qf
 
 using namespace qf;
@@ -2020,6 +2386,34 @@ int qf_quantize_rows_int8(const uint16_t* w, int64_t ldw, int8_t* q, float* s, i
                        q, s, H);
   }
   return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
+}
+
+int qf_quantize_tokens_int8(const uint16_t* x, int64_t ldx, int M, int K, int8_t* xq, int64_t ldq, float* s_a,
+                            void* stream) {
+  if (x == nullptr || xq == nullptr || s_a == nullptr || M < 1 || K < 1 || ldx < K || ldq < K) return QF_ERR_INVALID_ARG;
+  if (K % QF_W8A16_K_ALIGN || !aligned16(x) || ldx % 8 || (uintptr_t)xq % 8 || ldq % 8) return QF_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(quantize_tokens_kernel, dim3(M), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), x, ldx, K,
+                     xq, ldq, s_a);
+  return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
+}
+
+int qf_w8a8_pick_config(int M, int N, int K, int layout, qf_w8a16_config* cfg) {
+  if (cfg == nullptr) return QF_ERR_INVALID_ARG;
+  return auto_config_w8a8(M, N, K, layout, cfg) ? QF_OK : QF_ERR_UNSUPPORTED;
+}
+
+size_t qf_w8a8_workspace_bytes(int M, int N, int K, int layout, const qf_w8a16_config* cfg) {
+  qf_w8a16_config c;
+  if (resolve_w8a8(M, N, K, layout, cfg, &c) != QF_OK) return 0;
+  return workspace_for(c, M, N);
+}
+
+int qf_w8a8_gemm(const int8_t* xq, int64_t ldq, const float* s_a, const int8_t* w, int64_t ldw, int layout,
+                 const float* scale, void* y, int64_t ldy, int out_dtype, int M, int N, int K,
+                 const qf_w8a16_config* cfg, void* workspace, size_t workspace_bytes, void* stream) {
+  (void)ldw;  // the TILED image has no row stride
+  return run_w8a8(xq, ldq, s_a, w, layout, scale, y, ldy, out_dtype, M, N, K, cfg, workspace, workspace_bytes,
+                  stream);
 }
 
 int qf_read_probe(const void* buf, size_t bytes, uint32_t* sink, int blocks, void* stream) {

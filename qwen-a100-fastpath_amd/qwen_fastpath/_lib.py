@@ -29,6 +29,7 @@ KERNEL_GEMV = 1
 KERNEL_MFMA = 2
 KERNEL_MFMA_XRING = 3
 KERNEL_MFMA_WIDE = 4
+KERNEL_MFMA_W8A8 = 5
 
 MAX_M = 16
 K_ALIGN = 64
@@ -50,6 +51,10 @@ EXPORTS = (
     "qf_w8a16_gemm_argmax",
     "qf_w8a16_argmax_workspace_bytes",
     "qf_read_probe",
+    "qf_quantize_tokens_int8",
+    "qf_w8a8_gemm",
+    "qf_w8a8_pick_config",
+    "qf_w8a8_workspace_bytes",
 )
 
 
@@ -132,6 +137,14 @@ def load() -> ctypes.CDLL:
     L.qf_w8a16_gemm_argmax.restype = i32
     L.qf_w8a16_argmax_workspace_bytes.argtypes = [i32, i32, i32, i32, ctypes.POINTER(Config)]
     L.qf_w8a16_argmax_workspace_bytes.restype = sz
+    L.qf_quantize_tokens_int8.argtypes = [p, i64, i32, i32, p, i64, p, p]
+    L.qf_quantize_tokens_int8.restype = i32
+    L.qf_w8a8_gemm.argtypes = [p, i64, p, p, i64, i32, p, p, i64, i32, i32, i32, i32, ctypes.POINTER(Config), p, sz, p]
+    L.qf_w8a8_gemm.restype = i32
+    L.qf_w8a8_pick_config.argtypes = [i32, i32, i32, i32, ctypes.POINTER(Config)]
+    L.qf_w8a8_pick_config.restype = i32
+    L.qf_w8a8_workspace_bytes.argtypes = [i32, i32, i32, i32, ctypes.POINTER(Config)]
+    L.qf_w8a8_workspace_bytes.restype = sz
     L.qf_read_probe.argtypes = [p, sz, p, i32, p]
     L.qf_read_probe.restype = i32
     v = L.qf_abi_version()
@@ -159,6 +172,15 @@ def pick_config(M: int, N: int, K: int, layout: int = LAYOUT_ROWMAJOR) -> Config
     if rc == ERR_UNSUPPORTED:
         return None
     check(rc, "qf_w8a16_pick_config")
+    return c
+
+
+def w8a8_pick_config(M: int, N: int, K: int, layout: int = LAYOUT_TILED) -> Config | None:
+    c = Config()
+    rc = load().qf_w8a8_pick_config(M, N, K, layout, ctypes.byref(c))
+    if rc == ERR_UNSUPPORTED:
+        return None
+    check(rc, "qf_w8a8_pick_config")
     return c
 
 

@@ -28,7 +28,8 @@ from typing import Callable, NamedTuple, Optional
 import torch
 
 from . import _lib as L
-from .w8a16 import ROWMAJOR, SMALL_M, TILED, pick_config, to_tiled, w8a16_mm, w8a16_mm_argmax, w8a16_mm_prefill
+from .w8a16 import (ROWMAJOR, SMALL_M, TILED, pick_config, to_tiled, w8a16_mm, w8a16_mm_argmax, w8a16_mm_prefill,
+                    w8a8_mm)
 
 logger = logging.getLogger("vllm.qwen_fastpath")
 
@@ -209,7 +210,24 @@ _fallback_impl: Optional[Callable] = None
 TILED_WIDE_MAX_M = 1024
 
 
+def prefill_arithmetic() -> str:
+    """QWEN_FAST_LINEAR_PREFILL: the arithmetic of M > 16 calls on TILED layers.  "w8a8" (default) is the
+    reference's own M > 16 arithmetic (per-token int8 activations, exact integer sums:
+    scaled_int8_quant + cutlass_scaled_mm, patches.py:99-100) on the int8 MFMA; "w8a16" keeps the decode
+    path's arithmetic (exact bf16 products, fp32 sums) at every M."""
+    v = os.environ.get("QWEN_FAST_LINEAR_PREFILL", "w8a8").strip().lower()
+    if v not in ("w8a8", "w8a16"):
+        raise ValueError(f"QWEN_FAST_LINEAR_PREFILL must be w8a8 or w8a16, got {v!r}")
+    return v
+
+
 def _fallback(x2, w_q, w_s, bias, out_dtype, layout):
+    if layout == TILED and prefill_arithmetic() == "w8a8":
+        # The reference's M > 16 arithmetic, on the TILED image CUTLASS cannot read: per-token int8
+        # activations times the int8 weights on v_mfma_i32_16x16x64_i8 (gate_up M = 512: 169 us,
+        # M = 2048: 565 us, against 241 / 723 us for the W8A16 routes below).
+        y = w8a8_mm(x2, w_q, w_s.reshape(-1), out_dtype)
+        return y if bias is None else y + bias
     if layout == TILED:
         # No W8A8 library kernel reads the permuted image.  Up to TILED_WIDE_MAX_M rows the wide-M
         # kernel runs (one launch, each weight fragment feeding up to 64 token rows); above, the

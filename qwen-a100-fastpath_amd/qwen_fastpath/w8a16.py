@@ -292,6 +292,58 @@ def scale_cast_bf16(acc: torch.Tensor, w_scale: torch.Tensor, out: torch.Tensor)
     return out
 
 
+def quantize_tokens_int8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dynamic symmetric per-token int8 quantisation (qf_quantize_tokens_int8): s_a[m] = amax|x[m]| /
+    127 (as the fp32 reciprocal product), xq = clamp(round_half_even(x / s_a), -128, 127), zero rows -> 0.
+    The arithmetic of vLLM's scaled_int8_quant(x, symmetric=True) at the reference's fallback
+    (plugin/qwen_fastpath/patches.py:99).  x bf16 [M, K], K % 64 == 0.  Returns (xq int8 [M, K], s_a fp32 [M])."""
+    if x.dim() != 2 or x.dtype != torch.bfloat16:
+        raise TypeError("x must be a 2-D bf16 tensor")
+    M, K = x.shape
+    if x.stride(1) != 1 or x.data_ptr() % 16 or (M > 1 and x.stride(0) % 8):
+        x = x.contiguous()
+    xq = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    s_a = torch.empty((M,), dtype=torch.float32, device=x.device)
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    L.check(L.load().qf_quantize_tokens_int8(x.data_ptr(), x.stride(0) if M > 1 else K, M, K, xq.data_ptr(), K,
+                                             s_a.data_ptr(), stream), "qf_quantize_tokens_int8")
+    return xq, s_a
+
+
+def w8a8_mm(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, out_dtype: torch.dtype, cfg=None,
+            layout: int = TILED) -> torch.Tensor:
+    """y = ((xq @ W^T) * s_a) * w_scale with per-token int8 activations (quantize_tokens_int8), exact
+    int32 sums on the int8 MFMA, on weights in the TILED image: the arithmetic of the reference's
+    M > 16 fallback, scaled_int8_quant + cutlass_scaled_mm (plugin/qwen_fastpath/patches.py:99-100),
+    for a layer whose weights CUTLASS cannot read.  Any M."""
+    lib = L.load()
+    if w_scale.dtype != torch.float32:
+        raise TypeError(f"w_scale must be fp32, got {w_scale.dtype}")
+    M, K = x.shape
+    N = w_scale.numel()
+    _weight_geometry(w, N, K, layout)
+    xq, s_a = quantize_tokens_int8(x)
+    s = w_scale.reshape(-1)
+    if not s.is_contiguous() or s.data_ptr() % 16:
+        s = s.clone(memory_format=torch.contiguous_format)
+    if out_dtype == torch.bfloat16:
+        dt = L.DTYPE_BF16
+    elif out_dtype == torch.float32:
+        dt = L.DTYPE_F32
+    else:
+        raise TypeError(f"out_dtype must be bf16 or fp32, got {out_dtype}")
+    y = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    c = _config_struct(AUTO if cfg is None else cfg)
+    ws_bytes = int(lib.qf_w8a8_workspace_bytes(M, N, K, layout, ctypes.byref(c)))
+    ws = _workspace(x.device, ws_bytes) if ws_bytes else None
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    rc = lib.qf_w8a8_gemm(xq.data_ptr(), K, s_a.data_ptr(), w.data_ptr(), 0, layout, s.data_ptr(), y.data_ptr(), N,
+                          dt, M, N, K, ctypes.byref(c), ws.data_ptr() if ws is not None else None,
+                          ws.numel() if ws is not None else 0, stream)
+    L.check(rc, f"qf_w8a8_gemm(M={M}, N={N}, K={K}, layout={layout})")
+    return y
+
+
 def w8a16_mm_prefill(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, out_dtype: torch.dtype,
                      layout: int = TILED, chunk_rows: int | None = None) -> torch.Tensor:
     """y[M, N] = (x @ W^T) * w_scale for any M, the same product as w8a16_mm: the int8 weights are

@@ -236,3 +236,45 @@ def test_pick_config_wide_m_on_tiled_weights():
     c = L.Config.from_seq((L.KERNEL_MFMA_WIDE, 1, 2, 8, 4, 1, 1, 0))
     assert _gemm(x=fake, w=fake, s=fake, y=fake, layout=0, M=40, cfg=c) == L.ERR_UNSUPPORTED  # row-major
     assert _gemm(x=fake, w=fake, s=fake, y=fake, layout=0, M=40) == L.ERR_UNSUPPORTED
+
+
+def test_prefill_arithmetic_switch(monkeypatch):
+    """QWEN_FAST_LINEAR_PREFILL picks the arithmetic of M > 16 calls on TILED layers: the reference's W8A8
+    by default, W8A16 on request; anything else is an error rather than a silent choice."""
+    from qwen_fastpath import patches as P
+    monkeypatch.delenv("QWEN_FAST_LINEAR_PREFILL", raising=False)
+    assert P.prefill_arithmetic() == "w8a8"
+    for v, want in (("w8a16", "w8a16"), (" W8A8 ", "w8a8"), ("W8A16", "w8a16")):
+        monkeypatch.setenv("QWEN_FAST_LINEAR_PREFILL", v)
+        assert P.prefill_arithmetic() == want
+    monkeypatch.setenv("QWEN_FAST_LINEAR_PREFILL", "fp8")
+    with pytest.raises(ValueError):
+        P.prefill_arithmetic()
+
+
+def test_w8a8_configs_host_only():
+    """qf_w8a8_gemm: TILED weights only, its own kernel kind, any M; refused before any launch otherwise."""
+    lib = L.load()
+    for M in (1, 17, 64, 300, 2048):
+        for (N, K) in ((34816, 5120), (5120, 17408), (1000, 1024), (16, 64)):
+            c = L.w8a8_pick_config(M, N, K)
+            assert c is not None and c.kernel == L.KERNEL_MFMA_W8A8 and c.k_waves == 1, (M, N, K)
+            assert L.w8a8_pick_config(M, N, K, 0) is None  # row-major weights
+    fake = 1 << 20
+    def call(layout=1, cfg=None, M=40, K=1024, ldq=1024):
+        return lib.qf_w8a8_gemm(fake, ldq, fake, fake, 0, layout, fake, fake, 1000, 0, M, 1000, K,
+                                ctypes.byref(cfg) if cfg is not None else None, None, 0, None)
+    assert call(layout=0) == L.ERR_UNSUPPORTED
+    assert call(K=1000, ldq=1000) == L.ERR_UNSUPPORTED                     # K % 64
+    assert call(ldq=1024 + 8) == L.ERR_UNSUPPORTED                          # ldq % 16
+    assert call(M=0) == L.ERR_INVALID_ARG
+    for bad in ((L.KERNEL_MFMA_W8A8, 1, 1, 8, 4, 1, 1, 0), (L.KERNEL_MFMA_W8A8, 1, 2, 8, 8, 1, 1, 0),
+                (L.KERNEL_MFMA_W8A8, 1, 2, 16, 4, 1, 1, 0), (L.KERNEL_MFMA_WIDE, 1, 2, 8, 4, 1, 1, 0)):
+        assert call(cfg=L.Config.from_seq(bad)) != L.OK, bad
+    split = L.Config.from_seq((L.KERNEL_MFMA_W8A8, 2, 2, 8, 4, 1, 1, 1))
+    assert call(cfg=split) == L.ERR_WORKSPACE
+    # the W8A16 entry point does not take the W8A8 kind
+    assert _gemm(x=fake, w=fake, s=fake, y=fake, layout=1, M=40, K=1024, ldx=1024, ldw=1024,
+                 cfg=L.Config.from_seq((L.KERNEL_MFMA_W8A8, 1, 2, 8, 4, 1, 1, 0))) == L.ERR_INVALID_ARG
+    assert lib.qf_quantize_tokens_int8(None, 64, 1, 64, fake, 64, fake, None) == L.ERR_INVALID_ARG
+    assert lib.qf_quantize_tokens_int8(fake, 100, 1, 100, fake, 100, fake, None) == L.ERR_UNSUPPORTED  # K % 64

@@ -242,10 +242,11 @@ def test_top_tokens_row_split(oracle, M, N, num_pad):
         assert np.array_equal(ids, oracle.argmax_rows(bits, N - num_pad, 5))
 
 
-def test_load_time_tiled_repack(oracle):
+def test_load_time_tiled_repack(oracle, monkeypatch):
     """QWEN_FAST_LINEAR_LAYOUT=tiled: after the kernel class's own process_weights_after_loading has
     laid the checkpoint's [N, K] weight out as the [K, N] column-major view, the weight is replaced by
-    its TILED image (one copy); decode calls and M > 16 calls (16-row slices) both stay correct."""
+    its TILED image (one copy); decode calls and M > 16 calls (the reference's W8A8 arithmetic by
+    default, the W8A16 one with QWEN_FAST_LINEAR_PREFILL=w8a16) both stay correct."""
     class Kernel:  # stand-in for vLLM's int8 scaled-mm kernel class
         def process_weights_after_loading(self, layer):
             layer.weight = torch.nn.Parameter(layer.weight.t(), requires_grad=False)
@@ -268,7 +269,14 @@ def test_load_time_tiled_repack(oracle):
     assert oracle.check_w8a16(bf16_bits(y), inp.x, inp.w, inp.s).ok
     rng = np.random.default_rng(9)
     x20 = oracle.bf16_from_f64(rng.standard_normal((20, K)))
+    monkeypatch.setenv("QWEN_FAST_LINEAR_PREFILL", "w8a16")
     y20 = Kernel().apply_weights(layer, to_dev_bf16(x20, DEV))
     torch.cuda.synchronize()
     assert y20.shape == (20, N) and oracle.check_w8a16(bf16_bits(y20), x20, inp.w, inp.s).ok
+    monkeypatch.delenv("QWEN_FAST_LINEAR_PREFILL")
+    y20 = Kernel().apply_weights(layer, to_dev_bf16(x20, DEV))
+    ref = P.w8a8_reference(to_dev_bf16(x20, DEV), torch.from_numpy(inp.w).to(DEV).t(), torch.from_numpy(inp.s).to(DEV),
+                           None, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(y20.view(torch.int16), ref.view(torch.int16))
     assert not qf.repack_layer_weight(_Layer(torch.zeros(4, 4, dtype=torch.float32, device=DEV), None))

@@ -49,16 +49,29 @@ def test_prefill_tiled_against_oracle(oracle, M):
 
 
 @pytest.mark.parametrize("M", [40, 260, 1100])
-def test_prefill_dispatcher_on_tiled_layer(oracle, M):
-    """torch.ops.qwen_fastpath.qf_int8_linear with layout=TILED and M > 16: the wide-M kernel up to
-    1024 rows, the widened bf16 library GEMM above."""
+@pytest.mark.parametrize("mode", ["w8a8", "w8a16"])
+def test_prefill_dispatcher_on_tiled_layer(oracle, monkeypatch, M, mode):
+    """torch.ops.qwen_fastpath.qf_int8_linear with layout=TILED and M > 16.  Default (w8a8): the
+    reference's W8A8 arithmetic on the int8 MFMA, bitwise equal to the package's restatement of it.
+    QWEN_FAST_LINEAR_PREFILL=w8a16: the wide-M kernel up to 1024 rows, the widened bf16 library GEMM
+    above, within the W8A16 tolerance of the exact product."""
+    from qwen_fastpath import patches as P
+    if mode == "w8a16":
+        monkeypatch.setenv("QWEN_FAST_LINEAR_PREFILL", "w8a16")
+    else:
+        monkeypatch.delenv("QWEN_FAST_LINEAR_PREFILL", raising=False)
     N, K = 512, 1024
     inp = oracle.gen_inputs(M, N, K, seed=M)
     x, w, s = dev_inputs(inp, DEV)
     y = torch.ops.qwen_fastpath.qf_int8_linear(x.view(2, M // 2, K), qf.to_tiled(w), s, None, qf.TILED)
     torch.cuda.synchronize()
     assert y.shape == (2, M // 2, N)
-    assert oracle.check_w8a16(bf16_bits(y.view(M, N)), inp.x, inp.w, inp.s).ok
+    if mode == "w8a16":
+        assert oracle.check_w8a16(bf16_bits(y.view(M, N)), inp.x, inp.w, inp.s).ok
+    else:
+        ref = P.w8a8_reference(x, w, s, None, torch.bfloat16)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(M, N).view(torch.int16), ref.view(torch.int16))
 
 
 @pytest.mark.parametrize("M,N,offset", [(1, 8, 0), (7, 1000, 0), (64, 8192, 0), (33, 1001, 0), (5, 64, 1)])

@@ -1,0 +1,110 @@
+"""GPU parity of the W8A8 path on TILED weights (qf_quantize_tokens_int8 + qf_w8a8_gemm), the arithmetic
+of the reference's M > 16 fallback (scaled_int8_quant + cutlass_scaled_mm, plugin/qwen_fastpath/
+patches.py:99-100).  Pinned bit for bit against the package's torch restatement of that arithmetic
+(patches.w8a8_reference: per-token scale amax / 127, half-even rounding, exact integer sums,
+(sum * s_a) * s_w), and against the reference's published W8A8 error statistic."""
+import numpy as np
+import pytest
+import torch
+
+import qwen_fastpath as qf
+from qwen_fastpath import _lib as L
+from qwen_fastpath import patches as P
+from helpers import dev_inputs
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def bits(t):
+    return t.view(torch.int16 if t.dtype == torch.bfloat16 else torch.int32)
+
+
+def random_case(M, N, K, seed):
+    g = torch.Generator(device=DEV)
+    g.manual_seed(seed)
+    w = torch.randint(-128, 128, (N, K), dtype=torch.int8, device=DEV, generator=g)
+    s = (torch.rand(N, device=DEV, generator=g) * 0.004 + 1e-4).float()
+    x = (torch.randn(M, K, device=DEV, generator=g) * torch.exp2(torch.randint(-4, 5, (M, 1), device=DEV,
+                                                                               generator=g).float()))
+    return x.to(torch.bfloat16), w, s
+
+
+def test_quantize_tokens_closed_form():
+    """s_a = amax * fl(1/127); xq = clamp(rint(x / s_a)) with an IEEE division; a zero row gives 0 / 0;
+    rows holding the extremes quantise them to +-127 (and -128 never, as |x| <= amax)."""
+    M, K = 37, 5120
+    x, _, _ = random_case(M, 8, K, 1)
+    x[3] = 0
+    x[5, 7] = -1e4
+    xq, s_a = qf.quantize_tokens_int8(x)
+    xf = x.float()
+    amax = xf.abs().amax(dim=-1)
+    s_ref = amax * torch.tensor(1.0 / 127.0, dtype=torch.float32, device=DEV)
+    q_ref = torch.where(s_ref[:, None] > 0, torch.round(xf / torch.where(s_ref > 0, s_ref, 1.0)[:, None]),
+                        torch.zeros_like(xf)).clamp(-128, 127).to(torch.int8)
+    torch.cuda.synchronize()
+    assert torch.equal(s_a, s_ref)
+    assert torch.equal(xq, q_ref)
+    assert s_a[3].item() == 0.0 and int(xq[3].abs().max()) == 0
+    assert int(xq[5, 7]) == -127
+
+
+@pytest.mark.parametrize("M", [17, 64, 100, 300])
+def test_w8a8_matches_restatement(M):
+    N, K = 1000, 2048
+    x, w, s = random_case(M, N, K, M)
+    y = qf.w8a8_mm(x, qf.to_tiled(w.t()), s, torch.bfloat16)
+    ref = P.w8a8_reference(x, w.t(), s, None, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(bits(y), bits(ref)), M
+
+
+W8A8_SHAPES = [(nt, waves, depth) for nt in (2, 4) for waves in (4, 8) for depth in (2, 4)]
+
+
+@pytest.mark.parametrize("nt,waves,depth", W8A8_SHAPES)
+def test_w8a8_configs_and_splits_bitwise(nt, waves, depth):
+    """Every instantiated (tiles, wavefronts, depth) at 1..4 token tiles and several groups, K splits
+    with uneven ranges, fp32 output; int32 sums make every split order exact."""
+    N, K = 1000, 1024
+    x, w, s = random_case(160, N, K, 7 + nt + waves + depth)
+    wt = qf.to_tiled(w.t())
+    for M in (1, 16, 20, 48, 64, 100, 160):
+        for split in (1, 3):
+            cfg = (L.KERNEL_MFMA_W8A8, split, nt, waves, depth, 1, 1, 1)
+            y = qf.w8a8_mm(x[:M], wt, s, torch.bfloat16, cfg)
+            ref = P.w8a8_reference(x[:M], w.t(), s, None, torch.bfloat16)
+            torch.cuda.synchronize()
+            assert torch.equal(bits(y), bits(ref)), (nt, waves, depth, M, split)
+    cfg = (L.KERNEL_MFMA_W8A8, 2, nt, waves, depth, 1, 1, 1)
+    y = qf.w8a8_mm(x[:48], wt, s, torch.float32, cfg)
+    assert torch.equal(bits(y), bits(P.w8a8_reference(x[:48], w.t(), s, None, torch.float32)))
+
+
+@pytest.mark.parametrize("name,N,K", [("gate_up", 34816, 5120), ("o_proj", 5120, 8192), ("down", 5120, 17408),
+                                      ("qkv", 10240, 5120)])
+def test_w8a8_layer_shapes(name, N, K):
+    x, w, s = random_case(512, N, K, N ^ K)
+    wt = qf.to_tiled(w.t())
+    for M in (17, 96, 512):
+        y = qf.w8a8_mm(x[:M], wt, s, torch.bfloat16)
+        ref = P.w8a8_reference(x[:M], w.t(), s, None, torch.bfloat16)
+        torch.cuda.synchronize()
+        print(f"{name} M={M} cfg={L.w8a8_pick_config(M, N, K).to_tuple()}", flush=True)
+        assert torch.equal(bits(y), bits(ref)), (name, M)
+
+
+def test_w8a8_error_statistic(oracle):
+    """Against the exact product, the W8A8 path's rel-L2 is the reference's published W8A8 statistic
+    (0.0083-0.0094, data/measurements.json:420-427), as on its own fallback."""
+    M, N, K = 17, 5120, 6144
+    inp = oracle.gen_inputs(M, N, K, seed=4, dist="reftest")
+    x, w, s = dev_inputs(inp, DEV)
+    y = qf.w8a8_mm(x, qf.to_tiled(w), s, torch.bfloat16)
+    torch.cuda.synchronize()
+    ex = oracle.w8a16_f64(inp.x, inp.w, inp.s)
+    yf = y.float().cpu().numpy().astype(np.float64)
+    rel = np.linalg.norm(yf - ex) / np.linalg.norm(ex)
+    assert 0.006 <= rel <= 0.012, rel
