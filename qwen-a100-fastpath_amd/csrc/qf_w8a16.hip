@@ -2130,7 +2130,7 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
 // W8A8 GEMM on TILED weights (QF_KERNEL_MFMA_W8A8)
 // ---------------------------------------------------------------------------------------------
 
-// Instantiations: NT {2, 4} x MT {1..4} x WN {4, 8} x DEPTH {2, 4}.
+// Instantiations: NT {2, 4} x MT {1..4} x WN {4, 8} x DEPTH {2, 4}, and MT {5..8} for NT 2.
 template <int NT, int MT>
 KernelFn w8a8_by_shape(int wn, int depth) {
   if (wn == 4 && depth == 2) return &w8a8_wide_kernel<NT, MT, 4, 2>;
@@ -2147,8 +2147,18 @@ KernelFn w8a8_by_mt(int mt, int wn, int depth) {
     case 2: return w8a8_by_shape<NT, 2>(wn, depth);
     case 3: return w8a8_by_shape<NT, 3>(wn, depth);
     case 4: return w8a8_by_shape<NT, 4>(wn, depth);
-    default: return nullptr;
+    default: break;
   }
+  if constexpr (NT == 2) {
+    switch (mt) {
+      case 5: return w8a8_by_shape<NT, 5>(wn, depth);
+      case 6: return w8a8_by_shape<NT, 6>(wn, depth);
+      case 7: return w8a8_by_shape<NT, 7>(wn, depth);
+      case 8: return w8a8_by_shape<NT, 8>(wn, depth);
+      default: break;
+    }
+  }
+  return nullptr;
 }
 
 KernelFn select_w8a8(int nt, int mt, int waves, int depth) {
@@ -2157,10 +2167,23 @@ KernelFn select_w8a8(int nt, int mt, int waves, int depth) {
   return nullptr;
 }
 
+// Token groups of the W8A8 kernel.  Without the conversion work the int8 MFMAs go twice as fast as the
+// bf16 ones, and then 64-row groups leave a workgroup's k-step short of work for the weight bytes it
+// loads: groups of up to 128 rows are used once the workgroups they give number 128 or more (gate_up
+// M = 2048: 420 us against 552; o_proj M = 1024: 65 against 87), 64-row groups below that (narrow N at
+// small M needs the workgroups; there the K split fills the machine instead).
+void w8a8_groups(const qf_w8a16_config& c, int M, int N, int& groups, int& group_rows) {
+  const int blocks = workgroups(c, N);
+  const int max_rows = (c.tiles_per_wave == 2 && (int64_t)blocks * ((M + 127) / 128) >= 128) ? 128 : 64;
+  const int g0 = (M + max_rows - 1) / max_rows;
+  group_rows = ((M + g0 - 1) / g0 + 15) / 16 * 16;
+  groups = (M + group_rows - 1) / group_rows;
+}
+
 // LDS of one workgroup: two chunks of the group's rows, (depth + 1) 64-byte steps and a 16-byte pad each.
-size_t w8a8_lds_bytes(const qf_w8a16_config& c, int M) {
+size_t w8a8_lds_bytes(const qf_w8a16_config& c, int M, int N) {
   int groups, rows;
-  wide_groups(M, groups, rows);
+  w8a8_groups(c, M, N, groups, rows);
   return (size_t)2 * rows * ((c.depth + 1) * kStepK + 16);
 }
 
@@ -2171,10 +2194,10 @@ int validate_w8a8(int M, int N, int K, int layout, const qf_w8a16_config& c) {
     return QF_ERR_INVALID_ARG;
   if (layout != QF_LAYOUT_TILED || c.k_waves != 1 || K >= 132000) return QF_ERR_UNSUPPORTED;
   int groups, rows;
-  wide_groups(M, groups, rows);
+  w8a8_groups(c, M, N, groups, rows);
   if ((int64_t)workgroups(c, N) * groups * c.split_k > 0x7fffffff) return QF_ERR_UNSUPPORTED;
   if (select_w8a8(c.tiles_per_wave, rows / 16, c.waves, c.depth) == nullptr) return QF_ERR_UNSUPPORTED;
-  return w8a8_lds_bytes(c, M) > kMaxLds ? QF_ERR_UNSUPPORTED : QF_OK;
+  return w8a8_lds_bytes(c, M, N) > kMaxLds ? QF_ERR_UNSUPPORTED : QF_OK;
 }
 
 // Automatic W8A8 configuration (TILED weights, any M): 8 wavefronts of 2 tiles, 4 steps in flight, and
@@ -2194,7 +2217,7 @@ bool auto_config_w8a8(int M, int N, int K, int layout, qf_w8a16_config* c) {
   c->waves = 8;
   c->depth = 4;
   int groups, rows;
-  wide_groups(M, groups, rows);
+  w8a8_groups(*c, M, N, groups, rows);
   const int64_t wgs = (int64_t)workgroups(*c, N) * groups;
   const int ksteps = K / kStepK;
   while (wgs * c->split_k < 128 && c->split_k < 8 && ksteps / (c->split_k + 1) >= 16) ++c->split_k;
@@ -2249,12 +2272,12 @@ int run_w8a8(const int8_t* xq, int64_t ldq, const float* s_a, const int8_t* w, i
   a.split_k = c.split_k;
   a.out_f32 = out_dtype == QF_DTYPE_F32;
   a.vec_out = (ldy % 4) == 0;
-  wide_groups(M, a.groups, a.group_rows);
+  w8a8_groups(c, M, N, a.groups, a.group_rows);
   KernelFn fn = select_w8a8(c.tiles_per_wave, a.group_rows / 16, c.waves, c.depth);
   if (fn == nullptr) return QF_ERR_UNSUPPORTED;
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  int st = launch(fn, dim3(workgroups(c, N) * a.groups * c.split_k), dim3(c.waves * kWave), w8a8_lds_bytes(c, M), s,
-                  a);
+  int st = launch(fn, dim3(workgroups(c, N) * a.groups * c.split_k), dim3(c.waves * kWave), w8a8_lds_bytes(c, M, N),
+                  s, a);
   if (st != QF_OK || c.split_k == 1) return st;
   return launch(&splitk_reduce_w8a8_kernel, dim3(ceil_div(M * (a.n_pad / 4), 256)), dim3(256), 0, s, a);
 }

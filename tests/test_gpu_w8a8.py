@@ -108,3 +108,19 @@ def test_w8a8_error_statistic(oracle):
     yf = y.float().cpu().numpy().astype(np.float64)
     rel = np.linalg.norm(yf - ex) / np.linalg.norm(ex)
     assert 0.006 <= rel <= 0.012, rel
+
+
+@pytest.mark.parametrize("nt,waves,depth", [(2, 8, 4), (2, 8, 2), (2, 4, 4), (2, 4, 2)])
+def test_w8a8_128_row_groups_bitwise(nt, waves, depth):
+    """5..8 token tiles a weight fragment: N wide enough that the 128-row groups are taken (128 or more
+    workgroups), M over one and two groups with ragged tails, with and without a K split."""
+    N, K = 34816, 256
+    x, w, s = random_case(256, N, K, 31 + waves + depth)
+    wt = qf.to_tiled(w.t())
+    for M in (65, 80, 100, 128, 200, 256):
+        for split in (1, 2):
+            cfg = (L.KERNEL_MFMA_W8A8, split, nt, waves, depth, 1, 1, 1)
+            y = qf.w8a8_mm(x[:M], wt, s, torch.bfloat16, cfg)
+            ref = P.w8a8_reference(x[:M], w.t(), s, None, torch.bfloat16)
+            torch.cuda.synchronize()
+            assert torch.equal(bits(y), bits(ref)), (nt, waves, depth, M, split)
