@@ -28,6 +28,11 @@ What is restated here (reference paths relative to the reference repository):
                              correctly rounded value, and max|err|/RMS <= 1e-2 beyond the output's
                              own bf16 quantum.
 * ``check_w8a16_f32``        max|err|/RMS for fp32 outputs (the 1e-2 bound at fp32 precision).
+* ``quantize_tokens``        dynamic symmetric per-token int8 quantisation, the arithmetic of vLLM's
+                             scaled_int8_quant(x, symmetric=True) called at plugin/qwen_fastpath/patches.py:99.
+* ``w8a8_linear``            that quantisation, exact integer sums with the int8 weights, and the
+                             (sum * s_a) * s_w epilogue of cutlass_scaled_mm (patches.py:100): the
+                             reference's M > 16 arithmetic.
 """
 from __future__ import annotations
 
@@ -223,6 +228,36 @@ def ref_pick_config(N: int, K: int):
         if K % (bk * sk) == 0:
             return (16, 32, bk, sk, 4, 3)
     return None
+
+
+# ----------------------------------------------------------------------------------------------
+# W8A8: the reference's M > 16 fallback (scaled_int8_quant + cutlass_scaled_mm)
+# ----------------------------------------------------------------------------------------------
+
+def quantize_tokens(x_bits: np.ndarray):
+    """Per-token symmetric int8 quantisation of bf16 bits [M, K] (vLLM scaled_int8_quant, symmetric,
+    patches.py:99): s_a = amax_k |x| * fl32(1/127) in fp32 (how `amax / 127.0` evaluates on the device;
+    vLLM's own kernel divides, at most one ulp apart), q = clamp(round_half_even(x / s_a), -128, 127)
+    with an IEEE fp32 division; a row of zeros gets s_a = 0 and q = 0.  Returns (q int8, s_a fp32)."""
+    xf = bf16_to_f32(np.ascontiguousarray(x_bits, dtype=np.uint16))
+    amax = np.abs(xf).max(axis=1).astype(np.float32)
+    r = np.float32(1.0) / np.float32(127.0)
+    s_a = (amax * r).astype(np.float32)
+    safe = np.where(s_a > 0, s_a, np.float32(1.0)).astype(np.float32)
+    q = np.rint(xf / safe[:, None])
+    q = np.where(s_a[:, None] > 0, q, np.float32(0.0))
+    return np.clip(q, -128, 127).astype(np.int8), s_a
+
+
+def w8a8_linear(x_bits: np.ndarray, w: np.ndarray, s_w: np.ndarray, out_f32: bool = False):
+    """y[m, n] = ((fp32(sum_k q[m,k] w[n,k]) * s_a[m]) * s_w[n]) in fp32, rounded to bf16 bits unless
+    out_f32: the reference's M > 16 arithmetic (scaled_int8_quant + cutlass_scaled_mm,
+    patches.py:99-100).  The integer sums are exact (fp64 sums of |terms| <= 2^14, far below 2^53) and
+    are rounded once to fp32."""
+    q, s_a = quantize_tokens(x_bits)
+    acc = (q.astype(np.float64) @ np.asarray(w, dtype=np.int8).astype(np.float64).T).astype(np.float32)
+    y = (acc * s_a[:, None]) * np.asarray(s_w, dtype=np.float32)[None, :]
+    return y if out_f32 else bf16_from_f64(y.astype(np.float64))
 
 
 # ----------------------------------------------------------------------------------------------

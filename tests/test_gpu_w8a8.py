@@ -124,3 +124,20 @@ def test_w8a8_128_row_groups_bitwise(nt, waves, depth):
             ref = P.w8a8_reference(x[:M], w.t(), s, None, torch.bfloat16)
             torch.cuda.synchronize()
             assert torch.equal(bits(y), bits(ref)), (nt, waves, depth, M, split)
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 1000, 2048), (100, 513, 1024), (300, 64, 5120), (1, 16, 64)])
+def test_w8a8_against_oracle(oracle, M, N, K):
+    """The quantiser and the GEMM bit for bit against the oracle's numpy restatement (oracle.w8a8_linear),
+    bf16 and fp32 outputs."""
+    from helpers import bf16_bits
+    inp = oracle.gen_inputs(M, N, K, seed=M + N)
+    x, w, s = dev_inputs(inp, DEV)
+    xq, s_a = qf.quantize_tokens_int8(x)
+    y = qf.w8a8_mm(x, qf.to_tiled(w), s, torch.bfloat16)
+    y32 = qf.w8a8_mm(x, qf.to_tiled(w), s, torch.float32)
+    torch.cuda.synchronize()
+    q_ref, s_ref = oracle.quantize_tokens(inp.x)
+    assert np.array_equal(xq.cpu().numpy(), q_ref) and np.array_equal(s_a.cpu().numpy(), s_ref)
+    assert np.array_equal(bf16_bits(y), oracle.w8a8_linear(inp.x, inp.w, inp.s))
+    assert np.array_equal(y32.cpu().numpy(), oracle.w8a8_linear(inp.x, inp.w, inp.s, out_f32=True))
