@@ -870,7 +870,34 @@ __global__ void __launch_bounds__(WN * kWave) w8a16_wide_kernel(const GemmArgs a
 // divided by a scalar on the device; vLLM's kernel divides, at most an ulp away) and
 // xq[m, k] = clamp(rint(x / s_a), -128, 127) with an IEEE division; a row of zeros gets s_a = 0 and
 // xq = 0.  Finite inputs.  One workgroup per row, 8 values a thread per 16-byte load (K % 64 == 0,
-// 16-byte-aligned rows: the GEMM's own contract).
+// 16-byte-aligned rows: the GEMM's own contract).  With NP > 0 each thread keeps its (at most NP) pieces
+// of the row in registers between the two passes, so the row is read once; NP == 0 reads it twice (any
+// K).  The per-value arithmetic is the same, so the results are too.
+__device__ __forceinline__ float quant_amax8(float amax, const u32x4_t v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    amax = fmaxf(amax, fabsf(__uint_as_float(v[i] << 16)));
+    amax = fmaxf(amax, fabsf(__uint_as_float(v[i] & 0xffff0000u)));
+  }
+  return amax;
+}
+
+__device__ __forceinline__ u32x2_t quant_pack8(const u32x4_t v, float s) {
+  uint32_t b[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float f = __uint_as_float((i & 1) ? (v[i >> 1] & 0xffff0000u) : (v[i >> 1] << 16));
+    float t = s > 0.f ? rintf(__fdiv_rn(f, s)) : 0.f;
+    t = fminf(fmaxf(t, -128.f), 127.f);
+    b[i] = (uint32_t)(int)t & 0xffu;
+  }
+  u32x2_t o;
+  o.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+  o.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+  return o;
+}
+
+template <int NP>
 __global__ void __launch_bounds__(256) quantize_tokens_kernel(const uint16_t* x, int64_t ldx, int K, int8_t* xq,
                                                               int64_t ldq, float* s_a) {
   __shared__ float red[256 / kWave];
@@ -878,13 +905,16 @@ __global__ void __launch_bounds__(256) quantize_tokens_kernel(const uint16_t* x,
   const u32x4_t* row = reinterpret_cast<const u32x4_t*>(x + m * ldx);
   const int pieces = K / 8;
   float amax = 0.f;
-  for (int c = threadIdx.x; c < pieces; c += 256) {
-    const u32x4_t v = row[c];
+  u32x4_t keep[NP > 0 ? NP : 1];
+  if constexpr (NP > 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      amax = fmaxf(amax, fabsf(__uint_as_float(v[i] << 16)));
-      amax = fmaxf(amax, fabsf(__uint_as_float(v[i] & 0xffff0000u)));
+    for (int i = 0; i < NP; ++i) {
+      const int c = (int)threadIdx.x + i * 256;
+      keep[i] = c < pieces ? row[c] : (u32x4_t){0u, 0u, 0u, 0u};
+      amax = quant_amax8(amax, keep[i]);
     }
+  } else {
+    for (int c = threadIdx.x; c < pieces; c += 256) amax = quant_amax8(amax, row[c]);
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
@@ -897,20 +927,14 @@ __global__ void __launch_bounds__(256) quantize_tokens_kernel(const uint16_t* x,
   const float s = amax * inv127;
   if (threadIdx.x == 0) s_a[m] = s;
   u32x2_t* qrow = reinterpret_cast<u32x2_t*>(xq + m * ldq);
-  for (int c = threadIdx.x; c < pieces; c += 256) {
-    const u32x4_t v = row[c];
-    uint32_t b[8];
+  if constexpr (NP > 0) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float f = __uint_as_float((i & 1) ? (v[i >> 1] & 0xffff0000u) : (v[i >> 1] << 16));
-      float t = s > 0.f ? rintf(__fdiv_rn(f, s)) : 0.f;
-      t = fminf(fmaxf(t, -128.f), 127.f);
-      b[i] = (uint32_t)(int)t & 0xffu;
+    for (int i = 0; i < NP; ++i) {
+      const int c = (int)threadIdx.x + i * 256;
+      if (c < pieces) qrow[c] = quant_pack8(keep[i], s);
     }
-    u32x2_t o;
-    o.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-    o.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
-    qrow[c] = o;
+  } else {
+    for (int c = threadIdx.x; c < pieces; c += 256) qrow[c] = quant_pack8(row[c], s);
   }
 }
 
@@ -2415,8 +2439,14 @@ int qf_quantize_tokens_int8(const uint16_t* x, int64_t ldx, int M, int K, int8_t
                             void* stream) {
   if (x == nullptr || xq == nullptr || s_a == nullptr || M < 1 || K < 1 || ldx < K || ldq < K) return QF_ERR_INVALID_ARG;
   if (K % QF_W8A16_K_ALIGN || !aligned16(x) || ldx % 8 || (uintptr_t)xq % 8 || ldq % 8) return QF_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(quantize_tokens_kernel, dim3(M), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), x, ldx, K,
-                     xq, ldq, s_a);
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int per_thread = ceil_div(K / 8, 256);  // 16-byte pieces a thread
+  if (per_thread <= 4)
+    hipLaunchKernelGGL(quantize_tokens_kernel<4>, dim3(M), dim3(256), 0, st, x, ldx, K, xq, ldq, s_a);
+  else if (per_thread <= 12)
+    hipLaunchKernelGGL(quantize_tokens_kernel<12>, dim3(M), dim3(256), 0, st, x, ldx, K, xq, ldq, s_a);
+  else
+    hipLaunchKernelGGL(quantize_tokens_kernel<0>, dim3(M), dim3(256), 0, st, x, ldx, K, xq, ldq, s_a);
   return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
 }
 

@@ -141,3 +141,17 @@ def test_w8a8_against_oracle(oracle, M, N, K):
     assert np.array_equal(xq.cpu().numpy(), q_ref) and np.array_equal(s_a.cpu().numpy(), s_ref)
     assert np.array_equal(bf16_bits(y), oracle.w8a8_linear(inp.x, inp.w, inp.s))
     assert np.array_equal(y32.cpu().numpy(), oracle.w8a8_linear(inp.x, inp.w, inp.s, out_f32=True))
+
+
+@pytest.mark.parametrize("K", [64, 5120, 8192, 8256, 17408, 24576, 24640, 30720])
+def test_quantize_tokens_all_row_lengths(oracle, K):
+    """The three quantiser variants (row kept in registers up to 4 or 12 pieces a thread, read twice
+    beyond) against the oracle, at the row lengths on either side of each switch."""
+    M = 9
+    inp = oracle.gen_inputs(M, 16, K, seed=K)
+    x, _, _ = dev_inputs(inp, DEV)
+    xq, s_a = qf.quantize_tokens_int8(x)
+    torch.cuda.synchronize()
+    q_ref, s_ref = oracle.quantize_tokens(inp.x)
+    assert np.array_equal(s_a.cpu().numpy(), s_ref)
+    assert np.array_equal(xq.cpu().numpy(), q_ref)
