@@ -1037,6 +1037,11 @@ __global__ void __launch_bounds__(WN * kWave) w8a8_wide_kernel(const GemmArgs a)
     if (c + 1 < nchunks) load_chunk(c + 1);
     __builtin_amdgcn_sched_barrier(0);
     const uint8_t* slot = smem + (c & 1) * slot_bytes;
+    // x fragments of a step are read from LDS one step ahead, inside the chunk (its slot stays valid
+    // until the next barrier), so their latency overlaps the previous step's MFMAs.
+    i32x4_t xb[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) xb[mt] = *reinterpret_cast<const i32x4_t*>(slot + xoff[mt]);
 #pragma unroll
     for (int d = 0; d < RING; ++d) {
       const int s = c * RING + d;
@@ -1044,10 +1049,12 @@ __global__ void __launch_bounds__(WN * kWave) w8a8_wide_kernel(const GemmArgs a)
 #pragma unroll
       for (int t = 0; t < NT; ++t) buf[(d + DEPTH) % RING][t] = load16<true>(wp[t] + (int64_t)sn * step_bytes);
       __builtin_amdgcn_sched_barrier(0);  // keep the prefetch issue ahead of this step's math
-      if (s < nsteps) {                   // uniform
-        i32x4_t xb[MT];
+      i32x4_t xn[MT];
+      if (d + 1 < RING) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) xb[mt] = *reinterpret_cast<const i32x4_t*>(slot + xoff[mt] + d * 64);
+        for (int mt = 0; mt < MT; ++mt) xn[mt] = *reinterpret_cast<const i32x4_t*>(slot + xoff[mt] + (d + 1) * 64);
+      }
+      if (s < nsteps) {  // uniform
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           const i32x4_t wv = __builtin_bit_cast(i32x4_t, buf[d][t]);
@@ -1055,6 +1062,10 @@ __global__ void __launch_bounds__(WN * kWave) w8a8_wide_kernel(const GemmArgs a)
           for (int mt = 0; mt < MT; ++mt)
             acc[t][mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wv, xb[mt], acc[t][mt], 0, 0, 0);
         }
+      }
+      if (d + 1 < RING) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) xb[mt] = xn[mt];
       }
     }
   }
