@@ -374,8 +374,9 @@ def patch_int8_linear(kernel_cls=None, tiled: Optional[bool] = None) -> bool:
     """Install the W8A16 decode path on ``kernel_cls`` (default: vLLM's int8 scaled-mm kernel
     classes).  Idempotent (patches.py:80-82).  Returns False when no class could be patched.
     With ``tiled`` (default: QWEN_FAST_LINEAR_LAYOUT=tiled) the weights are also repacked into the
-    TILED image after loading; M > 16 calls on such layers run the wide-M W8A16 kernel up to
-    TILED_WIDE_MAX_M rows, and a bf16 library GEMM over exactly widened weights above."""
+    TILED image after loading; M > 16 calls on such layers run the reference's W8A8 arithmetic on the
+    int8 MFMA (w8a8_mm), or with QWEN_FAST_LINEAR_PREFILL=w8a16 the wide-M W8A16 kernel up to
+    TILED_WIDE_MAX_M rows and a bf16 library GEMM over exactly widened weights above."""
     tiled = tiled_layout_requested() if tiled is None else bool(tiled)
     classes = [kernel_cls] if kernel_cls is not None else []
     if kernel_cls is None:
