@@ -472,11 +472,32 @@ def run_prefill(torch, qf, dev, args):
                    "us_w8a16_wide_kernel": round(t["wide"], 1), "us_w8a16_widened_gemm": round(t["widened"], 1)}
         log(f"  prefill gate_up M={M:5d}: w8a8 {us:8.1f} us {tflops:7.1f} TOPS | w8a16: wide kernel {t['wide']:.1f} us, "
             f"widened + library GEMM {t['widened']:.1f} us")
+    # Roofline of the dominant kernel at M = 2048: the W8A8 GEMM alone (activations quantised beforehand),
+    # HIP events around graph replays on the stream it is launched on.  MFMA-bound: 2MNK int8 ops.
+    import ctypes
+    from qwen_fastpath import _lib as QL
+    M = 2048
+    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    xq, s_a = qf.quantize_tokens_int8(x)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    lib = QL.load()
+    cfg = QL.w8a8_pick_config(M, N, K)
+    assert int(lib.qf_w8a8_workspace_bytes(M, N, K, qf.TILED, ctypes.byref(cfg))) == 0
+    def gemm(i):
+        QL.check(lib.qf_w8a8_gemm(xq.data_ptr(), K, s_a.data_ptr(), sets[i][0].data_ptr(), 0, qf.TILED,
+                                  sets[i][1].data_ptr(), y.data_ptr(), N, QL.DTYPE_BF16, M, N, K, ctypes.byref(cfg),
+                                  None, 0, torch.cuda.current_stream().cuda_stream), "qf_w8a8_gemm")
+    us_k = min(time_graph(torch, lambda: [gemm(i) for _ in range(2) for i in range(2)], 4, reps=5) for _ in range(2))
+    tops_k = 2.0 * M * N * K / us_k / 1e6
+    log(f"  prefill gate_up M= 2048 W8A8 GEMM alone: {us_k:.1f} us {tops_k:.1f} TOPS ({100 * tops_k / 5000:.1f}% of 5 POP/s)")
+    roofline = {"bound": "mfma", "achieved": round(tops_k, 1), "peak": 5000.0, "unit": "TOPS",
+                "frac": round(tops_k / 5000.0, 4), "traffic": None,
+                "kernel": f"w8a8_wide_kernel gate_up M=2048 N={N} K={K} (int8 MFMA, cfg {cfg.to_tuple()})"}
     line = {"metric": METRIC, "value": rows[2048]["TOPS"], "unit": "TOPS", "n_gpus": 1, "steps": 4, "warmup": 1,
             "ms_per_step": round(rows[2048]["us"] / 1e3, 4), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "int8", "data": "synthetic (seeded int8 weights, fp32 scales, bf16 activations)",
             "config": {"workload": "gate_up 34816x5120 prefill widths on TILED weights, W8A8 (value = M=2048 TOPS)"},
-            "per_m": rows}
+            "per_m": rows, "roofline": roofline}
     if not args.no_cpu:
         line["cpu_baseline"] = prefill_cpu_baseline()
     print(json.dumps(line), flush=True)
