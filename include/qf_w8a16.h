@@ -24,6 +24,7 @@
  *   qf_w8a16_gemm_argmax     <- draft logits + pad mask + argmax in one launch   patches.py:160-166,178-185
  *   qf_quantize_tokens_int8  <- ops.scaled_int8_quant (dynamic, symmetric)   plugin/qwen_fastpath/patches.py:99
  *   qf_w8a8_gemm             <- ops.cutlass_scaled_mm on the int8 weights      plugin/qwen_fastpath/patches.py:100
+ *   qf_w8a8_pick_config / qf_w8a8_workspace_bytes: its configuration and workspace (host only)
  *   qf_w8a16_repack / qf_w8a16_unpack: load-time weight layout change (no reference counterpart;
  *                              the reference streams the checkpoint layout as is, w8a16.py:1-7)
  */

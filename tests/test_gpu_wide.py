@@ -108,9 +108,10 @@ def test_wide_layer_shapes_bitwise(name, N, K):
 
 
 def test_wide_and_widened_paths_in_a_graph():
-    """The wide-M kernel with a K split (workspace + second-pass sum), without one, and the widened-weights
-    path (widening, library GEMM, scale/cast) captured in one graph: four replays with eager work and
-    zeroed outputs between them, each bitwise equal to the eager results."""
+    """The wide-M kernel with a K split (workspace + second-pass sum), without one, the widened-weights
+    path (widening, library GEMM, scale/cast) and the W8A8 route (quantiser + int8 GEMM, with and
+    without a K split) captured in one graph: four replays with eager work and zeroed outputs between
+    them, each bitwise equal to the eager results."""
     cases = []
     for (M, N, K, seed) in ((40, 1000, 2048, 1), (300, 2000, 1024, 2)):
         wt, s, g = random_layer(N, K, seed)
@@ -119,10 +120,14 @@ def test_wide_and_widened_paths_in_a_graph():
     assert qf.resolve_config(40, 1000, 2048, qf.TILED).split_k > 1
     assert qf.resolve_config(300, 2000, 1024, qf.TILED).split_k == 1
 
+    from qwen_fastpath import _lib as L
+    assert L.w8a8_pick_config(40, 1000, 2048).split_k > 1
+
     def work():
         outs = [qf.w8a16_mm(x, wt, s, None, torch.bfloat16, qf.TILED) for (x, wt, s) in cases]
         x, wt, s = cases[1]
         outs.append(qf.w8a16_mm_prefill(x, wt, s, torch.bfloat16, qf.TILED, chunk_rows=768))
+        outs += [qf.w8a8_mm(x, wt, s, torch.bfloat16) for (x, wt, s) in cases]  # quantiser + int8 GEMM
         return outs
 
     eager = [o.clone() for o in work()]
