@@ -178,9 +178,9 @@ int qf_w8a16_dequant_bf16(const int8_t* w, int64_t ldw, int layout, int N, int K
 int qf_scale_cast_bf16(const float* acc, int64_t lda, const float* scale, int M, int N,
                        uint16_t* y, int64_t ldy, void* stream);
 
-/* ---- W8A8 path for M > 16 on TILED weights: the reference's fallback arithmetic (dynamic per-token int8
- * activations, int8 weights, exact integer sums, fp32 scales), plugin/qwen_fastpath/patches.py:99-100,
- * on weights kept in the TILED image, which CUTLASS cannot read. ---- */
+/* ---- W8A8 path for M > 16: the reference's fallback arithmetic (dynamic per-token int8 activations, int8
+ * weights, exact integer sums, fp32 scales), plugin/qwen_fastpath/patches.py:99-100, on MI355X's int8
+ * MFMA, for weights in either layout (CUTLASS cannot read the TILED image). ---- */
 
 /* Per-token symmetric int8 quantisation of bf16 x [M, K] (row stride ldx elements):
  *   s_a[m] = max_k |x[m,k]| * fl(1/127)          (fp32; 0 for a row of zeros)
@@ -193,8 +193,9 @@ int qf_quantize_tokens_int8(const uint16_t* x, int64_t ldx, int M, int K, int8_t
                             void* stream);
 
 /* y[m, n] = out_dtype( (float(sum_k xq[m,k] * w[n,k]) * s_a[m]) * scale[n] ), the integer sums exact in
- * int32 (K < 132000).  w is the TILED image (layout must be QF_LAYOUT_TILED, else QF_ERR_UNSUPPORTED; ldw is
- * ignored); xq / s_a as written by qf_quantize_tokens_int8 (xq 16-byte aligned, ldq % 16 == 0); any M >= 1.
+ * int32 (K < 132000).  w is the TILED image (ldw ignored) or row-major int8 [N, K] with row stride ldw >= K
+ * bytes, ldw % 16 == 0 (the row-major layout runs the automatic shape only: 2 tiles, 8 waves, depth 4);
+ * xq / s_a as written by qf_quantize_tokens_int8 (xq 16-byte aligned, ldq % 16 == 0); any M >= 1.
  * cfg may be NULL (automatic); its kernel must be QF_KERNEL_MFMA_W8A8 or AUTO.  Workspace
  * (qf_w8a8_workspace_bytes, 0 without a K split): the int32 split partials after the counter prefix, which
  * this path does not use; calls that may run at the same time need distinct workspaces.

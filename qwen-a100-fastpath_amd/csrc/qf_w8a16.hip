@@ -946,7 +946,9 @@ typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
 // of token row r at the same k, so there is no conversion work.  The x ring rows (CP 16-byte pieces of
 // 16 activations) are padded by 16 bytes: the 16 rows of a fragment read then sit on distinct 16-byte
 // bank groups.  Sums are exact in int32 (|sum| <= K * 128 * 127 < 2^31 for K < 132000).
-template <int NT, int MT, int WN, int DEPTH>
+// On row-major weights lane (g, r) loads the same 16 bytes from row r of the tile directly (a 64-byte
+// piece of each of 16 rows per k-step, as the decode kernel's row-major path reads them).
+template <int LAYOUT, int NT, int MT, int WN, int DEPTH>
 __global__ void __launch_bounds__(WN * kWave) w8a8_wide_kernel(const GemmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int THREADS = WN * kWave;
@@ -954,7 +956,7 @@ __global__ void __launch_bounds__(WN * kWave) w8a8_wide_kernel(const GemmArgs a)
   constexpr int CP = RING * 4;                               // 16-byte pieces per token row of a chunk
   constexpr int XP = (MT * 16 * CP + THREADS - 1) / THREADS;  // pieces per thread, at most
   constexpr int ROW = (CP + 1) * 16;
-  constexpr int64_t step_bytes = kTileN * kStepK;
+  constexpr int64_t step_bytes = LAYOUT == QF_LAYOUT_ROWMAJOR ? kStepK : kTileN * kStepK;
   const int lane = threadIdx.x & (kWave - 1);
   const int wn = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int g = lane >> 4;
@@ -985,7 +987,12 @@ __global__ void __launch_bounds__(WN * kWave) w8a8_wide_kernel(const GemmArgs a)
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int tile = min(tile0 + t, ntiles - 1);
-    wp[t] = a.w + (((int64_t)tile * a.ksteps + s_begin) * kWave + lane) * 16;
+    if constexpr (LAYOUT == QF_LAYOUT_ROWMAJOR) {
+      const int row = min(tile * kTileN + (lane & 15), a.N - 1);
+      wp[t] = a.w + (int64_t)row * a.ldw + (int64_t)s_begin * kStepK + g * 16;
+    } else {
+      wp[t] = a.w + (((int64_t)tile * a.ksteps + s_begin) * kWave + lane) * 16;
+    }
   }
 
   u32x4_t buf[RING][NT];
@@ -2168,11 +2175,27 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
 // Instantiations: NT {2, 4} x MT {1..4} x WN {4, 8} x DEPTH {2, 4}, and MT {5..8} for NT 2.
 template <int NT, int MT>
 KernelFn w8a8_by_shape(int wn, int depth) {
-  if (wn == 4 && depth == 2) return &w8a8_wide_kernel<NT, MT, 4, 2>;
-  if (wn == 4 && depth == 4) return &w8a8_wide_kernel<NT, MT, 4, 4>;
-  if (wn == 8 && depth == 2) return &w8a8_wide_kernel<NT, MT, 8, 2>;
-  if (wn == 8 && depth == 4) return &w8a8_wide_kernel<NT, MT, 8, 4>;
+  if (wn == 4 && depth == 2) return &w8a8_wide_kernel<QF_LAYOUT_TILED, NT, MT, 4, 2>;
+  if (wn == 4 && depth == 4) return &w8a8_wide_kernel<QF_LAYOUT_TILED, NT, MT, 4, 4>;
+  if (wn == 8 && depth == 2) return &w8a8_wide_kernel<QF_LAYOUT_TILED, NT, MT, 8, 2>;
+  if (wn == 8 && depth == 4) return &w8a8_wide_kernel<QF_LAYOUT_TILED, NT, MT, 8, 4>;
   return nullptr;
+}
+
+// Row-major weights: the automatic shape only (2 tiles, 8 wavefronts, DEPTH 4), MT {1..8}.
+KernelFn w8a8_rowmajor(int nt, int mt, int waves, int depth) {
+  if (nt != 2 || waves != 8 || depth != 4) return nullptr;
+  switch (mt) {
+    case 1: return &w8a8_wide_kernel<QF_LAYOUT_ROWMAJOR, 2, 1, 8, 4>;
+    case 2: return &w8a8_wide_kernel<QF_LAYOUT_ROWMAJOR, 2, 2, 8, 4>;
+    case 3: return &w8a8_wide_kernel<QF_LAYOUT_ROWMAJOR, 2, 3, 8, 4>;
+    case 4: return &w8a8_wide_kernel<QF_LAYOUT_ROWMAJOR, 2, 4, 8, 4>;
+    case 5: return &w8a8_wide_kernel<QF_LAYOUT_ROWMAJOR, 2, 5, 8, 4>;
+    case 6: return &w8a8_wide_kernel<QF_LAYOUT_ROWMAJOR, 2, 6, 8, 4>;
+    case 7: return &w8a8_wide_kernel<QF_LAYOUT_ROWMAJOR, 2, 7, 8, 4>;
+    case 8: return &w8a8_wide_kernel<QF_LAYOUT_ROWMAJOR, 2, 8, 8, 4>;
+    default: return nullptr;
+  }
 }
 
 template <int NT>
@@ -2196,7 +2219,8 @@ KernelFn w8a8_by_mt(int mt, int wn, int depth) {
   return nullptr;
 }
 
-KernelFn select_w8a8(int nt, int mt, int waves, int depth) {
+KernelFn select_w8a8(int layout, int nt, int mt, int waves, int depth) {
+  if (layout == QF_LAYOUT_ROWMAJOR) return w8a8_rowmajor(nt, mt, waves, depth);
   if (nt == 2) return w8a8_by_mt<2>(mt, waves, depth);
   if (nt == 4) return w8a8_by_mt<4>(mt, waves, depth);
   return nullptr;
@@ -2227,21 +2251,23 @@ int validate_w8a8(int M, int N, int K, int layout, const qf_w8a16_config& c) {
   if (c.kernel != QF_KERNEL_MFMA_W8A8) return QF_ERR_INVALID_ARG;
   if (c.split_k < 1 || c.split_k > ksteps || c.waves < 1 || c.k_waves < 1 || c.tiles_per_wave < 1)
     return QF_ERR_INVALID_ARG;
-  if (layout != QF_LAYOUT_TILED || c.k_waves != 1 || K >= 132000) return QF_ERR_UNSUPPORTED;
+  if ((layout != QF_LAYOUT_TILED && layout != QF_LAYOUT_ROWMAJOR) || c.k_waves != 1 || K >= 132000)
+    return QF_ERR_UNSUPPORTED;
   int groups, rows;
   w8a8_groups(c, M, N, groups, rows);
   if ((int64_t)workgroups(c, N) * groups * c.split_k > 0x7fffffff) return QF_ERR_UNSUPPORTED;
-  if (select_w8a8(c.tiles_per_wave, rows / 16, c.waves, c.depth) == nullptr) return QF_ERR_UNSUPPORTED;
+  if (select_w8a8(layout, c.tiles_per_wave, rows / 16, c.waves, c.depth) == nullptr) return QF_ERR_UNSUPPORTED;
   return w8a8_lds_bytes(c, M, N) > kMaxLds ? QF_ERR_UNSUPPORTED : QF_OK;
 }
 
-// Automatic W8A8 configuration (TILED weights, any M): 8 wavefronts of 2 tiles, 4 steps in flight, and
+// Automatic W8A8 configuration (either layout, any M): 8 wavefronts of 2 tiles, 4 steps in flight, and
 // K split across workgroups until they number 128 (at most 8 ways and 16 steps a split).  Measured on
 // the dense 27B-class layer at M = 64 .. 2048 against 4-tile and 4-wavefront shapes at depth 2 and 4:
 // within 9% of the best shape everywhere (gate_up M = 2048: 565 us against 533 for 4 tiles, 677 for
 // 4 wavefronts of 4 tiles).
 bool auto_config_w8a8(int M, int N, int K, int layout, qf_w8a16_config* c) {
-  if (M < 1 || N < 1 || K < QF_W8A16_K_ALIGN || K % QF_W8A16_K_ALIGN || layout != QF_LAYOUT_TILED) return false;
+  if (M < 1 || N < 1 || K < QF_W8A16_K_ALIGN || K % QF_W8A16_K_ALIGN) return false;
+  if (layout != QF_LAYOUT_TILED && layout != QF_LAYOUT_ROWMAJOR) return false;
   *c = qf_w8a16_config{};
   c->kernel = QF_KERNEL_MFMA_W8A8;
   c->k_waves = 1;
@@ -2274,14 +2300,15 @@ int resolve_w8a8(int M, int N, int K, int layout, const qf_w8a16_config* in, qf_
   return QF_OK;
 }
 
-int run_w8a8(const int8_t* xq, int64_t ldq, const float* s_a, const int8_t* w, int layout, const float* scale,
-             void* y, int64_t ldy, int out_dtype, int M, int N, int K, const qf_w8a16_config* cfg, void* workspace,
-             size_t workspace_bytes, void* stream) {
+int run_w8a8(const int8_t* xq, int64_t ldq, const float* s_a, const int8_t* w, int64_t ldw, int layout,
+             const float* scale, void* y, int64_t ldy, int out_dtype, int M, int N, int K, const qf_w8a16_config* cfg,
+             void* workspace, size_t workspace_bytes, void* stream) {
   if (xq == nullptr || s_a == nullptr || w == nullptr || scale == nullptr || y == nullptr) return QF_ERR_INVALID_ARG;
   if (M < 1 || N < 1 || K < 1 || ldq < K || ldy < N) return QF_ERR_INVALID_ARG;
   if (layout != QF_LAYOUT_ROWMAJOR && layout != QF_LAYOUT_TILED) return QF_ERR_INVALID_ARG;
   if (out_dtype != QF_DTYPE_BF16 && out_dtype != QF_DTYPE_F32) return QF_ERR_INVALID_ARG;
-  if (layout != QF_LAYOUT_TILED || K % QF_W8A16_K_ALIGN) return QF_ERR_UNSUPPORTED;
+  if (layout == QF_LAYOUT_ROWMAJOR && ldw < K) return QF_ERR_INVALID_ARG;
+  if (K % QF_W8A16_K_ALIGN || (layout == QF_LAYOUT_ROWMAJOR && ldw % 16)) return QF_ERR_UNSUPPORTED;
   if (!aligned16(xq) || !aligned16(w) || !aligned16(scale) || !aligned16(y) || ldq % 16) return QF_ERR_UNSUPPORTED;
   qf_w8a16_config c;
   const int rc = resolve_w8a8(M, N, K, layout, cfg, &c);
@@ -2298,6 +2325,7 @@ int run_w8a8(const int8_t* xq, int64_t ldq, const float* s_a, const int8_t* w, i
   a.partial = need > 0 ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + QF_W8A16_COUNTER_BYTES)
                        : nullptr;
   a.ldx = ldq;
+  a.ldw = ldw;
   a.ldy = ldy;
   a.M = M;
   a.N = N;
@@ -2308,7 +2336,7 @@ int run_w8a8(const int8_t* xq, int64_t ldq, const float* s_a, const int8_t* w, i
   a.out_f32 = out_dtype == QF_DTYPE_F32;
   a.vec_out = (ldy % 4) == 0;
   w8a8_groups(c, M, N, a.groups, a.group_rows);
-  KernelFn fn = select_w8a8(c.tiles_per_wave, a.group_rows / 16, c.waves, c.depth);
+  KernelFn fn = select_w8a8(layout, c.tiles_per_wave, a.group_rows / 16, c.waves, c.depth);
   if (fn == nullptr) return QF_ERR_UNSUPPORTED;
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   int st = launch(fn, dim3(workgroups(c, N) * a.groups * c.split_k), dim3(c.waves * kWave), w8a8_lds_bytes(c, M, N),
@@ -2475,8 +2503,7 @@ size_t qf_w8a8_workspace_bytes(int M, int N, int K, int layout, const qf_w8a16_c
 int qf_w8a8_gemm(const int8_t* xq, int64_t ldq, const float* s_a, const int8_t* w, int64_t ldw, int layout,
                  const float* scale, void* y, int64_t ldy, int out_dtype, int M, int N, int K,
                  const qf_w8a16_config* cfg, void* workspace, size_t workspace_bytes, void* stream) {
-  (void)ldw;  // the TILED image has no row stride
-  return run_w8a8(xq, ldq, s_a, w, layout, scale, y, ldy, out_dtype, M, N, K, cfg, workspace, workspace_bytes,
+  return run_w8a8(xq, ldq, s_a, w, ldw, layout, scale, y, ldy, out_dtype, M, N, K, cfg, workspace, workspace_bytes,
                   stream);
 }
 

@@ -243,8 +243,22 @@ def _fallback(x2, w_q, w_s, bias, out_dtype, layout):
         return y if bias is None else y + bias
     global _fallback_impl
     if _fallback_impl is None:
-        _fallback_impl = _vllm_w8a8() or w8a8_reference
+        _fallback_impl = _vllm_w8a8() or _w8a8_hip
     return _fallback_impl(x2, w_q, w_s, bias, out_dtype)
+
+
+def _w8a8_hip(x2, w_q, w_s, bias, out_dtype):
+    """Without vLLM: the same W8A8 arithmetic on the int8 MFMA (w8a8_mm on the row-major weight) when the
+    library serves the shape -- K % 64 == 0, the [K, N] stride-(1, K) view, bf16 activations -- and the
+    torch restatement otherwise, as the reference falls back when pick_config returns None."""
+    M, K = x2.shape
+    N = w_s.numel()
+    if (x2.dtype == torch.bfloat16 and out_dtype in (torch.bfloat16, torch.float32) and w_q.dim() == 2
+            and w_q.shape == (K, N) and w_q.stride(0) == 1 and w_q.stride(1) % 16 == 0
+            and w_s.dtype == torch.float32 and pick_config(N, K, ROWMAJOR) is not None):
+        y = w8a8_mm(x2, w_q, w_s.reshape(-1), out_dtype, layout=ROWMAJOR)
+        return y if bias is None else y + bias
+    return w8a8_reference(x2, w_q, w_s, bias, out_dtype)
 
 
 # ------------------------------------------------------------------------------------------------

@@ -313,15 +313,15 @@ def quantize_tokens_int8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 def w8a8_mm(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, out_dtype: torch.dtype, cfg=None,
             layout: int = TILED) -> torch.Tensor:
     """y = ((xq @ W^T) * s_a) * w_scale with per-token int8 activations (quantize_tokens_int8), exact
-    int32 sums on the int8 MFMA, on weights in the TILED image: the arithmetic of the reference's
-    M > 16 fallback, scaled_int8_quant + cutlass_scaled_mm (plugin/qwen_fastpath/patches.py:99-100),
-    for a layer whose weights CUTLASS cannot read.  Any M."""
+    int32 sums on the int8 MFMA: the arithmetic of the reference's M > 16 fallback, scaled_int8_quant +
+    cutlass_scaled_mm (plugin/qwen_fastpath/patches.py:99-100).  w is the TILED image or the [K, N]
+    stride-(1, K) view of the checkpoint's row-major weight (layout=ROWMAJOR).  Any M."""
     lib = L.load()
     if w_scale.dtype != torch.float32:
         raise TypeError(f"w_scale must be fp32, got {w_scale.dtype}")
     M, K = x.shape
     N = w_scale.numel()
-    _weight_geometry(w, N, K, layout)
+    ldw = _weight_geometry(w, N, K, layout)
     xq, s_a = quantize_tokens_int8(x)
     s = w_scale.reshape(-1)
     if not s.is_contiguous() or s.data_ptr() % 16:
@@ -337,7 +337,7 @@ def w8a8_mm(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, out_dtype: 
     ws_bytes = int(lib.qf_w8a8_workspace_bytes(M, N, K, layout, ctypes.byref(c)))
     ws = _workspace(x.device, ws_bytes) if ws_bytes else None
     stream = torch.cuda.current_stream(x.device).cuda_stream
-    rc = lib.qf_w8a8_gemm(xq.data_ptr(), K, s_a.data_ptr(), w.data_ptr(), 0, layout, s.data_ptr(), y.data_ptr(), N,
+    rc = lib.qf_w8a8_gemm(xq.data_ptr(), K, s_a.data_ptr(), w.data_ptr(), ldw, layout, s.data_ptr(), y.data_ptr(), N,
                           dt, M, N, K, ctypes.byref(c), ws.data_ptr() if ws is not None else None,
                           ws.numel() if ws is not None else 0, stream)
     L.check(rc, f"qf_w8a8_gemm(M={M}, N={N}, K={K}, layout={layout})")

@@ -253,18 +253,23 @@ def test_prefill_arithmetic_switch(monkeypatch):
 
 
 def test_w8a8_configs_host_only():
-    """qf_w8a8_gemm: TILED weights only, its own kernel kind, any M; refused before any launch otherwise."""
+    """qf_w8a8_gemm: either layout (row-major: the automatic shape only), its own kernel kind, any M;
+    refused before any launch otherwise."""
     lib = L.load()
     for M in (1, 17, 64, 300, 2048):
         for (N, K) in ((34816, 5120), (5120, 17408), (1000, 1024), (16, 64)):
             c = L.w8a8_pick_config(M, N, K)
             assert c is not None and c.kernel == L.KERNEL_MFMA_W8A8 and c.k_waves == 1, (M, N, K)
-            assert L.w8a8_pick_config(M, N, K, 0) is None  # row-major weights
+            cr = L.w8a8_pick_config(M, N, K, 0)  # row-major weights: the automatic shape
+            assert cr is not None and cr.to_tuple()[2:5] == (2, 8, 4), (M, N, K)
     fake = 1 << 20
     def call(layout=1, cfg=None, M=40, K=1024, ldq=1024):
         return lib.qf_w8a8_gemm(fake, ldq, fake, fake, 0, layout, fake, fake, 1000, 0, M, 1000, K,
                                 ctypes.byref(cfg) if cfg is not None else None, None, 0, None)
-    assert call(layout=0) == L.ERR_UNSUPPORTED
+    assert call(layout=0) == L.ERR_INVALID_ARG                               # row-major: ldw < K
+    assert lib.qf_w8a8_gemm(fake, 1024, fake, fake, 1032, 0, fake, fake, 1000, 0, 40, 1000, 1024, None, None, 0,
+                            None) == L.ERR_UNSUPPORTED                        # row-major: ldw % 16
+    assert call(layout=2) == L.ERR_INVALID_ARG
     assert call(K=1000, ldq=1000) == L.ERR_UNSUPPORTED                     # K % 64
     assert call(ldq=1024 + 8) == L.ERR_UNSUPPORTED                          # ldq % 16
     assert call(M=0) == L.ERR_INVALID_ARG

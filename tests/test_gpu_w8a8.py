@@ -155,3 +155,42 @@ def test_quantize_tokens_all_row_lengths(oracle, K):
     q_ref, s_ref = oracle.quantize_tokens(inp.x)
     assert np.array_equal(s_a.cpu().numpy(), s_ref)
     assert np.array_equal(xq.cpu().numpy(), q_ref)
+
+
+@pytest.mark.parametrize("name,N,K", [("small", 1000, 2048), ("o_proj", 5120, 8192), ("gate_up", 34816, 5120)])
+def test_w8a8_rowmajor_weights(oracle, name, N, K):
+    """Row-major weights (the checkpoint's [N, K], seen as the [K, N] stride-(1, K) view, and a strided copy
+    with rows 64 bytes apart more than K) give the TILED image's results bit for bit: each lane loads
+    the same 16 bytes either way."""
+    x, w, s = random_case(300, N, K, N + 3)
+    wt = qf.to_tiled(w.t())
+    wide = torch.zeros((N, K + 64), dtype=torch.int8, device=DEV)
+    wide[:, :K] = w
+    for M in (17, 64, 300):
+        y_t = qf.w8a8_mm(x[:M], wt, s, torch.bfloat16)
+        y_r = qf.w8a8_mm(x[:M], w.t(), s, torch.bfloat16, layout=qf.ROWMAJOR)
+        y_s = qf.w8a8_mm(x[:M], wide[:, :K].t(), s, torch.bfloat16, layout=qf.ROWMAJOR)
+        torch.cuda.synchronize()
+        assert torch.equal(bits(y_r), bits(y_t)) and torch.equal(bits(y_s), bits(y_t)), (name, M)
+    if name == "small":
+        inp = oracle.gen_inputs(40, N, K, seed=3)
+        xd, wd, sd = dev_inputs(inp, DEV)
+        from helpers import bf16_bits
+        assert np.array_equal(bf16_bits(qf.w8a8_mm(xd, wd, sd, torch.bfloat16, layout=qf.ROWMAJOR)),
+                              oracle.w8a8_linear(inp.x, inp.w, inp.s))
+
+
+def test_rowmajor_m17_dispatch_uses_the_int8_kernel(oracle, monkeypatch):
+    """Without vLLM, a row-major layer's M > 16 call runs the W8A8 arithmetic on the int8 MFMA: the
+    dispatcher op's output equals the oracle's W8A8 restatement bit for bit."""
+    P._fallback_impl = None
+    monkeypatch.setattr(P, "_vllm_w8a8", lambda: None)
+    try:
+        inp = oracle.gen_inputs(17, 5120, 6144, seed=4)
+        x, w, s = dev_inputs(inp, DEV)
+        y = torch.ops.qwen_fastpath.qf_int8_linear(x, w, s, None)
+        torch.cuda.synchronize()
+        from helpers import bf16_bits
+        assert np.array_equal(bf16_bits(y), oracle.w8a8_linear(inp.x, inp.w, inp.s))
+    finally:
+        P._fallback_impl = None
