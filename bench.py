@@ -20,7 +20,8 @@ step, the layer output re-normalised to unit RMS as the next layer's input); --w
 --workload lm_head (int8 draft head 151936x5120 + pad-masked argmax at M = 1, 4);
 --workload spec_attn (split-KV verification attention of one full-attention layer, H=24, H_kv=4,
 D=256, 800-position pages, at the reference's contexts and batch shapes);
---profile-gemm NAME --iters N (only that GEMM, for rocprofv3); --copy-probe (a plain device copy
+--profile-gemm NAME --iters N (only that GEMM, for rocprofv3); --profile-w8a8 M --iters N (only the
+W8A8 GEMM on gate_up at M rows, activations quantised beforehand); --copy-probe (a plain device copy
 of known size, for counter calibration).
 """
 from __future__ import annotations
@@ -49,6 +50,7 @@ GEMMS = {  # name: (N, K)
 DOMINANT = "gate_up"
 GRAPH_STEPS = 32  # decode steps captured per graph (a multiple of the rotated layer count)
 PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "w8a16_gate_up_m5_pmc.txt")
+W8A8_PROFILE = os.path.join(ROOT, "profiles", "w8a8_gate_up_m2048_pmc.txt")
 
 
 def algo_bytes(M: int, N: int, K: int) -> int:
@@ -162,6 +164,8 @@ def main():
     ap.add_argument("--layers", type=int, default=4, help="distinct layers rotated through (layer workload)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--profile-gemm", choices=list(GEMMS), default=None)
+    ap.add_argument("--profile-w8a8", type=int, default=None, metavar="M",
+                    help="only the W8A8 GEMM on gate_up at M rows, --iters launches (for rocprofv3)")
     ap.add_argument("--iters", type=int, default=200)
     ap.add_argument("--copy-probe", action="store_true")
     ap.add_argument("--read-probe", action="store_true", help="only the library's read probe over the dominant GEMM's bytes")
@@ -197,6 +201,18 @@ def main():
     if args.read_probe:
         ceiling = read_ceiling(torch, qf, dev, algo_bytes(M_TOKENS, *GEMMS[DOMINANT]))
         log(f"read probe: {ceiling:.0f} GB/s")
+        return
+
+    if args.profile_w8a8:
+        M = args.profile_w8a8
+        g = torch.Generator(device=dev)
+        g.manual_seed(13)
+        sets = prefill_weight_sets(torch, qf, dev, g)
+        gemm, cfg = w8a8_gate_up_gemm(torch, qf, dev, g, M, sets)
+        for i in range(args.iters):
+            gemm(i % 2)
+        torch.cuda.synchronize()
+        log(f"profile: {args.iters} launches of the W8A8 GEMM on gate_up M={M} cfg={cfg.to_tuple()}")
         return
 
     if args.profile_gemm:
@@ -437,6 +453,36 @@ def run_msweep(torch, qf, dev, args):
     print(json.dumps(line), flush=True)
 
 
+def w8a8_gate_up_gemm(torch, qf, dev, g, M, sets):
+    """The W8A8 GEMM alone on gate_up at M rows (activations quantised once, beforehand): returns a
+    callable that runs it on weight set i, and its configuration."""
+    import ctypes
+    from qwen_fastpath import _lib as QL
+    N, K = GEMMS["gate_up"]
+    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    xq, s_a = qf.quantize_tokens_int8(x)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    lib = QL.load()
+    cfg = QL.w8a8_pick_config(M, N, K)
+    assert int(lib.qf_w8a8_workspace_bytes(M, N, K, qf.TILED, ctypes.byref(cfg))) == 0
+
+    def gemm(i):
+        QL.check(lib.qf_w8a8_gemm(xq.data_ptr(), K, s_a.data_ptr(), sets[i][0].data_ptr(), 0, qf.TILED,
+                                  sets[i][1].data_ptr(), y.data_ptr(), N, QL.DTYPE_BF16, M, N, K, ctypes.byref(cfg),
+                                  None, 0, torch.cuda.current_stream().cuda_stream), "qf_w8a8_gemm")
+    return gemm, cfg
+
+
+def prefill_weight_sets(torch, qf, dev, g, count=2):
+    """gate_up int8 weights in the TILED layout with fp32 scales, `count` distinct sets."""
+    N, K = GEMMS["gate_up"]
+    sets = []
+    for _ in range(count):
+        w = qf.to_tiled(torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g).t())
+        sets.append((w, (torch.randn(N, device=dev, generator=g).abs() * 0.002 + 1e-4).float()))
+    return sets
+
+
 def run_prefill(torch, qf, dev, args):
     """gate_up (N=34816, K=5120) at prefill widths M = 64 ... 2048 on TILED weights, two weight sets
     rotated (356 MB, past the 256 MB last-level cache), three routes timed interleaved (best of 2
@@ -449,10 +495,7 @@ def run_prefill(torch, qf, dev, args):
     N, K = GEMMS["gate_up"]
     g = torch.Generator(device=dev)
     g.manual_seed(13)
-    sets = []
-    for _ in range(2):
-        w = qf.to_tiled(torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g).t())
-        sets.append((w, (torch.randn(N, device=dev, generator=g).abs() * 0.002 + 1e-4).float()))
+    sets = prefill_weight_sets(torch, qf, dev, g)
     rows = {}
     for M in (64, 256, 512, 1024, 2048):
         x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
@@ -474,24 +517,13 @@ def run_prefill(torch, qf, dev, args):
             f"widened + library GEMM {t['widened']:.1f} us")
     # Roofline of the dominant kernel at M = 2048: the W8A8 GEMM alone (activations quantised beforehand),
     # HIP events around graph replays on the stream it is launched on.  MFMA-bound: 2MNK int8 ops.
-    import ctypes
-    from qwen_fastpath import _lib as QL
     M = 2048
-    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
-    xq, s_a = qf.quantize_tokens_int8(x)
-    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-    lib = QL.load()
-    cfg = QL.w8a8_pick_config(M, N, K)
-    assert int(lib.qf_w8a8_workspace_bytes(M, N, K, qf.TILED, ctypes.byref(cfg))) == 0
-    def gemm(i):
-        QL.check(lib.qf_w8a8_gemm(xq.data_ptr(), K, s_a.data_ptr(), sets[i][0].data_ptr(), 0, qf.TILED,
-                                  sets[i][1].data_ptr(), y.data_ptr(), N, QL.DTYPE_BF16, M, N, K, ctypes.byref(cfg),
-                                  None, 0, torch.cuda.current_stream().cuda_stream), "qf_w8a8_gemm")
+    gemm, cfg = w8a8_gate_up_gemm(torch, qf, dev, g, M, sets)
     us_k = min(time_graph(torch, lambda: [gemm(i) for _ in range(2) for i in range(2)], 4, reps=5) for _ in range(2))
     tops_k = 2.0 * M * N * K / us_k / 1e6
     log(f"  prefill gate_up M= 2048 W8A8 GEMM alone: {us_k:.1f} us {tops_k:.1f} TOPS ({100 * tops_k / 5000:.1f}% of 5 POP/s)")
     roofline = {"bound": "mfma", "achieved": round(tops_k, 1), "peak": 5000.0, "unit": "TOPS",
-                "frac": round(tops_k / 5000.0, 4), "traffic": None,
+                "frac": round(tops_k / 5000.0, 4), "traffic": read_traffic(W8A8_PROFILE),
                 "kernel": f"w8a8_wide_kernel gate_up M=2048 N={N} K={K} (int8 MFMA, cfg {cfg.to_tuple()})"}
     line = {"metric": METRIC, "value": rows[2048]["TOPS"], "unit": "TOPS", "n_gpus": 1, "steps": 4, "warmup": 1,
             "ms_per_step": round(rows[2048]["us"] / 1e3, 4), "higher_is_better": True, "scaling": "weak",
