@@ -2261,7 +2261,8 @@ int validate_w8a8(int M, int N, int K, int layout, const qf_w8a16_config& c) {
 }
 
 // Automatic W8A8 configuration (either layout, any M): 8 wavefronts of 2 tiles, 4 steps in flight, and
-// K split across workgroups until they number 128 (at most 8 ways and 16 steps a split).  Measured on
+// K split across workgroups until they number 128 (at most 8 ways and 16 steps a split), with the two
+// exceptions below (a sweep of 9 shapes over the four layer shapes at M = 17 .. 2048).  Measured on
 // the dense 27B-class layer at M = 64 .. 2048 against 4-tile and 4-wavefront shapes at depth 2 and 4:
 // within 9% of the best shape everywhere (gate_up M = 2048: 565 us against 533 for 4 tiles, 677 for
 // 4 wavefronts of 4 tiles).
@@ -2281,7 +2282,24 @@ bool auto_config_w8a8(int M, int N, int K, int layout, qf_w8a16_config* c) {
   w8a8_groups(*c, M, N, groups, rows);
   const int64_t wgs = (int64_t)workgroups(*c, N) * groups;
   const int ksteps = K / kStepK;
+  if (layout == QF_LAYOUT_TILED && wgs < 128 && ksteps <= 128) {
+    // 4-wavefront workgroups, unsplit, where they number 128 .. 255 and the 8-wavefront ones would
+    // need a K split (qkv M = 128: 28.3 us against 32.4; o_proj M = 256: 37.2 against 38.7).
+    qf_w8a16_config c4 = *c;
+    c4.waves = 4;
+    int groups4, rows4;
+    w8a8_groups(c4, M, N, groups4, rows4);
+    const int64_t wgs4 = (int64_t)workgroups(c4, N) * groups4;
+    if (wgs4 >= 128 && wgs4 < 256) {
+      *c = c4;
+      return validate_w8a8(M, N, K, layout, *c) == QF_OK;
+    }
+  }
   while (wgs * c->split_k < 128 && c->split_k < 8 && ksteps / (c->split_k + 1) >= 16) ++c->split_k;
+  // 128-row workgroups run one per CU.  On a long K range, a grid whose last round leaves the 256 CUs at
+  // most a quarter busy is split in two (down M = 2048, 320 workgroups: 268 us against 290).
+  if (c->split_k == 1 && rows == 128 && ksteps >= 256 && wgs > 256 && wgs % 256 != 0 && wgs % 256 <= 64)
+    c->split_k = 2;
   return validate_w8a8(M, N, K, layout, *c) == QF_OK;
 }
 

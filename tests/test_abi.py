@@ -262,6 +262,15 @@ def test_w8a8_configs_host_only():
             assert c is not None and c.kernel == L.KERNEL_MFMA_W8A8 and c.k_waves == 1, (M, N, K)
             cr = L.w8a8_pick_config(M, N, K, 0)  # row-major weights: the automatic shape
             assert cr is not None and cr.to_tuple()[2:5] == (2, 8, 4), (M, N, K)
+    # The automatic rule's two exceptions: 4-wavefront workgroups, unsplit, where 8-wavefront ones
+    # would be under 128 (TILED only), and a split in two for a long K whose last round of 128-row
+    # workgroups would leave the CUs at most a quarter busy.
+    assert L.w8a8_pick_config(128, 10240, 5120).to_tuple()[1:5] == (1, 2, 4, 4)
+    assert L.w8a8_pick_config(128, 10240, 5120, 0).to_tuple()[1:5] == (2, 2, 8, 4)
+    assert L.w8a8_pick_config(256, 5120, 8192).to_tuple()[1:5] == (1, 2, 4, 4)
+    assert L.w8a8_pick_config(2048, 5120, 17408).to_tuple()[1:5] == (2, 2, 8, 4)
+    assert L.w8a8_pick_config(1024, 5120, 17408).to_tuple()[1:5] == (1, 2, 8, 4)
+    assert L.w8a8_pick_config(2048, 34816, 5120).to_tuple()[1:5] == (1, 2, 8, 4)
     fake = 1 << 20
     def call(layout=1, cfg=None, M=40, K=1024, ldq=1024):
         return lib.qf_w8a8_gemm(fake, ldq, fake, fake, 0, layout, fake, fake, 1000, 0, M, 1000, K,

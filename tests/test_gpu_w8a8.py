@@ -96,6 +96,20 @@ def test_w8a8_layer_shapes(name, N, K):
         assert torch.equal(bits(y), bits(ref)), (name, M)
 
 
+@pytest.mark.parametrize("name,M,N,K", [("qkv", 128, 10240, 5120), ("o_proj", 256, 5120, 8192),
+                                        ("down", 2048, 5120, 17408)])
+def test_w8a8_auto_exceptions(name, M, N, K):
+    """The automatic rule's exceptions (4-wavefront unsplit workgroups; a split in two on down at
+    M = 2048) against the restatement, on both layouts where they apply."""
+    x, w, s = random_case(M, N, K, M + N)
+    y = qf.w8a8_mm(x, qf.to_tiled(w.t()), s, torch.bfloat16)
+    ref = P.w8a8_reference(x, w.t(), s, None, torch.bfloat16)
+    y_r = qf.w8a8_mm(x, w.t(), s, torch.bfloat16, layout=qf.ROWMAJOR)
+    torch.cuda.synchronize()
+    print(f"{name} M={M} cfg={L.w8a8_pick_config(M, N, K).to_tuple()}", flush=True)
+    assert torch.equal(bits(y), bits(ref)) and torch.equal(bits(y_r), bits(ref)), name
+
+
 def test_w8a8_error_statistic(oracle):
     """Against the exact product, the W8A8 path's rel-L2 is the reference's published W8A8 statistic
     (0.0083-0.0094, data/measurements.json:420-427), as on its own fallback."""
