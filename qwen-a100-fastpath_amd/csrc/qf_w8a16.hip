@@ -2262,10 +2262,9 @@ int validate_w8a8(int M, int N, int K, int layout, const qf_w8a16_config& c) {
 
 // Automatic W8A8 configuration (either layout, any M): 8 wavefronts of 2 tiles, 4 steps in flight, and
 // K split across workgroups until they number 128 (at most 8 ways and 16 steps a split), with the two
-// exceptions below (a sweep of 9 shapes over the four layer shapes at M = 17 .. 2048).  Measured on
-// the dense 27B-class layer at M = 64 .. 2048 against 4-tile and 4-wavefront shapes at depth 2 and 4:
-// within 9% of the best shape everywhere (gate_up M = 2048: 565 us against 533 for 4 tiles, 677 for
-// 4 wavefronts of 4 tiles).
+// exceptions below.  Measured on the dense 27B-class layer's four shapes at M = 17 .. 2048 against
+// 2- and 4-tile, 4- and 8-wavefront shapes at depth 2 and 4 and splits of 1, 2 and 4: the best shape
+// or within 5% of it everywhere (down M = 512: 106.9 us against 101.7 split in four).
 bool auto_config_w8a8(int M, int N, int K, int layout, qf_w8a16_config* c) {
   if (M < 1 || N < 1 || K < QF_W8A16_K_ALIGN || K % QF_W8A16_K_ALIGN) return false;
   if (layout != QF_LAYOUT_TILED && layout != QF_LAYOUT_ROWMAJOR) return false;
