@@ -21,6 +21,7 @@
  *   qf_w8a16_workspace_bytes <- the fp32 split-K buffer torch.zeros   plugin/qwen_fastpath/w8a16.py:78-79
  *   qf_quantize_rows_int8    <- draft-head per-row quantizer   plugin/qwen_fastpath/patches.py:139-147
  *   qf_argmax_rows_bf16      <- pad mask + argmax of draft logits   plugin/qwen_fastpath/patches.py:182-185
+ *   qf_argmax_rows_bf16_ws   <- the same, with its candidate table in a caller workspace    patches.py:182-185
  *   qf_w8a16_gemm_argmax     <- draft logits + pad mask + argmax in one launch   patches.py:160-166,178-185
  *   qf_quantize_tokens_int8  <- ops.scaled_int8_quant (dynamic, symmetric)   plugin/qwen_fastpath/patches.py:99
  *   qf_w8a8_gemm             <- ops.cutlass_scaled_mm on the int8 weights      plugin/qwen_fastpath/patches.py:100
@@ -221,6 +222,23 @@ int qf_quantize_rows_int8(const uint16_t* w, int64_t ldw, int8_t* q, float* s,
  * out[m] = index + index_offset (int64).  Reference: plugin/qwen_fastpath/patches.py:182-185. */
 int qf_argmax_rows_bf16(const uint16_t* logits, int64_t ld, int M, int N, int n_valid,
                         int64_t index_offset, int64_t* out, void* stream);
+
+/* qf_argmax_rows_bf16 with the candidate table of its row-split kernel in a caller workspace
+ * (qf_argmax_rows_workspace_bytes() bytes, 16-byte aligned) instead of the library's device-resident
+ * table, so that calls on different streams may overlap when each has its own workspace.  The first
+ * QF_W8A16_COUNTER_BYTES bytes are arrival counters, zero on entry and returned to zero (the counter
+ * prefix of a qf_w8a16_gemm workspace: the same buffer may serve calls of both issued in order).
+ * Reference: plugin/qwen_fastpath/patches.py:182-185, as qf_argmax_rows_bf16. */
+size_t qf_argmax_rows_workspace_bytes(void);
+int qf_argmax_rows_bf16_ws(const uint16_t* logits, int64_t ld, int M, int N, int n_valid,
+                           int64_t index_offset, int64_t* out, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/* Host helper for callers that keep one workspace per graph capture (a workspace first used inside a
+ * capture is zeroed by a kernel recorded into that graph): *capturing = 1 while `stream` is capturing
+ * a HIP graph, and *id = that capture's id (unique per capture; 0 when not capturing).  No reference
+ * counterpart (the reference allocates its split-K buffer per call, plugin/qwen_fastpath/w8a16.py:76-79). */
+int qf_stream_capture_info(void* stream, int* capturing, unsigned long long* id);
 
 /* Diagnostic: read every byte of [buf, buf + bytes) once with 16-byte non-temporal loads across
  * `blocks` workgroups of 256 threads, writing one xor per workgroup to sink[blocks].  The practical

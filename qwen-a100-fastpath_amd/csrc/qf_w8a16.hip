@@ -617,10 +617,13 @@ __global__ void __launch_bounds__(WN * WK * kWave) w8a16_mfma_kernel(const GemmA
   }
   // The partials are written with device-scope stores (written through to the device's coherence
   // point) and every wavefront waits for its stores to complete; after the barrier, thread 0 counts
-  // the workgroup's arrival.  The last arrival reads the partials with device-scope loads, issued
-  // only once the increment has returned and selected this workgroup.  (A device-scope release
-  // fence would instead write back the XCD's whole L2, once per workgroup: measured, that costs
-  // more than the second-pass kernel it replaces.)
+  // the workgroup's arrival.  The last arrival takes a device-scope acquire fence and then reads the
+  // partials with device-scope loads, issued only once the increment has returned and selected this
+  // workgroup.  The acquire (an invalidate of this XCD's L2) runs once per n-block, on the last
+  // arrival only.  On the publishing side a device-scope release fence would write back the XCD's
+  // whole L2 once per workgroup (measured: slower than the second-pass kernel it replaces); the
+  // partials instead reach the coherence point as device-scope stores completed before the
+  // increment is issued.
   if (holder) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -641,6 +644,7 @@ __global__ void __launch_bounds__(WN * WK * kWave) w8a16_mfma_kernel(const GemmA
   }
   __syncthreads();
   if (!last_arrival) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   if (holder) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -1531,8 +1535,9 @@ __global__ void __launch_bounds__(kArgmaxThreads) argmax_rows_kernel(const uint1
 // index) with device-scope stores into a small device-resident table, waits for them, and counts
 // its arrival on the row's counter; the last workgroup of the row folds all candidates (the order
 // is total -- value, then index, NaN highest -- so the fold does not depend on arrival order),
-// writes the index and resets the counter to zero.  Calls that overlap on one device share the
-// table and must not run at the same time.
+// writes the index and resets the counter to zero.  The table is either the library's device-resident
+// one (qf_argmax_rows_bf16: calls that overlap on one device share it and must not run at the same
+// time) or the caller's workspace (qf_argmax_rows_bf16_ws: one workspace per stream).
 constexpr int kArgmaxSplitThreads = 256;
 constexpr int kArgmaxChunk = 8192;            // logits per workgroup (16 KiB)
 constexpr int kArgmaxMaxBlocks = 64;          // chunks per row
@@ -1540,6 +1545,15 @@ constexpr int kArgmaxMaxRows = QF_W8A16_MAX_M;
 __device__ float g_argmax_val[kArgmaxMaxRows * kArgmaxMaxBlocks];
 __device__ int g_argmax_idx[kArgmaxMaxRows * kArgmaxMaxBlocks];
 __device__ unsigned g_argmax_arrivals[kArgmaxMaxRows];
+
+// Candidate table of the row-split argmax in a caller workspace: the per-row arrival counters at the
+// front of the counter prefix (zero on entry, returned to zero), the (value, index) pairs after it.
+struct ArgmaxTable {
+  float* val;
+  int* idx;
+  unsigned* arrivals;
+};
+constexpr size_t kArgmaxTableBytes = (size_t)kArgmaxMaxRows * kArgmaxMaxBlocks * (sizeof(float) + sizeof(int));
 
 __device__ __forceinline__ void argmax_block_reduce(float& bv, int& bi, float* sv, int* si) {
 #pragma unroll
@@ -1559,9 +1573,13 @@ __device__ __forceinline__ void argmax_block_reduce(float& bv, int& bi, float* s
   }
 }
 
+template <bool kOwnTable>
 __global__ void __launch_bounds__(kArgmaxSplitThreads) argmax_rows_split_kernel(const uint16_t* logits, int64_t ld,
                                                                                 int n_valid, int64_t index_offset,
-                                                                                int64_t* out) {
+                                                                                int64_t* out, ArgmaxTable tab) {
+  float* const tval = kOwnTable ? g_argmax_val : tab.val;
+  int* const tidx = kOwnTable ? g_argmax_idx : tab.idx;
+  unsigned* const tarr = kOwnTable ? g_argmax_arrivals : tab.arrivals;
   __shared__ float sv[kArgmaxSplitThreads / kWave];
   __shared__ int si[kArgmaxSplitThreads / kWave];
   __shared__ int last;
@@ -1605,27 +1623,28 @@ __global__ void __launch_bounds__(kArgmaxSplitThreads) argmax_rows_split_kernel(
   argmax_block_reduce(bv, bi, sv, si);
   if (threadIdx.x == 0) {
     const int slot = m * kArgmaxMaxBlocks + b;
-    __hip_atomic_store(&g_argmax_val[slot], bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&g_argmax_idx[slot], bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&tval[slot], bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&tidx[slot], bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-    const unsigned prev = __hip_atomic_fetch_add(&g_argmax_arrivals[m], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned prev = __hip_atomic_fetch_add(&tarr[m], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last = prev == (unsigned)(nb - 1);
   }
   __syncthreads();
   if (!last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   bv = -__builtin_inff();
   bi = 0x7fffffff;
   if ((int)threadIdx.x < nb) {
     const int slot = m * kArgmaxMaxBlocks + threadIdx.x;
-    bv = __hip_atomic_load(&g_argmax_val[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    bi = __hip_atomic_load(&g_argmax_idx[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bv = __hip_atomic_load(&tval[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bi = __hip_atomic_load(&tidx[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();  // sv / si are reused
   argmax_block_reduce(bv, bi, sv, si);
   if (threadIdx.x == 0) {
     const int idx = (bi == 0x7fffffff) ? 0 : bi;
     out[m] = (int64_t)idx + index_offset;
-    __hip_atomic_store(&g_argmax_arrivals[m], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&tarr[m], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -2362,6 +2381,9 @@ int run_w8a8(const int8_t* xq, int64_t ldq, const float* s_a, const int8_t* w, i
   return launch(&splitk_reduce_w8a8_kernel, dim3(ceil_div(M * (a.n_pad / 4), 256)), dim3(256), 0, s, a);
 }
 
+int argmax_rows(const uint16_t* logits, int64_t ld, int M, int N, int n_valid, int64_t index_offset, int64_t* out,
+                const ArgmaxTable* tab, void* stream);
+
 }  // namespace qf
 
 using namespace qf;
@@ -2524,6 +2546,16 @@ int qf_w8a8_gemm(const int8_t* xq, int64_t ldq, const float* s_a, const int8_t* 
                   stream);
 }
 
+int qf_stream_capture_info(void* stream, int* capturing, unsigned long long* id) {
+  if (capturing == nullptr || id == nullptr) return QF_ERR_INVALID_ARG;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  unsigned long long cid = 0;
+  if (hipStreamGetCaptureInfo(reinterpret_cast<hipStream_t>(stream), &st, &cid) != hipSuccess) return QF_ERR_HIP;
+  *capturing = st == hipStreamCaptureStatusActive;
+  *id = *capturing ? cid : 0;
+  return QF_OK;
+}
+
 int qf_read_probe(const void* buf, size_t bytes, uint32_t* sink, int blocks, void* stream) {
   if (buf == nullptr || sink == nullptr || blocks < 1 || bytes % 16 || !aligned16(buf)) return QF_ERR_INVALID_ARG;
   hipLaunchKernelGGL(read_probe_kernel, dim3(blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
@@ -2531,15 +2563,45 @@ int qf_read_probe(const void* buf, size_t bytes, uint32_t* sink, int blocks, voi
   return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
 }
 
+size_t qf_argmax_rows_workspace_bytes(void) { return QF_W8A16_COUNTER_BYTES + qf::kArgmaxTableBytes; }
+
+int qf_argmax_rows_bf16_ws(const uint16_t* logits, int64_t ld, int M, int N, int n_valid, int64_t index_offset,
+                           int64_t* out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (workspace == nullptr || workspace_bytes < qf_argmax_rows_workspace_bytes() || !aligned16(workspace))
+    return QF_ERR_WORKSPACE;
+  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  ArgmaxTable tab;
+  tab.arrivals = reinterpret_cast<unsigned*>(ws);
+  tab.val = reinterpret_cast<float*>(ws + QF_W8A16_COUNTER_BYTES);
+  tab.idx = reinterpret_cast<int*>(ws + QF_W8A16_COUNTER_BYTES + (size_t)kArgmaxMaxRows * kArgmaxMaxBlocks * sizeof(float));
+  return argmax_rows(logits, ld, M, N, n_valid, index_offset, out, &tab, stream);
+}
+
 int qf_argmax_rows_bf16(const uint16_t* logits, int64_t ld, int M, int N, int n_valid, int64_t index_offset,
                         int64_t* out, void* stream) {
+  return argmax_rows(logits, ld, M, N, n_valid, index_offset, out, nullptr, stream);
+}
+
+}  // extern "C"
+
+namespace qf {
+
+// Row argmax (qf_argmax_rows_bf16 / _ws): the row-split kernel for long aligned rows, with the
+// library's own candidate table (tab == nullptr) or the caller's; one workgroup per row otherwise.
+int argmax_rows(const uint16_t* logits, int64_t ld, int M, int N, int n_valid, int64_t index_offset, int64_t* out,
+                const ArgmaxTable* tab, void* stream) {
   if (logits == nullptr || out == nullptr || M < 1 || N < 1 || ld < N || n_valid < 0 || n_valid > N)
     return QF_ERR_INVALID_ARG;
   const bool vec = aligned16(logits) && (ld % 8) == 0;
   const int chunks = ceil_div(n_valid, kArgmaxChunk);
   if (vec && M <= kArgmaxMaxRows && chunks >= 2 && chunks <= kArgmaxMaxBlocks) {
-    hipLaunchKernelGGL(argmax_rows_split_kernel, dim3(chunks, M), dim3(kArgmaxSplitThreads), 0,
-                       reinterpret_cast<hipStream_t>(stream), logits, ld, n_valid, index_offset, out);
+    const ArgmaxTable none = {nullptr, nullptr, nullptr};
+    if (tab == nullptr)
+      hipLaunchKernelGGL(argmax_rows_split_kernel<true>, dim3(chunks, M), dim3(kArgmaxSplitThreads), 0,
+                         reinterpret_cast<hipStream_t>(stream), logits, ld, n_valid, index_offset, out, none);
+    else
+      hipLaunchKernelGGL(argmax_rows_split_kernel<false>, dim3(chunks, M), dim3(kArgmaxSplitThreads), 0,
+                         reinterpret_cast<hipStream_t>(stream), logits, ld, n_valid, index_offset, out, *tab);
   } else if (vec)
     hipLaunchKernelGGL(argmax_rows_kernel<true>, dim3(M), dim3(kArgmaxThreads), 0, reinterpret_cast<hipStream_t>(stream),
                        logits, ld, n_valid, index_offset, out);
@@ -2549,4 +2611,4 @@ int qf_argmax_rows_bf16(const uint16_t* logits, int64_t ld, int M, int N, int n_
   return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
 }
 
-}  // extern "C"
+}  // namespace qf

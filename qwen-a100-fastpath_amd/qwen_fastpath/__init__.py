@@ -29,7 +29,9 @@ from .patches import (  # noqa: F401
     qf_int8_linear,
     quantize_lm_head,
     repack_layer_weight,
+    shape_eligible,
     top_tokens,
+    weight_layout,
     w8a8_reference,
 )
 

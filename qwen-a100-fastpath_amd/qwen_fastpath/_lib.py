@@ -33,6 +33,7 @@ KERNEL_MFMA_W8A8 = 5
 
 MAX_M = 16
 K_ALIGN = 64
+COUNTER_BYTES = 65536  # QF_W8A16_COUNTER_BYTES: arrival counters at the front of a workspace
 
 # Every symbol include/qf_w8a16.h declares.
 EXPORTS = (
@@ -48,8 +49,11 @@ EXPORTS = (
     "qf_scale_cast_bf16",
     "qf_quantize_rows_int8",
     "qf_argmax_rows_bf16",
+    "qf_argmax_rows_workspace_bytes",
+    "qf_argmax_rows_bf16_ws",
     "qf_w8a16_gemm_argmax",
     "qf_w8a16_argmax_workspace_bytes",
+    "qf_stream_capture_info",
     "qf_read_probe",
     "qf_quantize_tokens_int8",
     "qf_w8a8_gemm",
@@ -132,6 +136,12 @@ def load() -> ctypes.CDLL:
     L.qf_quantize_rows_int8.restype = i32
     L.qf_argmax_rows_bf16.argtypes = [p, i64, i32, i32, i32, i64, p, p]
     L.qf_argmax_rows_bf16.restype = i32
+    L.qf_argmax_rows_workspace_bytes.argtypes = []
+    L.qf_argmax_rows_workspace_bytes.restype = sz
+    L.qf_argmax_rows_bf16_ws.argtypes = [p, i64, i32, i32, i32, i64, p, p, sz, p]
+    L.qf_argmax_rows_bf16_ws.restype = i32
+    L.qf_stream_capture_info.argtypes = [p, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_ulonglong)]
+    L.qf_stream_capture_info.restype = i32
     L.qf_w8a16_gemm_argmax.argtypes = [p, i64, p, i64, i32, p, p, i64, i32, i32, i32, i32, i32, i64, p,
                                        ctypes.POINTER(Config), p, sz, p]
     L.qf_w8a16_gemm_argmax.restype = i32
@@ -182,6 +192,14 @@ def w8a8_pick_config(M: int, N: int, K: int, layout: int = LAYOUT_TILED) -> Conf
         return None
     check(rc, "qf_w8a8_pick_config")
     return c
+
+
+def capture_id(stream_handle: int) -> int:
+    """Id of the graph capture `stream_handle` is recording (0 when it is not capturing)."""
+    capturing, cid = ctypes.c_int(0), ctypes.c_ulonglong(0)
+    check(load().qf_stream_capture_info(stream_handle, ctypes.byref(capturing), ctypes.byref(cid)),
+          "qf_stream_capture_info")
+    return int(cid.value) if capturing.value else 0
 
 
 def workspace_bytes(M: int, N: int, K: int, layout: int, cfg: Config | None) -> int:

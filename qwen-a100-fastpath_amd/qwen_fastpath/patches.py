@@ -28,8 +28,8 @@ from typing import Callable, NamedTuple, Optional
 import torch
 
 from . import _lib as L
-from .w8a16 import (ROWMAJOR, SMALL_M, TILED, pick_config, to_tiled, w8a16_mm, w8a16_mm_argmax, w8a16_mm_prefill,
-                    w8a8_mm)
+from .w8a16 import (ROWMAJOR, SMALL_M, TILED, _workspace, from_tiled, pick_config, to_tiled, w8a16_mm,
+                    w8a16_mm_argmax, w8a16_mm_prefill, w8a8_mm)
 
 logger = logging.getLogger("vllm.qwen_fastpath")
 
@@ -106,8 +106,8 @@ def make_attention_forward(orig_forward: Callable, split_kv_cache: Callable = _i
             num_reqs = md.query_start_loc.shape[0] - 1
             key_cache, value_cache = split_kv_cache(kv_cache, self.head_size)
             q3 = query.view(query.shape[0], self.num_heads, self.head_size)
-            if supported(q3, key_cache, q_len, self.num_kv_heads):
-                o3 = output.view(output.shape[0], self.num_heads, self.head_size)
+            o3 = output.view(output.shape[0], self.num_heads, self.head_size)
+            if supported(q3, key_cache, q_len, self.num_kv_heads, value_cache, o3, num_reqs):
                 gqa_packed_spec_attention(q3, key_cache, value_cache, o3, md.seq_lens, md.block_table,
                                           num_reqs, q_len, self.num_kv_heads, self.scale)
                 return output
@@ -222,6 +222,11 @@ def prefill_arithmetic() -> str:
 
 
 def _fallback(x2, w_q, w_s, bias, out_dtype, layout):
+    if layout == TILED and x2.dtype != torch.bfloat16:
+        # The library's kernels take bf16 activations.  Others (fp16 models) get the reference's W8A8
+        # arithmetic restated in torch over the row-major weights recovered from the image (exact).
+        N = w_s.numel()
+        return w8a8_reference(x2, from_tiled(w_q, N, x2.shape[1]), w_s.reshape(-1).float(), bias, out_dtype)
     if layout == TILED and prefill_arithmetic() == "w8a8":
         # The reference's M > 16 arithmetic, on the TILED image CUTLASS cannot read: per-token int8
         # activations times the int8 weights on v_mfma_i32_16x16x64_i8 (gate_up M = 512: 169 us,
@@ -254,8 +259,8 @@ def _w8a8_hip(x2, w_q, w_s, bias, out_dtype):
     M, K = x2.shape
     N = w_s.numel()
     if (x2.dtype == torch.bfloat16 and out_dtype in (torch.bfloat16, torch.float32) and w_q.dim() == 2
-            and w_q.shape == (K, N) and w_q.stride(0) == 1 and w_q.stride(1) % 16 == 0
-            and w_s.dtype == torch.float32 and pick_config(N, K, ROWMAJOR) is not None):
+            and w_q.shape == (K, N) and w_q.stride(0) == 1 and w_q.stride(1) % 16 == 0 and w_q.data_ptr() % 16 == 0
+            and w_q.is_cuda and w_s.dtype == torch.float32 and pick_config(N, K, ROWMAJOR) is not None):
         y = w8a8_mm(x2, w_q, w_s.reshape(-1), out_dtype, layout=ROWMAJOR)
         return y if bias is None else y + bias
     return w8a8_reference(x2, w_q, w_s, bias, out_dtype)
@@ -265,8 +270,22 @@ def _w8a8_hip(x2, w_q, w_s, bias, out_dtype):
 # dispatcher op (patches.py:84-106)
 # ------------------------------------------------------------------------------------------------
 
-def eligible(x2: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, layout: int = ROWMAJOR) -> bool:
-    """The reference's predicate (patches.py:90-92), plus: the tensors live on the GPU."""
+def weight_layout(w_q: torch.Tensor) -> int:
+    """The layout a weight tensor holds: the TILED image is 1-D (to_tiled), the checkpoint's row-major
+    weight the 2-D [K, N] view with stride (1, K) (w8a16.py:72)."""
+    return TILED if w_q.dim() == 1 else ROWMAJOR
+
+
+def out_features(w_q: torch.Tensor, w_s: torch.Tensor) -> int:
+    """N: the [K, N] view's second dimension, or one per scale for the TILED image."""
+    return w_s.numel() if w_q.dim() == 1 else w_q.shape[1]
+
+
+def shape_eligible(x2: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, layout: Optional[int] = None) -> bool:
+    """The reference's predicate (patches.py:90-92): M <= SMALL_M, bf16 activations, w_q.stride(0) == 1
+    (the [K, N] view of the row-major weight; the TILED image has no such stride), one scale per output
+    channel, and a configuration for (N, K) (None when K % 64 != 0)."""
+    layout = weight_layout(w_q) if layout is None else layout
     M, K = x2.shape
     if layout == ROWMAJOR:
         N = w_q.shape[1]
@@ -275,14 +294,23 @@ def eligible(x2: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, layout: int
         N = w_s.numel()
         layout_ok = True
     return (M <= SMALL_M and x2.dtype == torch.bfloat16 and layout_ok and w_s.numel() == N
-            and x2.is_cuda and pick_config(N, K, layout) is not None)
+            and pick_config(N, K, layout) is not None)
 
 
-def _qf_int8_linear_impl(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, bias: Optional[torch.Tensor],
-                         layout: int = ROWMAJOR) -> torch.Tensor:
+def eligible(x2: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, layout: Optional[int] = None) -> bool:
+    """shape_eligible, and the tensors live on the GPU."""
+    return x2.is_cuda and shape_eligible(x2, w_q, w_s, layout)
+
+
+def _qf_int8_linear_impl(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor,
+                         bias: Optional[torch.Tensor]) -> torch.Tensor:
+    layout = weight_layout(w_q)
     lead = x.shape[:-1]
     x2 = x.reshape(-1, x.shape[-1])
-    N = w_q.shape[1] if layout == ROWMAJOR else w_s.numel()
+    N = out_features(w_q, w_s)
+    if x2.shape[0] == 0:  # no tokens
+        y = x.new_empty((*lead, N))
+        return y if bias is None else y + bias
     if eligible(x2, w_q, w_s, layout):
         if x2.stride(-1) != 1:
             x2 = x2.contiguous()
@@ -297,18 +325,36 @@ def _qf_int8_linear_impl(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, 
     return y.view(*lead, N)
 
 
-@torch.library.custom_op("qwen_fastpath::qf_int8_linear", mutates_args=())
-def qf_int8_linear(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, bias: Optional[torch.Tensor],
-                   layout: int = 0) -> torch.Tensor:
-    """torch.ops.qwen_fastpath.qf_int8_linear(x, w_q, w_s, bias, layout=0): one opaque node under
-    torch.compile, like the reference's torch.ops.vllm.qf_int8_linear."""
-    return _qf_int8_linear_impl(x, w_q, w_s, bias, layout)
+def _qf_int8_linear_fake(x, w_q, w_s, bias):
+    return x.new_empty((*x.shape[:-1], out_features(w_q, w_s)))
 
 
-@qf_int8_linear.register_fake
-def _qf_int8_linear_fake(x, w_q, w_s, bias, layout=0):
-    N = w_q.shape[1] if layout == ROWMAJOR else w_s.numel()
-    return x.new_empty((*x.shape[:-1], N))
+def _define_op(qualname: str):
+    op = torch.library.custom_op(qualname, mutates_args=())(_op_body)
+    op.register_fake(_qf_int8_linear_fake)
+    return op
+
+
+def _op_body(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, bias: Optional[torch.Tensor]) -> torch.Tensor:
+    """qf_int8_linear(x, w_q, w_s, bias): y [..., N] in x.dtype.  w_q is the [K, N] stride-(1, K) view of
+    the checkpoint's int8 weight, or its TILED image (1-D); w_s holds the N fp32 per-channel scales."""
+    return _qf_int8_linear_impl(x, w_q, w_s, bias)
+
+
+# torch.ops.vllm.qf_int8_linear(x, w_q, w_s, bias): the reference's op (patches.py:84-106, registered
+# there with vLLM's direct_register_custom_op), one opaque node under torch.compile with a fake impl;
+# torch.ops.qwen_fastpath.qf_int8_linear is the same op under this package's namespace.
+qf_int8_linear = _define_op("qwen_fastpath::qf_int8_linear")
+try:
+    qf_int8_linear_vllm = _define_op("vllm::qf_int8_linear")
+except RuntimeError as e:  # another plugin already defined it
+    qf_int8_linear_vllm = None
+    logger.warning("qwen_fastpath: vllm::qf_int8_linear already defined (%s); using qwen_fastpath::qf_int8_linear", e)
+
+
+def _linear_op():
+    """The op the patched surfaces call: vllm::qf_int8_linear when this package defined it."""
+    return torch.ops.vllm.qf_int8_linear if qf_int8_linear_vllm is not None else torch.ops.qwen_fastpath.qf_int8_linear
 
 
 # ------------------------------------------------------------------------------------------------
@@ -322,7 +368,7 @@ def make_apply_weights(orig_apply: Callable) -> Callable:
     def apply_weights(self, layer, x, bias=None):
         w_q, w_s, i_s, i_zp, azp_adj = self._get_layer_params(layer)
         if i_s is None and i_zp is None and azp_adj is None:  # dynamic symmetric per-token
-            return torch.ops.qwen_fastpath.qf_int8_linear(x, w_q, w_s, bias, getattr(layer, "_qf_layout", ROWMAJOR))
+            return _linear_op()(x, w_q, w_s, bias)
         return orig_apply(self, layer, x, bias)
 
     apply_weights._qwen_fastpath = True
@@ -346,8 +392,13 @@ def _import_attr(path: str):
 
 
 def tiled_layout_requested() -> bool:
-    """QWEN_FAST_LINEAR_LAYOUT=tiled: repack W8A8 linear weights into the TILED image at load time."""
-    return os.environ.get("QWEN_FAST_LINEAR_LAYOUT", "rowmajor").strip().lower() == "tiled"
+    """QWEN_FAST_LINEAR_LAYOUT: "tiled" (default) repacks W8A8 linear weights into the TILED image at load
+    time, in place of the row-major copy; "rowmajor" keeps the checkpoint layout, as the reference does
+    (plugin/qwen_fastpath/w8a16.py:1-7)."""
+    v = os.environ.get("QWEN_FAST_LINEAR_LAYOUT", "tiled").strip().lower()
+    if v not in ("tiled", "rowmajor"):
+        raise ValueError(f"QWEN_FAST_LINEAR_LAYOUT must be tiled or rowmajor, got {v!r}")
+    return v == "tiled"
 
 
 def repack_layer_weight(layer) -> bool:
@@ -360,6 +411,9 @@ def repack_layer_weight(layer) -> bool:
     if w is None or w.dtype != torch.int8 or w.dim() != 2 or not w.is_cuda or w.stride(0) != 1:
         return False
     if any(getattr(layer, n, None) is not None for n in ("input_scale", "input_zero_point", "azp_adj")):
+        return False
+    # the image serves bf16 activations; a model in another dtype keeps the layout its fallback reads
+    if getattr(layer, "params_dtype", torch.bfloat16) != torch.bfloat16:
         return False
     K, N = w.shape
     if pick_config(N, K, TILED) is None:
@@ -431,14 +485,13 @@ class W8A16LinearMethod:
         if self.fallback is not None:
             return self.fallback(layer, x, bias)
         x2 = x.reshape(-1, x.shape[-1])
-        y = _fallback(x2, layer.weight, layer.weight_scale, bias, x.dtype, getattr(layer, "_qf_layout", ROWMAJOR))
+        y = _fallback(x2, layer.weight, layer.weight_scale, bias, x.dtype, weight_layout(layer.weight))
         return y.view(*x.shape[:-1], y.shape[-1])
 
     def apply(self, layer, x: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
         dynamic = all(getattr(layer, n, None) is None for n in ("input_scale", "input_zero_point", "azp_adj"))
         if self.enabled and dynamic:
-            return torch.ops.qwen_fastpath.qf_int8_linear(x, layer.weight, layer.weight_scale, bias,
-                                                          getattr(layer, "_qf_layout", ROWMAJOR))
+            return _linear_op()(x, layer.weight, layer.weight_scale, bias)
         return self._original(layer, x, bias)
 
 
@@ -529,9 +582,12 @@ def top_tokens(logits: torch.Tensor, num_pad: int = 0, vocab_start: int = 0) -> 
         raise TypeError("top_tokens expects 2-D bf16 logits with unit column stride")
     M, N = logits.shape
     out = torch.empty((M,), dtype=torch.int64, device=logits.device)
+    lib = L.load()
+    ws = _workspace(logits.device, int(lib.qf_argmax_rows_workspace_bytes()))
     stream = torch.cuda.current_stream(logits.device).cuda_stream
-    L.check(L.load().qf_argmax_rows_bf16(logits.data_ptr(), logits.stride(0), M, N, N - int(num_pad),
-                                         int(vocab_start), out.data_ptr(), stream), "qf_argmax_rows_bf16")
+    L.check(lib.qf_argmax_rows_bf16_ws(logits.data_ptr(), logits.stride(0) if M > 1 else N, M, N, N - int(num_pad),
+                                       int(vocab_start), out.data_ptr(), ws.data_ptr(), ws.numel(), stream),
+            "qf_argmax_rows_bf16_ws")
     return out
 
 

@@ -53,13 +53,31 @@ def _check_bf16_rows(t: torch.Tensor, name: str):
         raise ValueError(f"{name} must be a GPU tensor")
 
 
-def supported(query: torch.Tensor, key_cache: torch.Tensor, Q: int, num_kv_heads: int) -> bool:
-    """Shapes the library serves: head size 64/128/256, Q * (H / H_kv) <= 64 packed rows,
-    pages of at least 16 positions, 16-byte aligned rows."""
+def supported(query: torch.Tensor, key_cache: torch.Tensor, Q: int, num_kv_heads: int,
+              value_cache: torch.Tensor | None = None, out: torch.Tensor | None = None,
+              num_reqs: int | None = None) -> bool:
+    """Calls the library serves, the checks of qf_spec_attention (csrc/qf_spec_attn.hip) restated so
+    that anything else takes the caller's original path instead of raising: head size 64/128/256,
+    Q * (H / H_kv) <= 64 packed rows, pages of at least 16 positions, every row stride a multiple of
+    8 elements, 16-byte aligned tensors, a grid of at most 65535 (request, kv head) pairs, a 32-bit
+    token count and per-stage byte offsets, and the same head geometry in every tensor."""
     H, D = query.shape[1], query.shape[2]
-    if D not in AL.HEAD_SIZES or H % num_kv_heads or Q < 1 or Q * (H // num_kv_heads) > AL.MAX_ROWS:
+    if D not in AL.HEAD_SIZES or num_kv_heads < 1 or H % num_kv_heads or Q < 1 or Q * (H // num_kv_heads) > AL.MAX_ROWS:
         return False
     if key_cache.shape[1] < AL.MIN_PAGE:
+        return False
+    tensors = [t for t in (query, key_cache, value_cache, out) if t is not None]
+    for t in tensors:
+        if t.dtype != torch.bfloat16 or t.stride(-1) != 1 or not t.is_cuda or t.data_ptr() % 16:
+            return False
+        if any(s < 0 or s % 8 for s in t.stride()[:-1]):
+            return False
+    if out is not None and (out.shape[1] != H or out.shape[2] != D):
+        return False
+    tok_strides = [key_cache.stride(1)] + ([value_cache.stride(1)] if value_cache is not None else [])
+    if max(tok_strides) * 2 * AL.KEY_BLOCK >= 1 << 31:
+        return False
+    if num_reqs is not None and (num_reqs < 1 or num_reqs * num_kv_heads > 65535 or num_reqs * Q * H > 0x7FFFFFFF):
         return False
     return True
 

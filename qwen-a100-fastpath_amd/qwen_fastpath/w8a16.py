@@ -93,29 +93,37 @@ def _weight_geometry(w: torch.Tensor, N: int, K: int, layout: int) -> int:
     raise ValueError(f"unknown layout {layout}")
 
 
-# Split-K workspace, one per device: allocated zeroed outside graph capture and reused.  The
-# library's arrival counters at the front of it are zero before every call and are returned to zero
-# by it, so every call issued in order on the device -- eager, or replayed from a graph, whichever
-# stream captured it -- can share the buffer; the partial sums behind the counters need no
-# clearing.  Two split-K calls running at the same time on different streams of one device would
-# share it too, which is not supported.
-_workspaces: dict[int, torch.Tensor] = {}
-_retired: list[torch.Tensor] = []  # superseded workspaces stay allocated: captured graphs may hold them
+# Workspaces (split-K partials and arrival counters, the fused argmax's candidate table, the row-split
+# argmax table), one per (device, stream): calls issued in order on one stream share it, and calls on
+# different streams never do, so they may overlap.  The library's arrival counters at the front of a
+# workspace must be zero when a call starts and every call leaves them zero, so:
+# * an eager workspace is allocated zeroed, grown by doubling, and reused by every later call on its
+#   stream;
+# * inside a graph capture, calls get a workspace of that capture (keyed by the capture id), whose
+#   counters are cleared by a fill kernel recorded into the graph ahead of its first use: each replay
+#   starts from zero, whatever ran on the stream before.  It stays allocated with the graph's memory.
+_workspaces: dict[tuple, torch.Tensor] = {}
+_capture_keep: list[torch.Tensor] = []  # superseded capture workspaces still referenced by their graph
 _WS_MIN = 8 << 20
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    key = device.index if device.index is not None else torch.cuda.current_device()
+    dev = device.index if device.index is not None else torch.cuda.current_device()
+    handle = torch.cuda.current_stream(device).cuda_stream
+    if torch.cuda.is_current_stream_capturing():
+        key = (dev, handle, L.capture_id(handle))
+        ws = _workspaces.get(key)
+        if ws is None or ws.numel() < nbytes:
+            if ws is not None:
+                _capture_keep.append(ws)
+            ws = torch.empty(max(nbytes, L.COUNTER_BYTES), dtype=torch.uint8, device=device)
+            ws[:L.COUNTER_BYTES].zero_()
+            _workspaces[key] = ws
+        return ws
+    key = (dev, handle)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError(
-                f"W8A16 split-K workspace of {nbytes} bytes is not allocated on this device; run the op "
-                "once outside graph capture (a warm-up) before capturing it")
-        size = max(nbytes, _WS_MIN, 0 if ws is None else 2 * ws.numel())
-        if ws is not None:
-            _retired.append(ws)
-        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        ws = torch.zeros(max(nbytes, _WS_MIN, 0 if ws is None else 2 * ws.numel()), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
 
@@ -130,6 +138,10 @@ def _launch(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, layout: int
     M, K = x.shape
     N = w_scale.numel()
     ldw = _weight_geometry(w, N, K, layout)
+    if M == 0:  # no tokens: an empty result, as the reference's masked grid gives
+        if out_dtype not in (torch.bfloat16, torch.float32):
+            raise TypeError(f"out_dtype must be bf16 or fp32, got {out_dtype}")
+        return x.new_empty((0, N), dtype=out_dtype)
     if x.stride(1) != 1 and K > 1:
         x = x.contiguous()
     ldx = x.stride(0) if M > 1 else K
@@ -200,7 +212,7 @@ def w8a16_mm_argmax(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, n_v
     if ws_bytes == 0:
         return None
     if x.stride(1) != 1 or x.data_ptr() % 16 or (M > 1 and x.stride(0) % 8):
-        x = x.contiguous()
+        x = x.clone(memory_format=torch.contiguous_format)
     ldx = x.stride(0) if M > 1 else K
     s = w_scale.reshape(-1)
     if not s.is_contiguous() or s.data_ptr() % 16:
@@ -301,9 +313,11 @@ def quantize_tokens_int8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         raise TypeError("x must be a 2-D bf16 tensor")
     M, K = x.shape
     if x.stride(1) != 1 or x.data_ptr() % 16 or (M > 1 and x.stride(0) % 8):
-        x = x.contiguous()
+        x = x.clone(memory_format=torch.contiguous_format)
     xq = torch.empty((M, K), dtype=torch.int8, device=x.device)
     s_a = torch.empty((M,), dtype=torch.float32, device=x.device)
+    if M == 0:
+        return xq, s_a
     stream = torch.cuda.current_stream(x.device).cuda_stream
     L.check(L.load().qf_quantize_tokens_int8(x.data_ptr(), x.stride(0) if M > 1 else K, M, K, xq.data_ptr(), K,
                                              s_a.data_ptr(), stream), "qf_quantize_tokens_int8")
@@ -322,6 +336,10 @@ def w8a8_mm(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, out_dtype: 
     M, K = x.shape
     N = w_scale.numel()
     ldw = _weight_geometry(w, N, K, layout)
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"out_dtype must be bf16 or fp32, got {out_dtype}")
+    if M == 0:
+        return x.new_empty((0, N), dtype=out_dtype)
     xq, s_a = quantize_tokens_int8(x)
     s = w_scale.reshape(-1)
     if not s.is_contiguous() or s.data_ptr() % 16:

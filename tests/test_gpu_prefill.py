@@ -63,7 +63,7 @@ def test_prefill_dispatcher_on_tiled_layer(oracle, monkeypatch, M, mode):
     N, K = 512, 1024
     inp = oracle.gen_inputs(M, N, K, seed=M)
     x, w, s = dev_inputs(inp, DEV)
-    y = torch.ops.qwen_fastpath.qf_int8_linear(x.view(2, M // 2, K), qf.to_tiled(w), s, None, qf.TILED)
+    y = torch.ops.qwen_fastpath.qf_int8_linear(x.view(2, M // 2, K), qf.to_tiled(w), s, None)
     torch.cuda.synchronize()
     assert y.shape == (2, M // 2, N)
     if mode == "w8a16":

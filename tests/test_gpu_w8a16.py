@@ -116,7 +116,7 @@ def test_fused_split_k_counters_return_to_zero(oracle):
         cfg = qf.W8A16Config(L.KERNEL_MFMA, sk, 1, 16 if wk > 1 else 4, 8, 1, wk)
         for _ in range(3):
             ys.append(bf16_bits(run(x, w, s, cfg)))
-            ws = W._workspaces[0]
+            ws = W._workspaces[(0, torch.cuda.current_stream().cuda_stream)]
             assert int(ws[:65536].view(torch.int32).abs().sum()) == 0
         assert np.array_equal(ys[-1], ys[-2]) and np.array_equal(ys[-1], ys[-3])
         check(oracle, inp, ys[-1], label=f"fused split-K sk={sk} wk={wk}")

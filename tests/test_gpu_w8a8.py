@@ -96,11 +96,25 @@ def test_w8a8_layer_shapes(name, N, K):
         assert torch.equal(bits(y), bits(ref)), (name, M)
 
 
-@pytest.mark.parametrize("name,M,N,K", [("qkv", 128, 10240, 5120), ("o_proj", 256, 5120, 8192),
-                                        ("down", 2048, 5120, 17408)])
-def test_w8a8_auto_exceptions(name, M, N, K):
-    """The automatic rule's exceptions (4-wavefront unsplit workgroups; a split in two on down at
-    M = 2048) against the restatement, on both layouts where they apply."""
+def w8a8_group_rows(cfg, M, N):
+    """Token rows per group of the W8A8 launch (w8a8_groups in csrc/qf_w8a16.hip, restated)."""
+    blocks = -(-((N + 15) // 16) // (cfg.waves * cfg.tiles_per_wave))
+    max_rows = 128 if cfg.tiles_per_wave == 2 and blocks * -(-M // 128) >= 128 else 64
+    g0 = -(-M // max_rows)
+    return (-(-M // g0) + 15) // 16 * 16
+
+
+@pytest.mark.parametrize("name,M,N,K,rows", [
+    ("qkv", 128, 10240, 5120, 64), ("o_proj", 256, 5120, 8192, 64), ("down", 2048, 5120, 17408, 128),
+    # 4-wavefront workgroups with token groups of more than 64 rows (5 to 8 token tiles a fragment)
+    ("qkv", 160, 10240, 5120, 80), ("qkv", 192, 10240, 5120, 96), ("n1280", 1600, 1280, 5120, 128)])
+def test_w8a8_auto_exceptions(name, M, N, K, rows):
+    """The automatic rule's exceptions (4-wavefront unsplit workgroups, also with 80- to 128-row token
+    groups; a split in two on down at M = 2048) against the restatement, on both layouts."""
+    cfg = L.w8a8_pick_config(M, N, K)
+    if name != "down":
+        assert cfg.waves == 4 and cfg.split_k == 1, cfg.to_tuple()
+    assert w8a8_group_rows(cfg, M, N) == rows, cfg.to_tuple()
     x, w, s = random_case(M, N, K, M + N)
     y = qf.w8a8_mm(x, qf.to_tiled(w.t()), s, torch.bfloat16)
     ref = P.w8a8_reference(x, w.t(), s, None, torch.bfloat16)
