@@ -48,6 +48,8 @@ extern "C" {
 #define QF_W8A16_K_ALIGN 64
 /* Bytes at the front of a split-K workspace that hold arrival counters (one per workgroup column). */
 #define QF_W8A16_COUNTER_BYTES 65536
+/* Size of the static device scratch of qf_w8a16_gemm_noalloc (counters + split partials), per device. */
+#define QF_W8A16_SCRATCH_BYTES (4u << 20)
 
 typedef enum qf_status {
   QF_OK = 0,
@@ -127,6 +129,22 @@ int qf_w8a16_gemm(const uint16_t* x, int64_t ldx,
                   const qf_w8a16_config* cfg,
                   void* workspace, size_t workspace_bytes,
                   void* stream);
+
+/* qf_w8a16_gemm without a workspace argument, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid allocation).  No counterpart in
+ * the reference.  The split-K workspace is a static device array of QF_W8A16_SCRATCH_BYTES per device,
+ * held until the process ends; a call that needs more (qf_w8a16_workspace_bytes > QF_W8A16_SCRATCH_BYTES)
+ * returns QF_ERR_WORKSPACE before launching anything.  Nothing is allocated or freed.  Every call on a
+ * device shares that device's array, so calls that may overlap on one device (different streams) race:
+ * issue them in order, or give them distinct workspaces through qf_w8a16_gemm.  Same results, bit for
+ * bit, as qf_w8a16_gemm with the same configuration. */
+int qf_w8a16_gemm_noalloc(const uint16_t* x, int64_t ldx,
+                          const int8_t* w, int64_t ldw, int layout,
+                          const float* scale,
+                          void* y, int64_t ldy, int out_dtype,
+                          int M, int N, int K,
+                          const qf_w8a16_config* cfg,
+                          void* stream);
 
 /* Fused draft-head argmax: the product of qf_w8a16_gemm, and
  *   ids[m] = index_offset + argmax_{n < n_valid} bf16(y[m, n])      (int64, m < M)

@@ -2384,6 +2384,43 @@ int run_w8a8(const int8_t* xq, int64_t ldq, const float* s_a, const int8_t* w, i
 int argmax_rows(const uint16_t* logits, int64_t ld, int M, int N, int n_valid, int64_t index_offset, int64_t* out,
                 const ArgmaxTable* tab, void* stream);
 
+// ---------------------------------------------------------------------------------------------
+// Static scratch of qf_w8a16_gemm_noalloc: the split-K workspace (arrival counters, then the fp32
+// partials) for callers that cannot allocate.  Every device the library runs on holds one copy until
+// the process ends.  Host code never uses the array's name as an address: it takes the device address
+// hipGetSymbolAddress returns, once per device with that device current, and passes that pointer.
+// ---------------------------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t scratch[QF_W8A16_SCRATCH_BYTES];
+
+__global__ void __launch_bounds__(256) clear_words_kernel(unsigned* p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];
+
+// The current device's scratch address.  The first call on a device fetches it and clears the arrival
+// counters with a kernel on `stream`, ahead of the call's own launches (the array is zero at load, and
+// every GEMM returns the counters it uses to zero).
+int device_scratch(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return QF_ERR_HIP;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return QF_ERR_HIP;
+    constexpr int words = QF_W8A16_COUNTER_BYTES / 4;
+    hipLaunchKernelGGL(clear_words_kernel, dim3(ceil_div(words, 256)), dim3(256), 0, stream,
+                       reinterpret_cast<unsigned*>(p), words);
+    if (hipGetLastError() != hipSuccess) return QF_ERR_HIP;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return QF_OK;
+}
+
 }  // namespace qf
 
 using namespace qf;
@@ -2425,6 +2462,20 @@ int qf_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, 
   if (y == nullptr) return QF_ERR_INVALID_ARG;
   return run_gemm(x, ldx, w, ldw, layout, scale, y, ldy, out_dtype, M, N, K, cfg, workspace, workspace_bytes, stream,
                   nullptr);
+}
+
+int qf_w8a16_gemm_noalloc(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int layout, const float* scale,
+                          void* y, int64_t ldy, int out_dtype, int M, int N, int K, const qf_w8a16_config* cfg,
+                          void* stream) {
+  const size_t need = qf_w8a16_workspace_bytes(M, N, K, layout, cfg);
+  if (need > QF_W8A16_SCRATCH_BYTES) return QF_ERR_WORKSPACE;
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = device_scratch(reinterpret_cast<hipStream_t>(stream), &ws);
+    if (rc != QF_OK) return rc;
+  }
+  return run_gemm(x, ldx, w, ldw, layout, scale, y, ldy, out_dtype, M, N, K, cfg, ws,
+                  ws != nullptr ? QF_W8A16_SCRATCH_BYTES : 0, stream, nullptr);
 }
 
 size_t qf_w8a16_argmax_workspace_bytes(int M, int N, int K, int layout, const qf_w8a16_config* cfg) {

@@ -34,6 +34,7 @@ KERNEL_MFMA_W8A8 = 5
 MAX_M = 16
 K_ALIGN = 64
 COUNTER_BYTES = 65536  # QF_W8A16_COUNTER_BYTES: arrival counters at the front of a workspace
+SCRATCH_BYTES = 4 << 20  # QF_W8A16_SCRATCH_BYTES: static scratch of qf_w8a16_gemm_noalloc, per device
 
 # Every symbol include/qf_w8a16.h declares.
 EXPORTS = (
@@ -42,6 +43,7 @@ EXPORTS = (
     "qf_w8a16_pick_config",
     "qf_w8a16_workspace_bytes",
     "qf_w8a16_gemm",
+    "qf_w8a16_gemm_noalloc",
     "qf_w8a16_tiled_bytes",
     "qf_w8a16_repack",
     "qf_w8a16_unpack",
@@ -122,6 +124,8 @@ def load() -> ctypes.CDLL:
     L.qf_w8a16_gemm.argtypes = [p, i64, p, i64, i32, p, p, i64, i32, i32, i32, i32,
                                 ctypes.POINTER(Config), p, sz, p]
     L.qf_w8a16_gemm.restype = i32
+    L.qf_w8a16_gemm_noalloc.argtypes = [p, i64, p, i64, i32, p, p, i64, i32, i32, i32, i32, ctypes.POINTER(Config), p]
+    L.qf_w8a16_gemm_noalloc.restype = i32
     L.qf_w8a16_tiled_bytes.argtypes = [i32, i32]
     L.qf_w8a16_tiled_bytes.restype = sz
     L.qf_w8a16_repack.argtypes = [p, i64, p, i32, i32, p]
