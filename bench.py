@@ -49,7 +49,7 @@ GEMMS = {  # name: (N, K)
 }
 DOMINANT = "gate_up"
 GRAPH_STEPS = 32  # decode steps captured per graph (a multiple of the rotated layer count)
-PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "w8a16_gate_up_m5_pmc.txt")
+PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "w8a16_layer_m5_pmc.md")
 W8A8_PROFILE = os.path.join(ROOT, "profiles", "w8a8_gate_up_m2048_pmc.txt")
 
 
@@ -111,46 +111,65 @@ def read_traffic(path=PROFILE_SUMMARY):
     return float(f.group(1)) + float(w.group(1))
 
 
-def cpu_baseline(M: int, seed: int = 0):
-    """Time the oracle's fp32-dequant restatement of the reference CPU path on one layer's GEMMs."""
-    import numpy as np
-    from oracle import oracle as O
+def host_threads() -> int:
+    """Threads for the CPU baseline: the box's OMP_NUM_THREADS when set (its CPU share), else every core
+    this process may run on."""
     try:
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
         cores = os.cpu_count() or 1
-    cores = max(1, min(cores, 16))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, int(env)) if env.isdigit() else cores
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def cpu_baseline(M: int, seed: int = 0):
+    """The oracle's fp32-dequant restatement of the reference CPU path (bench/test_w8a16.py:15,
+    F.linear(x.float(), W.float() * s[:, None])) per GEMM: the single 5120x5120 linear at M = 1 and each of
+    the layer's four GEMMs at M, one warm-up then the best of five.  value = the layer's four GEMMs'
+    algorithmic bytes / the sum of their best times."""
+    from oracle import oracle as O
+    cores = host_threads()
     try:
         from threadpoolctl import threadpool_limits
         limiter = threadpool_limits(limits=cores)
     except Exception:  # noqa: BLE001 - threadpoolctl optional
         limiter = None
-    inputs = [O.gen_inputs(M, N, K, seed=seed + i) for i, (N, K) in enumerate(GEMMS.values())]
-    total_bytes = sum(algo_bytes(M, N, K) for (N, K) in GEMMS.values())
-    best = float("inf")
-    for rep in range(3):
-        t0 = time.perf_counter()
-        for inp in inputs:
+    shapes = [("single_linear_m1", 1, 5120, 5120)] + [(n, M, N, K) for n, (N, K) in GEMMS.items()]
+    per = {}
+    for i, (name, m, N, K) in enumerate(shapes):
+        inp = O.gen_inputs(m, N, K, seed=seed + i)
+        O.fp32_dequant_linear(inp.x, inp.w, inp.s)
+        best = float("inf")
+        for _ in range(5):
+            t0 = time.perf_counter()
             O.fp32_dequant_linear(inp.x, inp.w, inp.s)
-        best = min(best, time.perf_counter() - t0)
-    if limiter is not None:
-        limiter.unregister() if hasattr(limiter, "unregister") else None
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+            best = min(best, time.perf_counter() - t0)
+        per[name] = {"M": m, "N": N, "K": K, "ms": round(best * 1e3, 2),
+                     "GB_s": round(algo_bytes(m, N, K) / best / 1e9, 3)}
+    if limiter is not None and hasattr(limiter, "unregister"):
+        limiter.unregister()
+    layer_s = sum(per[n]["ms"] for n in GEMMS) / 1e3
+    total_bytes = sum(algo_bytes(M, N, K) for (N, K) in GEMMS.values())
+    model = cpu_model()
     return {
-        "value": round(total_bytes / best / 1e9, 3),
+        "value": round(total_bytes / layer_s / 1e9, 3),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"one layer's 4 GEMMs at M={M} (qkv, o_proj, gate_up, down; {total_bytes / 1e6:.1f} MB), "
-                   f"best of 3, numpy fp32 BLAS over {cores} threads: {best * 1e3:.1f} ms/layer"
-                   + (f"; {cpu_model}" if cpu_model else "")),
+        "sample": (f"per GEMM, 1 warm-up + best of 5, numpy fp32 BLAS over {cores} threads: the layer's 4 GEMMs at M={M} "
+                   f"({total_bytes / 1e6:.1f} MB) take {layer_s * 1e3:.1f} ms; 5120x5120 at M=1 "
+                   f"{per['single_linear_m1']['ms']} ms" + (f"; {model}" if model else "")),
+        "per_gemm": per,
     }
 
 
@@ -163,7 +182,9 @@ def main():
                     default="layer")
     ap.add_argument("--layers", type=int, default=4, help="distinct layers rotated through (layer workload)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--profile-gemm", choices=list(GEMMS), default=None)
+    ap.add_argument("--profile-gemm", choices=list(GEMMS) + ["single"], default=None,
+                    help="only that GEMM at M=5 (single: the 5120x5120 linear at M=1), --iters launches, weights "
+                         "rotating past the MALL (for rocprofv3)")
     ap.add_argument("--profile-w8a8", type=int, default=None, metavar="M",
                     help="only the W8A8 GEMM on gate_up at M rows, --iters launches (for rocprofv3)")
     ap.add_argument("--iters", type=int, default=200)
@@ -213,6 +234,24 @@ def main():
             gemm(i % 2)
         torch.cuda.synchronize()
         log(f"profile: {args.iters} launches of the W8A8 GEMM on gate_up M={M} cfg={cfg.to_tuple()}")
+        return
+
+    if args.profile_gemm == "single":
+        N1 = K1 = 5120
+        g1 = torch.Generator(device=dev)
+        g1.manual_seed(99)
+        sets1 = []
+        for i in range(16):  # 16 x 26 MB rotate past the 256 MB MALL
+            w1 = torch.randint(-127, 128, (N1, K1), dtype=torch.int8, device=dev, generator=g1).t()
+            sets1.append((qf.to_tiled(w1) if layout == qf.TILED else w1,
+                          (torch.randn(N1, device=dev, generator=g1).abs() * 0.002 + 1e-4).float(),
+                          torch.randn(1, K1, device=dev, generator=g1).to(torch.bfloat16)))
+        for i in range(args.iters):
+            w1, s1, x1 = sets1[i % len(sets1)]
+            qf.w8a16_mm(x1, w1, s1, None, torch.bfloat16, layout)
+        torch.cuda.synchronize()
+        log(f"profile: {args.iters} launches of the single linear M=1 N=K=5120 layout={args.layout} "
+            f"cfg={tuple(qf.resolve_config(1, N1, K1, layout))}")
         return
 
     if args.profile_gemm:
@@ -338,9 +377,20 @@ def main():
                 "kernel": f"{DOMINANT} M={M} N={GEMMS[DOMINANT][0]} K={GEMMS[DOMINANT][1]}",
                 "algorithmic_bytes_per_launch": dom_bytes, "mean_launch_us": round(dominant_us, 2)}
 
-    ceiling = read_ceiling(torch, qf, dev, algo_bytes(M, *GEMMS[DOMINANT]))
-    log(f"  read probe ({algo_bytes(M, *GEMMS[DOMINANT]) / 1e6:.0f} MB windows): {ceiling:.0f} GB/s")
-    roofline["read_probe_GB_s"] = round(ceiling, 1)
+    # the practical ceiling at each GEMM's size: the library's read probe over the same bytes (no math)
+    for name, (N, K) in GEMMS.items():
+        b = algo_bytes(M, N, K)
+        gbs = read_ceiling(torch, qf, dev, b)
+        per_gemm[name]["read_probe_us"] = round(b / gbs / 1e3, 2)
+        per_gemm[name]["pct_of_read_probe"] = round(100 * per_gemm[name]["read_probe_us"] / per_gemm[name]["us"], 1)
+        log(f"  read probe {name:8s} ({b / 1e6:6.1f} MB): {b / gbs / 1e3:7.2f} us  {gbs:6.0f} GB/s")
+        if name == DOMINANT:
+            roofline["read_probe_GB_s"] = round(gbs, 1)
+    b1 = algo_bytes(1, N1, K1)
+    gbs1 = read_ceiling(torch, qf, dev, b1)
+    single["read_probe_us"] = round(b1 / gbs1 / 1e3, 2)
+
+    stack = stack64(torch, qf, dev, layout, steps=10, warmup=2)
 
     cpu = None if args.no_cpu else cpu_baseline(M)
 
@@ -365,6 +415,7 @@ def main():
         "pct_of_peak": round(100 * value / PEAK_GBS, 2),
         "per_gemm": per_gemm,
         "single_linear_m1": single,
+        "stack64": stack,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
@@ -372,36 +423,40 @@ def main():
 
 
 def read_ceiling(torch, qf, dev, window: int) -> float:
-    """GB/s of the library's read probe over rotating windows of `window` bytes in a 2 GB buffer
-    (the practical HBM read ceiling at the dominant GEMM's size), timed like the GEMMs."""
+    """GB/s of the library's read probe over rotating windows of `window` bytes (at least 768 MB in all, past
+    the 256 MB MALL), timed like the GEMMs; the best of two grid sizes: the practical HBM read ceiling at
+    that size, a launch included."""
     from qwen_fastpath import _lib as L
     window = window // 4096 * 4096
-    nwin = 8
+    nwin = max(8, -(-(768 << 20) // window))
     buf = torch.empty(nwin * window, dtype=torch.uint8, device=dev)
     buf.fill_(1)
-    blocks = 256 * 8
-    sink = torch.empty(blocks, dtype=torch.int32, device=dev)
     lib = L.load()
+    best = 0.0
+    for blocks in (512, 2048):
+        sink = torch.empty(blocks, dtype=torch.int32, device=dev)
 
-    def fn():
-        st = torch.cuda.current_stream().cuda_stream
-        for i in range(nwin):
-            L.check(lib.qf_read_probe(buf.data_ptr() + i * window, window, sink.data_ptr(), blocks, st), "probe")
+        def fn():
+            st = torch.cuda.current_stream().cuda_stream
+            for i in range(nwin):
+                L.check(lib.qf_read_probe(buf.data_ptr() + i * window, window, sink.data_ptr(), blocks, st), "probe")
 
-    g, _ = capture(torch, fn)
-    g.replay()
-    times = []
-    for _ in range(10):
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
+        g, _ = capture(torch, fn)
         g.replay()
-        e1.record()
-        e1.synchronize()
-        times.append(e0.elapsed_time(e1) * 1e3 / nwin)
-    us = sorted(times)[len(times) // 2]
+        times = []
+        for _ in range(10):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g.replay()
+            e1.record()
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3 / nwin)
+        us = sorted(times)[len(times) // 2]
+        best = max(best, window / us / 1e3)
+        del g
     del buf
-    return window / us / 1e3
+    return best
 
 
 def time_graph(torch, fn, launches, reps=10):
@@ -787,18 +842,35 @@ def run_spec_attn(torch, qf, dev, args):
     print(json.dumps(line), flush=True)
 
 
-def run_stack64(torch, qf, dev, args):
-    """64 layers x 4 GEMMs at M=5 with distinct weights, one hipGraph per decode step.  Glue between
-    GEMMs (the workload leaves it open): o_proj reads the first 8192 qkv outputs and down the first
-    17408 gate_up outputs, both as strided views (no copy); the next layer's input is the layer output
-    re-normalised to unit RMS per row (one fused torch rms_norm)."""
+class StackLayer:
+    """One layer of the 64-layer stack: its four weights drawn straight into the layout the GEMMs read
+    (random int8 in [-127, 127]; the TILED image is a permutation of the row-major weight, so random bytes
+    in it are a random weight) and scales |N(0,1)|*0.002 + 1e-4."""
+
+    def __init__(self, torch, qf, dev, seed: int, layout: int):
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        self.w, self.s = {}, {}
+        for name, (N, K) in GEMMS.items():
+            if layout == qf.TILED:
+                self.w[name] = torch.randint(-127, 128, (qf.tiled_numel(N, K),), dtype=torch.int8, device=dev,
+                                             generator=g)
+            else:
+                self.w[name] = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g).t()
+            self.s[name] = torch.randn(N, device=dev, generator=g).abs_().mul_(0.002).add_(1e-4)
+
+
+def stack64(torch, qf, dev, layout: int, steps: int, warmup: int) -> dict:
+    """64 layers x 4 GEMMs at M=5 with distinct weights (23.2 GB), one hipGraph per decode step.  Glue
+    between GEMMs (the workload leaves it open): o_proj reads the first 8192 qkv outputs and down the
+    first 17408 gate_up outputs, both as strided views (no copy); the next layer's input is the layer
+    output re-normalised to unit RMS per row (one fused torch rms_norm).  Timed by wall clock around
+    `steps` replays after `warmup`."""
     M = M_TOKENS
     nl = 64
     log(f"stack64: allocating {nl} layers ({nl * sum(N * K for N, K in GEMMS.values()) / 1e9:.1f} GB)")
-    layout = qf.TILED if args.layout == "tiled" else qf.ROWMAJOR
-    layers = [Layer(torch, qf, dev, 5000 + i, M, layout) for i in range(nl)]
+    layers = [StackLayer(torch, qf, dev, 5000 + i, layout) for i in range(nl)]
     x0 = torch.randn(M, 5120, device=dev).to(torch.bfloat16)
-    rms = lambda t: torch.nn.functional.rms_norm(t, (t.shape[-1],))  # noqa: E731
 
     def step():
         h = x0
@@ -808,32 +880,42 @@ def run_stack64(torch, qf, dev, args):
             o = mm(qkv[:, :8192], "o_proj")
             gu = mm(o, "gate_up")
             d = mm(gu[:, :17408], "down")
-            h = rms(d)
+            h = torch.nn.functional.rms_norm(d, (d.shape[-1],))
         return h
 
     g, _ = capture(torch, step)
     bytes_per_step = nl * sum(algo_bytes(M, N, K) for (N, K) in GEMMS.values())
-    for _ in range(max(1, args.warmup // 10)):
+    for _ in range(max(1, warmup)):
         g.replay()
     torch.cuda.synchronize()
-    steps = max(1, args.steps // 50)
     t0 = time.perf_counter()
     for _ in range(steps):
         g.replay()
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     value = steps * bytes_per_step / el / 1e9
-    log(f"stack64: {steps} steps, {el / steps * 1e3:.3f} ms/step, {value:.0f} GB/s ({100 * value / PEAK_GBS:.1f}% of 8 TB/s)")
+    log(f"stack64: {steps} steps, {el / steps * 1e3:.3f} ms/step, {value:.0f} GB/s "
+        f"({100 * value / PEAK_GBS:.1f}% of 8 TB/s)")
+    del g, layers
+    return {"layers": nl, "M": M, "steps": steps, "warmup": max(1, warmup), "bytes_per_step": bytes_per_step,
+            "ms_per_step": round(el / steps * 1e3, 4), "us_per_layer": round(el / steps / nl * 1e6, 2),
+            "GB_s": round(value, 1), "pct_peak": round(100 * value / PEAK_GBS, 2),
+            "timing": "wall clock around graph replays, one graph per decode step (256 GEMMs + 64 rms_norm)"}
+
+
+def run_stack64(torch, qf, dev, args):
+    layout = qf.TILED if args.layout == "tiled" else qf.ROWMAJOR
+    st = stack64(torch, qf, dev, layout, max(1, args.steps // 50), max(1, args.warmup // 10))
     line = {
-        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps,
-        "warmup": max(1, args.warmup // 10), "ms_per_step": round(el / steps * 1e3, 4), "higher_is_better": True,
+        "metric": METRIC, "value": st["GB_s"], "unit": "GB/s", "n_gpus": 1, "steps": st["steps"],
+        "warmup": st["warmup"], "ms_per_step": st["ms_per_step"], "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded int8 weights, fp32 scales, bf16 activations)",
         "config": {"workload": "64-layer decode-step linear stack at M=5 (4 GEMMs/layer, distinct weights, "
-                               "one rms_norm per layer), one hipGraph per step", "M": M, "layers": nl,
-                   "bytes_per_step": bytes_per_step},
-        "us_per_layer": round(el / steps / nl * 1e6, 2),
-        "pct_of_peak": round(100 * value / PEAK_GBS, 2),
+                               "one rms_norm per layer), one hipGraph per step", "M": st["M"], "layers": st["layers"],
+                   "bytes_per_step": st["bytes_per_step"]},
+        "us_per_layer": st["us_per_layer"],
+        "pct_of_peak": st["pct_peak"],
     }
     print(json.dumps(line), flush=True)
 

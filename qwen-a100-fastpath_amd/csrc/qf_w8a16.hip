@@ -617,13 +617,14 @@ __global__ void __launch_bounds__(WN * WK * kWave) w8a16_mfma_kernel(const GemmA
   }
   // The partials are written with device-scope stores (written through to the device's coherence
   // point) and every wavefront waits for its stores to complete; after the barrier, thread 0 counts
-  // the workgroup's arrival.  The last arrival takes a device-scope acquire fence and then reads the
-  // partials with device-scope loads, issued only once the increment has returned and selected this
-  // workgroup.  The acquire (an invalidate of this XCD's L2) runs once per n-block, on the last
-  // arrival only.  On the publishing side a device-scope release fence would write back the XCD's
-  // whole L2 once per workgroup (measured: slower than the second-pass kernel it replaces); the
-  // partials instead reach the coherence point as device-scope stores completed before the
-  // increment is issued.
+  // the workgroup's arrival.  The last arrival reads the partials with device-scope loads, which are
+  // served by the coherence point and are issued only once the increment has returned and selected
+  // this workgroup: every other split's stores had completed there before its own increment.  The
+  // ordering is that of the hardware, not a release/acquire pair of the memory model: a device-scope
+  // release fence writes back the XCD's whole L2 (measured: once per workgroup, slower than the
+  // second-pass kernel), and an acquire fence on the last arrival invalidates it (measured: down
+  // 5120x17408 at M = 5, 80 last arrivals in the kernel's tail, 18.5 -> 22.1 us).  reduce = 1 (the
+  // second-pass kernel) orders the partials by the kernel boundary instead.
   if (holder) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -644,7 +645,6 @@ __global__ void __launch_bounds__(WN * WK * kWave) w8a16_mfma_kernel(const GemmA
   }
   __syncthreads();
   if (!last_arrival) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   if (holder) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
