@@ -390,6 +390,17 @@ def main():
     gbs1 = read_ceiling(torch, qf, dev, b1)
     single["read_probe_us"] = round(b1 / gbs1 / 1e3, 2)
 
+    # the launch floor: the period of back-to-back graph launches of a kernel that reads 16 KiB -- what
+    # every GEMM launch pays before it moves its bytes; a GEMM of B bytes cannot take less than
+    # floor + B / 8 TB/s in this timing
+    floor = launch_floor(torch, qf, dev)
+    log(f"  launch floor (graph of trivial kernels): {floor:.2f} us per launch")
+    for name, (N, K) in list(GEMMS.items()) + [("single_linear_m1", (N1, K1))]:
+        d = per_gemm[name] if name in per_gemm else single
+        b = algo_bytes(1 if name == "single_linear_m1" else M, N, K)
+        d["us_at_peak_with_floor"] = round(floor + b / PEAK_GBS / 1e3, 2)
+        d["pct_peak_after_floor"] = round(100 * b / max(d["us"] - floor, 1e-3) / 1e3 / PEAK_GBS, 1)
+
     stack = stack64(torch, qf, dev, layout, steps=10, warmup=2)
 
     cpu = None if args.no_cpu else cpu_baseline(M)
@@ -415,6 +426,7 @@ def main():
         "pct_of_peak": round(100 * value / PEAK_GBS, 2),
         "per_gemm": per_gemm,
         "single_linear_m1": single,
+        "launch_floor_us": round(floor, 2),
         "stack64": stack,
         "roofline": roofline,
         "cpu_baseline": cpu,
@@ -457,6 +469,22 @@ def read_ceiling(torch, qf, dev, window: int) -> float:
         del g
     del buf
     return best
+
+
+def launch_floor(torch, qf, dev) -> float:
+    """µs per launch of a graph of 64 back-to-back launches of the library's read probe over 16 KiB (one
+    workgroup): the fixed cost of a dependent kernel launch on this device."""
+    from qwen_fastpath import _lib as L
+    buf = torch.ones(16384, dtype=torch.uint8, device=dev)
+    sink = torch.empty(1, dtype=torch.int32, device=dev)
+    lib = L.load()
+
+    def fn():
+        st = torch.cuda.current_stream().cuda_stream
+        for _ in range(64):
+            L.check(lib.qf_read_probe(buf.data_ptr(), buf.numel(), sink.data_ptr(), 1, st), "probe")
+
+    return time_graph(torch, fn, 64)
 
 
 def time_graph(torch, fn, launches, reps=10):

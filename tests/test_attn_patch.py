@@ -111,3 +111,124 @@ def test_patched_forward_runs_the_kernel(oracle):
                            2, 3, 4, 256 ** -0.5)
     rep = A.check_spec_attn(out.float().cpu().numpy().reshape(6, 24, 256), ref, inp.seq_lens, 3)
     assert rep.ok, rep
+
+
+@pytest.mark.gpu
+def test_unserved_calls_keep_the_original_forward(oracle):
+    """Calls the library would refuse -- a misaligned query, a row stride that is not a multiple of 8
+    elements, a cache whose token stride overflows the kernel's 32-bit stage offsets -- are recognised by
+    spec_attn.supported (the C checks restated) and take the original forward instead of raising."""
+    from oracle import attn as A
+    from qwen_fastpath import spec_attn as S
+
+    class Impl(_Impl):
+        calls = 0
+    P.patch_flash_attention(Impl)
+    dev = torch.device("cuda:0")
+    inp = A.gen_spec_inputs(300, 3, 2, seed=5)
+    kv = torch.from_numpy(inp.kv.view(np.int16)).to(dev).view(torch.bfloat16)
+    md = _md(2, 3, seq_lens=torch.from_numpy(inp.seq_lens).to(dev),
+             block_table=torch.from_numpy(inp.block_table).to(dev))
+    key_cache, value_cache = P._interleaved_kv_split(kv, 256)
+    q = torch.zeros(6, 24 * 256, dtype=torch.bfloat16, device=dev)
+    q3 = q.view(6, 24, 256)
+    assert S.supported(q3, key_cache, 3, 4, value_cache, q3, 2)
+    # misaligned query: a view one element into a larger buffer
+    big = torch.zeros(6 * 24 * 256 + 8, dtype=torch.bfloat16, device=dev)
+    qm = big[1:1 + 6 * 24 * 256].view(6, 24 * 256)
+    assert not S.supported(qm.view(6, 24, 256), key_cache, 3, 4, value_cache, q3, 2)
+    out = torch.zeros(6, 24 * 256, dtype=torch.bfloat16, device=dev)
+    Impl.forward(Impl(), None, qm, None, None, kv, md, out)
+    assert Impl.calls == 1 and torch.all(out == -7)
+    # the same call on an aligned query takes the kernel
+    Impl.forward(Impl(), None, q, None, None, kv, md, out)
+    torch.cuda.synchronize()
+    assert Impl.calls == 1 and not torch.any(out == -7)
+
+
+class _Desc:
+    """A tensor descriptor with the attributes spec_attn.supported reads, standing for a device tensor
+    without allocating one, so each refusal is exercised on the host."""
+
+    def __init__(self, shape, stride=None, ptr=0, dtype=torch.bfloat16):
+        self.shape = tuple(shape)
+        if stride is None:
+            stride, acc = [], 1
+            for n in reversed(self.shape):
+                stride.insert(0, acc)
+                acc *= n
+        self._stride, self._ptr, self.dtype, self.is_cuda = tuple(stride), ptr, dtype, True
+
+    def stride(self, dim=None):
+        return self._stride if dim is None else self._stride[dim]
+
+    def data_ptr(self):
+        return self._ptr
+
+
+def _cache(page=16, hkv=4, d=256, tok_stride=None):
+    # [blocks, PAGE, H_kv, D] view of the interleaved [blocks, H_kv, PAGE, 2D] cache
+    ts = 2 * d if tok_stride is None else tok_stride
+    return _Desc((10, page, hkv, d), (hkv * page * 2 * d, ts, page * 2 * d, 1))
+
+
+@pytest.mark.parametrize("case,expect", [
+    ("served", True),
+    ("misaligned query", False),
+    ("query row stride not a multiple of 8", False),
+    ("fp16 cache", False),
+    ("host tensors", False),
+    ("page of 8 positions", False),
+    ("head size 96", False),
+    ("Q x group rows above 64", False),
+    ("token stride overflows 32-bit stage offsets", False),
+    ("more than 65535 (request, kv head) pairs", False),
+    ("output head geometry differs", False),
+    ("negative stride", False),
+])
+def test_supported_restates_the_library_checks(case, expect):
+    """spec_attn.supported refuses exactly the calls the library's own checks reject, so the patched
+    forward falls back instead of raising; one refusal per case, on host-side descriptors."""
+    from qwen_fastpath import spec_attn as S
+    q = _Desc((6, 24, 256), ptr=4096)
+    kc, vc = _cache(), _cache()
+    o = _Desc((6, 24, 256), ptr=8192)
+    Q, hkv, nreq = 3, 4, 2
+    if case == "misaligned query":
+        q._ptr = 4098
+    elif case == "query row stride not a multiple of 8":
+        q._stride = (24 * 256 + 4, 256, 1)
+    elif case == "fp16 cache":
+        kc.dtype = torch.float16
+    elif case == "host tensors":
+        vc.is_cuda = False
+    elif case == "page of 8 positions":
+        kc, vc = _cache(page=8), _cache(page=8)
+    elif case == "head size 96":
+        q, o = _Desc((6, 24, 96), ptr=4096), _Desc((6, 24, 96), ptr=8192)
+    elif case == "Q x group rows above 64":
+        Q = 11   # 11 x 6 = 66 packed rows
+    elif case == "token stride overflows 32-bit stage offsets":
+        vc = _cache(tok_stride=1 << 25)
+    elif case == "more than 65535 (request, kv head) pairs":
+        nreq = 16384 + 1
+    elif case == "output head geometry differs":
+        o = _Desc((6, 12, 256), ptr=8192)
+    elif case == "negative stride":
+        kc._stride = (-kc._stride[0],) + kc._stride[1:]
+    assert S.supported(q, kc, Q, hkv, vc, o, nreq) is expect, case
+
+
+@pytest.mark.gpu
+def test_w8a8_fallback_predicate_takes_misaligned_weights():
+    """A row-major weight view that is not 16-byte aligned fails _w8a8_hip's predicate and is served by
+    the torch restatement instead of raising from the library."""
+    dev = torch.device("cuda:0")
+    M, N, K = 20, 256, 1024
+    x = torch.randn(M, K, device=dev).to(torch.bfloat16)
+    buf = torch.randint(-127, 128, (N * K + 16,), dtype=torch.int8, device=dev)
+    w = buf[1:1 + N * K].view(N, K).t()  # [K, N] view, stride (1, K), data_ptr % 16 == 1
+    s = torch.rand(N, device=dev) * 0.002 + 1e-4
+    assert w.data_ptr() % 16
+    y = P._w8a8_hip(x, w, s, None, torch.bfloat16)
+    assert torch.equal(y, P.w8a8_reference(x, w, s, None, torch.bfloat16))
