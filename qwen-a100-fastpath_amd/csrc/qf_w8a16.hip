@@ -399,8 +399,20 @@ __global__ void __launch_bounds__(kFoldThreads) argmax_fold_kernel(const uint64_
   }
 }
 
+// Occupancy floor of the MFMA kernel.  One-tile, DEPTH-4 wavefronts fit in 80 VGPRs (the compiler's
+// own choice is 84-92), which allows 6 wavefronts per SIMD instead of 5: three 8-wavefront workgroups
+// per CU where the x slice leaves LDS for three (gate_up 34816x5120 at M = 5, 1088 workgroups, then
+// runs in 1.4 rounds instead of 2.1: 33.05 -> 32.43 us, results unchanged).  Other shapes keep the
+// compiler's allocation: forcing them to 6 wavefronts makes them spill.
+template <int NT, int DEPTH, int WAVES>
+struct MfmaMinWaves {
+  static constexpr int value = (NT == 1 && DEPTH == 4) ? 6 : (WAVES >= 8 ? 2 : 1);
+};
+
 template <int LAYOUT, int NT, int WN, int WK, int DEPTH, bool NTH, bool XRING>
-__global__ void __launch_bounds__(WN * WK * kWave) w8a16_mfma_kernel(const GemmArgs a) {
+__global__ void __launch_bounds__(WN * WK * kWave)
+    __attribute__((amdgpu_waves_per_eu(MfmaMinWaves<NT, DEPTH, WN * WK>::value, 8)))
+    w8a16_mfma_kernel(const GemmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ int last_arrival;
   constexpr int WAVES = WN * WK;

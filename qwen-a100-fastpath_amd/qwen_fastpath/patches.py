@@ -47,8 +47,35 @@ def attn_switch_enabled() -> bool:
 
 def _interleaved_kv_split(kv_cache: torch.Tensor, head_size: int):
     """The layer's cache as the reference reads it (patches.py:59): [blocks, H_kv, PAGE, 2D] with K
-    and V interleaved per row, viewed as two [blocks, PAGE, H_kv, D] tensors."""
+    and V interleaved per row, viewed as two [blocks, PAGE, H_kv, D] tensors.  None for another shape."""
+    if kv_cache is None or kv_cache.dim() != 4 or kv_cache.shape[-1] != 2 * head_size:
+        return None
     return kv_cache.transpose(1, 2).split(head_size, dim=-1)
+
+
+def _stacked_kv_split(kv_cache: torch.Tensor, head_size: int):
+    """A cache of shape [2, blocks, PAGE, H_kv, D] whose memory is laid out as its shape says (K then V,
+    each [blocks][PAGE][H_kv][D]; vLLM's FlashAttention and ROCm AITER FlashAttention backends read it
+    with ``kv_cache.unbind(0)``).  None for another shape."""
+    if kv_cache is None or kv_cache.dim() != 5 or kv_cache.shape[0] != 2 or kv_cache.shape[-1] != head_size:
+        return None
+    return kv_cache.unbind(0)
+
+
+def _paired_kv_split(kv_cache: torch.Tensor, head_size: int):
+    """A cache of shape [blocks, 2, PAGE, H_kv, D] (K and V pages side by side per block; vLLM's Triton
+    attention backend, the default on ROCm, reads it with ``kv_cache.unbind(1)``).  None for another
+    shape."""
+    if kv_cache is None or kv_cache.dim() != 5 or kv_cache.shape[1] != 2 or kv_cache.shape[-1] != head_size:
+        return None
+    return kv_cache.unbind(1)
+
+
+def _flash_attn_kv_split(kv_cache: torch.Tensor, head_size: int):
+    """vLLM's FlashAttention cache: the reference's interleaved 4-D layout, or the stacked 5-D one."""
+    if kv_cache is not None and kv_cache.dim() == 5:
+        return _stacked_kv_split(kv_cache, head_size)
+    return _interleaved_kv_split(kv_cache, head_size)
 
 
 def attn_impl_eligible(impl) -> bool:
@@ -95,7 +122,10 @@ def spec_batch_q_len(md) -> Optional[int]:
 
 def make_attention_forward(orig_forward: Callable, split_kv_cache: Callable = _interleaved_kv_split) -> Callable:
     """Replacement for ``forward(self, layer, query, key, value, kv_cache, attn_metadata, output,
-    output_scale=None, output_block_scale=None)`` of an attention implementation class."""
+    output_scale=None, output_block_scale=None)`` of an attention implementation class.
+    ``split_kv_cache(kv_cache, head_size)`` returns the (key, value) [blocks, PAGE, H_kv, D] views of the
+    layer's cache, or None when the cache is not in the layout it reads (the call then stays on the
+    original forward)."""
     from .spec_attn import gqa_packed_spec_attention, supported
 
     def forward(self, layer, query, key, value, kv_cache, attn_metadata, output,
@@ -104,10 +134,12 @@ def make_attention_forward(orig_forward: Callable, split_kv_cache: Callable = _i
         q_len = spec_batch_q_len(md) if output_scale is None and output_block_scale is None else None
         if q_len is not None and attn_impl_eligible(self):
             num_reqs = md.query_start_loc.shape[0] - 1
-            key_cache, value_cache = split_kv_cache(kv_cache, self.head_size)
-            q3 = query.view(query.shape[0], self.num_heads, self.head_size)
-            o3 = output.view(output.shape[0], self.num_heads, self.head_size)
-            if supported(q3, key_cache, q_len, self.num_kv_heads, value_cache, o3, num_reqs):
+            kv = split_kv_cache(kv_cache, self.head_size) if output is not None else None
+            if kv is not None:
+                key_cache, value_cache = kv
+                q3 = query.view(query.shape[0], self.num_heads, self.head_size)
+                o3 = output.view(output.shape[0], self.num_heads, self.head_size)
+            if kv is not None and supported(q3, key_cache, q_len, self.num_kv_heads, value_cache, o3, num_reqs):
                 gqa_packed_spec_attention(q3, key_cache, value_cache, o3, md.seq_lens, md.block_table,
                                           num_reqs, q_len, self.num_kv_heads, self.scale)
                 return output
@@ -118,31 +150,44 @@ def make_attention_forward(orig_forward: Callable, split_kv_cache: Callable = _i
     return forward
 
 
+# The attention implementations patched by default, each with the adapter that reads its cache layout.
+# FlashAttention is the class the reference patches (patches.py:13); on ROCm vLLM runs Triton attention
+# by default, or AITER FlashAttention when AITER is enabled.  ROCm's paged-attention backend
+# (rocm_attn:RocmAttentionImpl) is not listed: its cache keeps the legacy paged layout under a 5-D shape
+# (each K row cut into 16-byte groups strided by the page, V stored transposed), which the kernel does
+# not read.  An entry may also be a bare "module:Class" string, read with the reference's layout.
 VLLM_ATTENTION_CLASSES = (
-    "vllm.v1.attention.backends.flash_attn:FlashAttentionImpl",
+    ("vllm.v1.attention.backends.flash_attn:FlashAttentionImpl", _flash_attn_kv_split),
+    ("vllm.v1.attention.backends.triton_attn:TritonAttentionImpl", _paired_kv_split),
+    ("vllm.v1.attention.backends.rocm_aiter_fa:AiterFlashAttentionImpl", _stacked_kv_split),
 )
 
 
-def patch_flash_attention(impl_cls=None, split_kv_cache: Callable = _interleaved_kv_split) -> bool:
-    """Install the verification-attention path on ``impl_cls`` (default: vLLM's FlashAttention
-    implementation, as the reference patches, patches.py:10-69).  Idempotent.  ``split_kv_cache(kv_cache,
-    head_size) -> (key_cache, value_cache)`` gives the [blocks, PAGE, H_kv, D] views of the layer's cache
-    (default: the reference's interleaved layout).  Returns False when no class could be patched."""
-    classes = [impl_cls] if impl_cls is not None else []
-    if impl_cls is None:
-        for path in VLLM_ATTENTION_CLASSES:
+def patch_flash_attention(impl_cls=None, split_kv_cache: Optional[Callable] = None) -> bool:
+    """Install the verification-attention path on ``impl_cls``, or by default on every class of
+    VLLM_ATTENTION_CLASSES that imports (the reference patches vLLM's FlashAttention implementation,
+    patches.py:10-69).  Idempotent.  ``split_kv_cache(kv_cache, head_size) -> (key_cache, value_cache) or
+    None`` gives the [blocks, PAGE, H_kv, D] views of the layer's cache (default for an explicit class:
+    the reference's interleaved layout).  Returns False when no class could be patched."""
+    classes = []
+    if impl_cls is not None:
+        classes.append((impl_cls, split_kv_cache or _interleaved_kv_split))
+    else:
+        for entry in VLLM_ATTENTION_CLASSES:
+            path, adapter = (entry, _interleaved_kv_split) if isinstance(entry, str) else entry
             try:
-                classes.append(_import_attr(path))
-            except (ImportError, AttributeError):
+                classes.append((_import_attr(path), split_kv_cache or adapter))
+            except (ImportError, AttributeError, RuntimeError, OSError) as e:  # backend absent on this platform
+                logger.debug("qwen_fastpath: %s not patched: %s", path, e)
                 continue
     if not classes:
         logger.info("qwen_fastpath: vLLM attention implementation not found; split-KV attention available as "
                     "qwen_fastpath.gqa_packed_spec_attention only")
         return False
-    for cls in classes:
+    for cls, adapter in classes:
         orig = cls.forward
         if not getattr(orig, "_qwen_fastpath", False):
-            cls.forward = make_attention_forward(orig, split_kv_cache)
+            cls.forward = make_attention_forward(orig, adapter)
     logger.info("qwen_fastpath: split-KV GQA-packed attention enabled for speculative-decode verification")
     return True
 

@@ -34,7 +34,8 @@ class _Impl:
     def forward(self, layer, query, key, value, kv_cache, attn_metadata, output, output_scale=None,
                 output_block_scale=None):
         type(self).calls += 1
-        output.fill_(-7.0)
+        if output is not None:
+            output.fill_(-7.0)
         return output
 
 
@@ -232,3 +233,118 @@ def test_w8a8_fallback_predicate_takes_misaligned_weights():
     assert w.data_ptr() % 16
     y = P._w8a8_hip(x, w, s, None, torch.bfloat16)
     assert torch.equal(y, P.w8a8_reference(x, w, s, None, torch.bfloat16))
+
+
+def _kv_layouts(nblk=3, page=16, hkv=2, d=64):
+    """One cache's contents in the three layouts: K[b, t, h, :] = 1000 b + 10 t + h + d-index / 1000 and
+    V the same, negated."""
+    b = torch.arange(nblk).view(-1, 1, 1, 1).float()
+    t = torch.arange(page).view(1, -1, 1, 1).float()
+    h = torch.arange(hkv).view(1, 1, -1, 1).float()
+    e = torch.arange(d).view(1, 1, 1, -1).float()
+    K = 1000 * b + 10 * t + h + e / 1000
+    V = -K
+    inter = torch.cat([K, V], dim=-1).transpose(1, 2).contiguous()   # [blocks, H_kv, PAGE, 2D]
+    stacked = torch.stack([K, V]).contiguous()                       # [2, blocks, PAGE, H_kv, D]
+    paired = torch.stack([K, V], dim=1).contiguous()                 # [blocks, 2, PAGE, H_kv, D]
+    return K, V, inter, stacked, paired
+
+
+def test_cache_layout_adapters():
+    K, V, inter, stacked, paired = _kv_layouts()
+    for fn, cache in ((P._interleaved_kv_split, inter), (P._stacked_kv_split, stacked),
+                      (P._paired_kv_split, paired), (P._flash_attn_kv_split, inter),
+                      (P._flash_attn_kv_split, stacked)):
+        k, v = fn(cache, 64)
+        assert k.shape == K.shape and torch.equal(k, K) and torch.equal(v, V), fn.__name__
+        assert k.data_ptr() >= cache.data_ptr() and k.stride(-1) == 1  # views of the cache, no copy
+    # a cache in another layout (or head size) is declined, so the call keeps the original forward
+    assert P._interleaved_kv_split(stacked, 64) is None and P._interleaved_kv_split(inter, 128) is None
+    assert P._stacked_kv_split(inter, 64) is None and P._stacked_kv_split(paired, 64) is None
+    assert P._paired_kv_split(stacked, 64) is None and P._paired_kv_split(inter, 64) is None
+    assert P._stacked_kv_split(None, 64) is None
+
+
+def test_default_classes_each_with_its_adapter(monkeypatch):
+    """Every class of VLLM_ATTENTION_CLASSES that imports is patched with its own adapter; a bare string
+    entry reads the reference's layout; classes that do not import are skipped."""
+    import sys
+    mod = types.ModuleType("qf_standin_attn_backends")
+
+    class FA(_Impl):
+        calls = 0
+
+    class Triton(_Impl):
+        calls = 0
+
+    class Legacy(_Impl):
+        calls = 0
+
+    mod.FA, mod.Triton, mod.Legacy = FA, Triton, Legacy
+    monkeypatch.setitem(sys.modules, "qf_standin_attn_backends", mod)
+    seen = []
+
+    def spy(name, fn):
+        def adapter(kv_cache, head_size):
+            seen.append(name)
+            return fn(kv_cache, head_size)
+        return adapter
+
+    monkeypatch.setattr(P, "VLLM_ATTENTION_CLASSES", (
+        ("qf_standin_attn_backends:FA", spy("fa", P._flash_attn_kv_split)),
+        ("qf_standin_attn_backends:Triton", spy("triton", P._paired_kv_split)),
+        "qf_standin_attn_backends:Legacy",
+        ("qf_standin_attn_backends:Missing", P._stacked_kv_split),
+        ("qf_no_such_module:X", P._stacked_kv_split),
+    ))
+    assert P.patch_flash_attention()
+    for cls in (FA, Triton, Legacy):
+        assert getattr(cls.forward, "_qwen_fastpath", False)
+    f = Triton.forward
+    assert P.patch_flash_attention() and Triton.forward is f
+    # host tensors never take the kernel: each call reaches its adapter, then the original forward
+    _, _, inter, stacked, paired = _kv_layouts(page=16, hkv=4, d=256)
+    out = torch.zeros(6, 24 * 256)
+    for cls, cache in ((FA, stacked), (Triton, paired)):
+        cls.forward(cls(), None, torch.zeros(6, 24 * 256), None, None, cache, _md(2, 3), out)
+        assert cls.calls == 1 and torch.all(out == -7)
+    assert seen == ["fa", "triton"]
+    # no output buffer: the original forward, without reading the cache
+    Triton.forward(Triton(), None, torch.zeros(6, 24 * 256), None, None, paired, _md(2, 3), None)
+    assert Triton.calls == 2 and seen == ["fa", "triton"]
+
+
+@pytest.mark.gpu
+def test_patched_forward_on_each_cache_layout(oracle):
+    """The same batch through the patched forward with the cache in the reference's interleaved layout,
+    the stacked [2, blocks, PAGE, H_kv, D] layout and the paired [blocks, 2, PAGE, H_kv, D] layout: all
+    three take the kernel, give the same bits, and pass the oracle."""
+    from oracle import attn as A
+
+    inp = A.gen_spec_inputs(2000, 3, 2, seed=6)
+    dev = torch.device("cuda:0")
+    kv = torch.from_numpy(inp.kv.view(np.int16)).to(dev).view(torch.bfloat16)   # [blocks, H_kv, PAGE, 2D]
+    K = kv[..., :256].transpose(1, 2)
+    V = kv[..., 256:].transpose(1, 2)
+    caches = {"interleaved": (kv, P._flash_attn_kv_split),
+              "stacked": (torch.stack([K, V]).contiguous(), P._stacked_kv_split),
+              "paired": (torch.stack([K, V], dim=1).contiguous(), P._paired_kv_split)}
+    q = torch.from_numpy(inp.q.view(np.int16)).to(dev).view(torch.bfloat16).reshape(6, 24 * 256)
+    md = _md(2, 3, seq_lens=torch.from_numpy(inp.seq_lens).to(dev),
+             block_table=torch.from_numpy(inp.block_table).to(dev))
+    ref = A.spec_attention(inp.query(), inp.key_cache(), inp.value_cache(), inp.seq_lens, inp.block_table,
+                           2, 3, 4, 256 ** -0.5)
+    outs = {}
+    for name, (cache, adapter) in caches.items():
+        class Impl(_Impl):
+            calls = 0
+        P.patch_flash_attention(Impl, adapter)
+        out = torch.full_like(q, float("nan"))
+        Impl.forward(Impl(), None, q, None, None, cache, md, out)
+        torch.cuda.synchronize()
+        assert Impl.calls == 0, name
+        rep = A.check_spec_attn(out.float().cpu().numpy().reshape(6, 24, 256), ref, inp.seq_lens, 3)
+        print(f"{name}: {rep}", flush=True)
+        assert rep.ok, (name, rep)
+        outs[name] = out
+    assert torch.equal(outs["stacked"], outs["interleaved"]) and torch.equal(outs["paired"], outs["interleaved"])
