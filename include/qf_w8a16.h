@@ -78,8 +78,11 @@ typedef enum qf_kernel {
                                launch; k_waves must be 1, split_k > 1 needs the workspace;
                                tiles_per_wave 1 or 2 with 4 or 8 waves at depth 4 or 8, or 4 tiles
                                with 4 waves at depth 2 */
-  QF_KERNEL_MFMA_W8A8 = 5   /* qf_w8a8_gemm only: the same tiling on v_mfma_i32_16x16x64_i8 with int8
+  QF_KERNEL_MFMA_W8A8 = 5,  /* qf_w8a8_gemm only: the same tiling on v_mfma_i32_16x16x64_i8 with int8
                                activations; tiles_per_wave 2 or 4, 4 or 8 waves, depth 2 or 4 */
+  QF_KERNEL_MFMA_W8A8_TILE = 6 /* qf_w8a8_gemm only, either layout, picked for large M x N: 256-channel x
+                               256-token workgroups, both operands staged in LDS by direct-to-LDS copies
+                               through a 4-stage ring; waves 8, tiles_per_wave 8, depth 4, split_k 1 */
 } qf_kernel;
 
 /* Launch configuration.  A zero field means "choose automatically". */
@@ -213,9 +216,10 @@ int qf_quantize_tokens_int8(const uint16_t* x, int64_t ldx, int M, int K, int8_t
 
 /* y[m, n] = out_dtype( (float(sum_k xq[m,k] * w[n,k]) * s_a[m]) * scale[n] ), the integer sums exact in
  * int32 (K < 132000).  w is the TILED image (ldw ignored) or row-major int8 [N, K] with row stride ldw >= K
- * bytes, ldw % 16 == 0 (the row-major layout runs the automatic shape only: 2 tiles, 8 waves, depth 4);
+ * bytes, ldw % 16 == 0 (the row-major layout runs QF_KERNEL_MFMA_W8A8_TILE or the automatic
+ * QF_KERNEL_MFMA_W8A8 shape only: 2 tiles, 8 waves, depth 4);
  * xq / s_a as written by qf_quantize_tokens_int8 (xq 16-byte aligned, ldq % 16 == 0); any M >= 1.
- * cfg may be NULL (automatic); its kernel must be QF_KERNEL_MFMA_W8A8 or AUTO.  Workspace
+ * cfg may be NULL (automatic); its kernel must be QF_KERNEL_MFMA_W8A8, QF_KERNEL_MFMA_W8A8_TILE or AUTO.  Workspace
  * (qf_w8a8_workspace_bytes, 0 without a K split): the int32 split partials after the counter prefix, which
  * this path does not use; calls that may run at the same time need distinct workspaces.
  * Reference: ops.cutlass_scaled_mm(x_q, w_q, scale_a, scale_b, out_dtype, bias=None) at

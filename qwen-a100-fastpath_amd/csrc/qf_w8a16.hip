@@ -1130,6 +1130,213 @@ __global__ void __launch_bounds__(WN * kWave) w8a8_wide_kernel(const GemmArgs a)
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// W8A8 LDS-tiled kernel (QF_KERNEL_MFMA_W8A8_TILE): large M, either weight layout.
+//
+// A workgroup of 8 wavefronts owns a 256-channel x 256-token output tile over the whole K range.  Each
+// 64-k step stages 32 fragments of 1 KiB in LDS: the 16 weight tiles (16 channels x 64 k: the TILED
+// block as stored, or on row-major weights lane (g, r) reading row r, bytes 16 g .. 16 g + 15 of the
+// step) and the 16 activation tiles of 16 tokens (lane (g, r): token r, k 16 g .. 16 g + 15).  Each is
+// copied global -> LDS with one 16-byte-per-lane direct-to-LDS load, lane l's bytes landing at 16 l, so
+// a fragment read is one conflict-free ds_read_b128 and no VGPR holds staged data.  The stages go
+// through a ring of kW8A8TileStages slots; each iteration waits for its own copies of the next stage,
+// meets the other wavefronts at one barrier, refills the slot all of them finished reading, reads the
+// next step's 12 fragments and runs this step's 32 MFMAs.
+// Wavefront (wn, wm) = (wave & 1, wave >> 1) computes channels 128 wn .. +127 and tokens 64 wm .. +63:
+// 8 weight fragments (the A operand of v_mfma_i32_16x16x64_i8) by 4 activation fragments (B), 128
+// int32 accumulators.  Integer sums are exact in any order, so results equal the other W8A8 kernels'.
+// Per step and CU: 32 KiB copied, 96 KiB of fragment reads, 256 MFMAs (measured best of 3, 4 and 5
+// stages at 4; 3 leaves the copies exposed).
+// The bf16 epilogue stages each wavefront's 64 x 128 block in its own 16 KiB of LDS and stores whole
+// 256-byte row pieces (the MFMA layout alone would store 16 rows x 32 bytes per instruction: gate_up
+// M = 2048 406 -> 379 us); fp32 output or rows without 16-byte alignment store from the registers.
+// ---------------------------------------------------------------------------------------------
+typedef const void __attribute__((address_space(1)))* glb_ptr_t;
+typedef void __attribute__((address_space(3)))* lds_ptr_t;
+
+constexpr int kW8A8TileStages = 4;
+constexpr int kW8A8TileRows = 256;                        // tokens per workgroup
+constexpr int kW8A8TileTiles = 16;                        // 16-channel weight tiles per workgroup
+constexpr int kW8A8TileStageBytes = 32 * 1024;            // 16 weight + 16 activation fragments
+constexpr int kW8A8TileLds = kW8A8TileStages * kW8A8TileStageBytes;
+
+// s_waitcnt with vmcnt = n (0..63) and the other counters unconstrained.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+template <int LAYOUT>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+    w8a8_tile_kernel(const GemmArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  constexpr int S = kW8A8TileStages;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wn = wave & 1, wm = wave >> 1;
+  const int g = lane >> 4, r = lane & 15;
+  const int ntiles = a.n_pad / kTileN;
+  const int mblocks = (a.M + kW8A8TileRows - 1) / kW8A8TileRows;
+  // The hardware hands workgroup i to XCD i % kXcds; consecutive logical blocks share an XCD, so the
+  // token blocks of one channel block run together and share its weights in that XCD's L2.
+  int l;
+  {
+    const int total = gridDim.x;
+    const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+    const int per = total / kXcds, rem = total % kXcds;
+    l = xcd < rem ? xcd * (per + 1) + j : rem * (per + 1) + (xcd - rem) * per + j;
+  }
+  const int tile0 = (l / mblocks) * kW8A8TileTiles;
+  const int m0 = (l % mblocks) * kW8A8TileRows;
+  const int ksteps = a.ksteps;
+
+  // Wavefronts 0..3 copy the weight fragments 4 wave .. 4 wave + 3, wavefronts 4..7 the activation
+  // fragments 4 (wave - 4) .. + 3.  Channels and tokens past the matrix read its last row instead; their
+  // outputs are never stored.
+  const int8_t* src[4];
+  int64_t adv;  // bytes between the same fragment of consecutive steps
+  if (wave < 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = min(tile0 + 4 * wave + j, ntiles - 1);
+      if constexpr (LAYOUT == QF_LAYOUT_ROWMAJOR) {
+        src[j] = a.w + (int64_t)min(t * kTileN + r, a.N - 1) * a.ldw + 16 * g;
+      } else {
+        src[j] = a.w + ((int64_t)t * ksteps * kWave + lane) * 16;
+      }
+    }
+    adv = LAYOUT == QF_LAYOUT_ROWMAJOR ? kStepK : kTileN * kStepK;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = min(m0 + 16 * (4 * (wave - 4) + j) + r, a.M - 1);
+      src[j] = a.xq + (int64_t)row * a.ldx + 16 * g;
+    }
+    adv = kStepK;
+  }
+  // Copy group s: stage min(s, ksteps - 1) into slot s % S.  Groups past the last stage copy it again
+  // into a slot whose stage every wavefront has consumed, so every iteration issues exactly one group
+  // and the vmcnt waits are constants.
+  auto copy = [&](int s) {
+    uint8_t* slot = smem + (s % S) * kW8A8TileStageBytes + wave * 4 * 1024;
+    const int64_t off = (int64_t)min(s, ksteps - 1) * adv;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_global_load_lds((glb_ptr_t)(src[j] + off), (lds_ptr_t)(slot + j * 1024), 16, 0, 0);
+  };
+  auto read_frags = [&](int s, i32x4_t (&A)[8], i32x4_t (&B)[4]) {
+    const uint8_t* slot = smem + (s % S) * kW8A8TileStageBytes + lane * 16;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) A[i] = *reinterpret_cast<const i32x4_t*>(slot + (8 * wn + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) B[i] = *reinterpret_cast<const i32x4_t*>(slot + (16 + 4 * wm + i) * 1024);
+  };
+  // The ring barrier: every wavefront has waited for its own copies of the stage before it; the acquire
+  // keeps the stage's reads after it.  (A release fence would wait for the copies still in flight, which
+  // count as LDS writes.)
+  auto ring_barrier = []() {
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  };
+
+  i32x4_t acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = (i32x4_t){0, 0, 0, 0};
+
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s) copy(s);
+  wait_vmcnt<4 * (S - 2)>();  // groups 1 .. S - 2 may still be in flight: stage 0 has landed
+  ring_barrier();
+  i32x4_t fa[8], fb[4], ga[8], gb[4];
+  read_frags(0, fa, fb);
+  // Step s: stage s + 1 becomes readable at the barrier (S - 3 groups were issued after its group), the
+  // slot of stage s - 1 is refilled with group s + S - 1, the fragments of step s + 1 are read into
+  // (na, nb) while the MFMAs of step s run on (ca, cb).  Unrolled by two so the fragment sets alternate
+  // without copies.
+  auto step = [&](int s, i32x4_t (&ca)[8], i32x4_t (&cb)[4], i32x4_t (&na)[8], i32x4_t (&nb)[4]) {
+    wait_vmcnt<4 * (S - 3)>();
+    ring_barrier();
+    copy(s + S - 1);
+    read_frags(min(s + 1, ksteps - 1), na, nb);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ca[i], cb[j], acc[i][j], 0, 0, 0);
+  };
+  int s = 0;
+  for (; s + 1 < ksteps; s += 2) {
+    step(s, fa, fb, ga, gb);
+    step(s + 1, ga, gb, fa, fb);
+  }
+  if (s < ksteps) step(s, fa, fb, ga, gb);
+  wait_vmcnt<0>();  // the last groups' copies have landed before LDS is reused or released
+
+  // Lane (g, r) holds C[n = 16 (tile0 + 8 wn + i) + 4 g + e][m = m0 + 64 wm + 16 j + r], e = 0..3.
+  const bool staged = !a.out_f32 && a.vec_out && (a.ldy % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
+  if (staged) {
+    // Each wavefront's 64 x 128 bf16 block goes to its own 16 KiB of LDS: row t, 16-byte chunk c at
+    // t * 256 + ((c ^ (t & 15)) << 4), so the 8-byte writes and the 16-byte reads are conflict-free.
+    __syncthreads();  // every wavefront is done with the ring
+    uint8_t* blk = smem + wave * 16384;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int n = (tile0 + 8 * wn + i) * kTileN + 4 * g;
+      const f32x4_t sc = load_scale4(a.scale, a.N, min(n, a.n_pad - 4));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = 16 * j + r;
+        const float st = a.s_tok[min(m0 + 64 * wm + t, a.M - 1)];
+        const i32x4_t v = acc[i][j];
+        const f32x4_t f = {(float)v.x, (float)v.y, (float)v.z, (float)v.w};
+        const f32x4_t o = (f * st) * sc;
+        u32x2_t p;
+        p.x = pack_bf16_rne(o.x, o.y);
+        p.y = pack_bf16_rne(o.z, o.w);
+        const int c = 2 * i + (g >> 1);
+        *reinterpret_cast<u32x2_t*>(blk + t * 256 + ((c ^ (t & 15)) << 4) + 8 * (g & 1)) = p;
+      }
+    }
+    const int c = lane & 15;
+    const int n0 = (tile0 + 8 * wn) * kTileN + 8 * c;  // the first of this lane's 8 channels
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int t = 4 * q + (lane >> 4);
+      const int m = m0 + 64 * wm + t;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(blk + t * 256 + ((c ^ (t & 15)) << 4));
+      if (m < a.M) {
+        uint16_t* row = reinterpret_cast<uint16_t*>(a.y) + (int64_t)m * a.ldy + n0;
+        if (n0 + 8 <= a.N) {
+          *reinterpret_cast<u32x4_t*>(row) = v;
+        } else if (n0 < a.N) {
+          const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
+          for (int k = 0; k < a.N - n0; ++k) row[k] = e[k];
+        }
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int tile = tile0 + 8 * wn + i;
+    const int n = tile * kTileN + 4 * g;
+    if (tile < ntiles && n < a.N) {
+      const f32x4_t sc = load_scale4(a.scale, a.N, n);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = m0 + 64 * wm + 16 * j + r;
+        if (m < a.M) {
+          const i32x4_t v = acc[i][j];
+          const f32x4_t f = {(float)v.x, (float)v.y, (float)v.z, (float)v.w};
+          store_out4(a.y, a.ldy, a.out_f32, a.vec_out, m, n, min(4, a.N - n), (f * a.s_tok[m]) * sc);
+        }
+      }
+    }
+  }
+}
+
 // Sum of the W8A8 kernel's int32 split partials (exact in any order), then the scales.
 __global__ void __launch_bounds__(256) splitk_reduce_w8a8_kernel(const GemmArgs a) {
   const int groups = a.n_pad / 4;
@@ -2277,8 +2484,19 @@ size_t w8a8_lds_bytes(const qf_w8a16_config& c, int M, int N) {
   return (size_t)2 * rows * ((c.depth + 1) * kStepK + 16);
 }
 
+// The tile kernel's grid: 256-channel x 256-token workgroups.
+int64_t w8a8_tile_workgroups(int M, int N) {
+  return (int64_t)ceil_div(round_up16(N) / kTileN, kW8A8TileTiles) * ceil_div(M, kW8A8TileRows);
+}
+
 int validate_w8a8(int M, int N, int K, int layout, const qf_w8a16_config& c) {
   const int ksteps = K / kStepK;
+  if (c.kernel == QF_KERNEL_MFMA_W8A8_TILE) {
+    if (c.split_k != 1 || c.waves != 8 || c.tiles_per_wave != 8 || c.depth != kW8A8TileStages || c.k_waves != 1)
+      return QF_ERR_INVALID_ARG;
+    if ((layout != QF_LAYOUT_TILED && layout != QF_LAYOUT_ROWMAJOR) || K >= 132000) return QF_ERR_UNSUPPORTED;
+    return w8a8_tile_workgroups(M, N) > 0x7fffffff ? QF_ERR_UNSUPPORTED : QF_OK;
+  }
   if (c.kernel != QF_KERNEL_MFMA_W8A8) return QF_ERR_INVALID_ARG;
   if (c.split_k < 1 || c.split_k > ksteps || c.waves < 1 || c.k_waves < 1 || c.tiles_per_wave < 1)
     return QF_ERR_INVALID_ARG;
@@ -2308,6 +2526,22 @@ bool auto_config_w8a8(int M, int N, int K, int layout, qf_w8a16_config* c) {
   c->tiles_per_wave = 2;
   c->waves = 8;
   c->depth = 4;
+  // The LDS-tiled kernel once its 256 x 256 workgroups number 136 or more, unless they spill a few
+  // (<= 32) past a whole round of 256 (measured on the four layer shapes at M = 256 .. 4096: 10-33%
+  // faster there, e.g. gate_up M = 2048 377 against 420 us, down M = 2048 173 against 238 us; slower
+  // with fewer workgroups, where the shapes below split K, and at 272 workgroups, gate_up M = 512
+  // 152 against 137 us).  Its token blocks are 256 rows whatever M is, so it also needs M >= 256 with
+  // at most a quarter of the rows it computes past M.
+  const int64_t twgs = w8a8_tile_workgroups(M, N);
+  const int64_t tile_rows = (int64_t)ceil_div(M, kW8A8TileRows) * kW8A8TileRows;
+  if (K < 132000 && M >= kW8A8TileRows && 4 * (int64_t)M >= 3 * tile_rows && twgs >= 136 &&
+      !(twgs > 256 && twgs % 256 != 0 && twgs % 256 <= 32)) {
+    c->kernel = QF_KERNEL_MFMA_W8A8_TILE;
+    c->tiles_per_wave = 8;
+    c->waves = 8;
+    c->depth = kW8A8TileStages;
+    return validate_w8a8(M, N, K, layout, *c) == QF_OK;
+  }
   int groups, rows;
   w8a8_groups(*c, M, N, groups, rows);
   const int64_t wgs = (int64_t)workgroups(*c, N) * groups;
@@ -2337,10 +2571,11 @@ int resolve_w8a8(int M, int N, int K, int layout, const qf_w8a16_config* in, qf_
   if (!auto_config_w8a8(M, N, K, layout, out)) return QF_ERR_UNSUPPORTED;
   if (in == nullptr || in->kernel == QF_KERNEL_AUTO) return QF_OK;
   qf_w8a16_config c = *in;
-  if (c.waves == 0) c.waves = 4;
+  const bool tile = c.kernel == QF_KERNEL_MFMA_W8A8_TILE;
+  if (c.waves == 0) c.waves = tile ? 8 : 4;
   if (c.k_waves == 0) c.k_waves = 1;
-  if (c.tiles_per_wave == 0) c.tiles_per_wave = 4;
-  if (c.depth == 0) c.depth = 4;
+  if (c.tiles_per_wave == 0) c.tiles_per_wave = tile ? 8 : 4;
+  if (c.depth == 0) c.depth = tile ? kW8A8TileStages : 4;
   if (c.split_k == 0) c.split_k = 1;
   const int rc = validate_w8a8(M, N, K, layout, c);
   if (rc != QF_OK) return rc;
@@ -2383,10 +2618,14 @@ int run_w8a8(const int8_t* xq, int64_t ldq, const float* s_a, const int8_t* w, i
   a.split_k = c.split_k;
   a.out_f32 = out_dtype == QF_DTYPE_F32;
   a.vec_out = (ldy % 4) == 0;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (c.kernel == QF_KERNEL_MFMA_W8A8_TILE) {
+    KernelFn tf = layout == QF_LAYOUT_ROWMAJOR ? &w8a8_tile_kernel<QF_LAYOUT_ROWMAJOR> : &w8a8_tile_kernel<QF_LAYOUT_TILED>;
+    return launch(tf, dim3((unsigned)w8a8_tile_workgroups(M, N)), dim3(8 * kWave), kW8A8TileLds, s, a);
+  }
   w8a8_groups(c, M, N, a.groups, a.group_rows);
   KernelFn fn = select_w8a8(layout, c.tiles_per_wave, a.group_rows / 16, c.waves, c.depth);
   if (fn == nullptr) return QF_ERR_UNSUPPORTED;
-  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   int st = launch(fn, dim3(workgroups(c, N) * a.groups * c.split_k), dim3(c.waves * kWave), w8a8_lds_bytes(c, M, N),
                   s, a);
   if (st != QF_OK || c.split_k == 1) return st;

@@ -30,6 +30,7 @@ KERNEL_MFMA = 2
 KERNEL_MFMA_XRING = 3
 KERNEL_MFMA_WIDE = 4
 KERNEL_MFMA_W8A8 = 5
+KERNEL_MFMA_W8A8_TILE = 6
 
 MAX_M = 16
 K_ALIGN = 64

@@ -30,7 +30,8 @@ class W8A16Config(NamedTuple):
     """Launch configuration; zero fields are chosen by the library for the call's M (see
     qf_w8a16_pick_config).  kernel: 0 auto, 1 gemv (M <= 4), 2 mfma, 3 mfma with x staged in
     chunks through a two-slot LDS ring (k_waves 1), 4 the wide-M mfma kernel (TILED weights, any M;
-    k_waves and split_k 1).  waves = wavefronts per workgroup, of which
+    k_waves and split_k 1); w8a8_mm only: 5 the int8 wide-M kernel, 6 the int8 LDS-tiled kernel (256 x
+    256 workgroups; waves 8, tiles_per_wave 8, depth 4, split_k 1).  waves = wavefronts per workgroup, of which
     k_waves split K inside the workgroup (MFMA); reduce (MFMA, split_k > 1):
     0 = the last workgroup of each n-block sums the splits, 1 = a second kernel does."""
 

@@ -258,19 +258,35 @@ def test_w8a8_configs_host_only():
     lib = L.load()
     for M in (1, 17, 64, 300, 2048):
         for (N, K) in ((34816, 5120), (5120, 17408), (1000, 1024), (16, 64)):
-            c = L.w8a8_pick_config(M, N, K)
-            assert c is not None and c.kernel == L.KERNEL_MFMA_W8A8 and c.k_waves == 1, (M, N, K)
-            cr = L.w8a8_pick_config(M, N, K, 0)  # row-major weights: the automatic shape
-            assert cr is not None and cr.to_tuple()[2:5] == (2, 8, 4), (M, N, K)
+            tile = M == 2048 and N >= 5120  # 1088 and 160 workgroups of 256 x 256
+            for layout in (1, 0):  # TILED, row-major (the automatic 2-tile shape or the tile kernel)
+                c = L.w8a8_pick_config(M, N, K, layout)
+                assert c is not None and c.k_waves == 1, (M, N, K, layout)
+                if tile:
+                    assert c.to_tuple()[:5] == (L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 4), (M, N, K, layout)
+                else:
+                    assert c.kernel == L.KERNEL_MFMA_W8A8, (M, N, K, layout)
+                    if layout == 0:
+                        assert c.to_tuple()[2:5] == (2, 8, 4), (M, N, K)
+    # The tile kernel's rule: 136 or more workgroups, not just past a whole round, M >= 256 with at most
+    # a quarter of the computed rows past M.
+    assert L.w8a8_pick_config(256, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8_TILE      # 136 workgroups
+    assert L.w8a8_pick_config(255, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8           # M < 256
+    assert L.w8a8_pick_config(512, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8           # 272 = 256 + 16
+    assert L.w8a8_pick_config(768, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8_TILE      # 408
+    assert L.w8a8_pick_config(513, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8           # 513 of 768 rows
+    assert L.w8a8_pick_config(600, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8_TILE      # 600 of 768 rows
+    assert L.w8a8_pick_config(1024, 10240, 5120).kernel == L.KERNEL_MFMA_W8A8_TILE     # 160
+    assert L.w8a8_pick_config(1536, 5120, 8192).kernel == L.KERNEL_MFMA_W8A8           # 120
     # The automatic rule's two exceptions: 4-wavefront workgroups, unsplit, where 8-wavefront ones
     # would be under 128 (TILED only), and a split in two for a long K whose last round of 128-row
     # workgroups would leave the CUs at most a quarter busy.
     assert L.w8a8_pick_config(128, 10240, 5120).to_tuple()[1:5] == (1, 2, 4, 4)
     assert L.w8a8_pick_config(128, 10240, 5120, 0).to_tuple()[1:5] == (2, 2, 8, 4)
     assert L.w8a8_pick_config(256, 5120, 8192).to_tuple()[1:5] == (1, 2, 4, 4)
-    assert L.w8a8_pick_config(2048, 5120, 17408).to_tuple()[1:5] == (2, 2, 8, 4)
+    assert L.w8a8_pick_config(2304, 3840, 17408).to_tuple()[1:5] == (2, 2, 8, 4)
     assert L.w8a8_pick_config(1024, 5120, 17408).to_tuple()[1:5] == (1, 2, 8, 4)
-    assert L.w8a8_pick_config(2048, 34816, 5120).to_tuple()[1:5] == (1, 2, 8, 4)
+    assert L.w8a8_pick_config(2048, 3072, 5120).to_tuple()[1:5] == (1, 2, 8, 4)
     fake = 1 << 20
     def call(layout=1, cfg=None, M=40, K=1024, ldq=1024):
         return lib.qf_w8a8_gemm(fake, ldq, fake, fake, 0, layout, fake, fake, 1000, 0, M, 1000, K,
@@ -283,7 +299,9 @@ def test_w8a8_configs_host_only():
     assert call(ldq=1024 + 8) == L.ERR_UNSUPPORTED                          # ldq % 16
     assert call(M=0) == L.ERR_INVALID_ARG
     for bad in ((L.KERNEL_MFMA_W8A8, 1, 1, 8, 4, 1, 1, 0), (L.KERNEL_MFMA_W8A8, 1, 2, 8, 8, 1, 1, 0),
-                (L.KERNEL_MFMA_W8A8, 1, 2, 16, 4, 1, 1, 0), (L.KERNEL_MFMA_WIDE, 1, 2, 8, 4, 1, 1, 0)):
+                (L.KERNEL_MFMA_W8A8, 1, 2, 16, 4, 1, 1, 0), (L.KERNEL_MFMA_WIDE, 1, 2, 8, 4, 1, 1, 0),
+                (L.KERNEL_MFMA_W8A8_TILE, 2, 8, 8, 4, 1, 1, 0), (L.KERNEL_MFMA_W8A8_TILE, 1, 8, 4, 4, 1, 1, 0),
+                (L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 3, 1, 1, 0), (L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 4, 1, 2, 0)):
         assert call(cfg=L.Config.from_seq(bad)) != L.OK, bad
     split = L.Config.from_seq((L.KERNEL_MFMA_W8A8, 2, 2, 8, 4, 1, 1, 1))
     assert call(cfg=split) == L.ERR_WORKSPACE

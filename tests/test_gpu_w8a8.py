@@ -105,14 +105,18 @@ def w8a8_group_rows(cfg, M, N):
 
 
 @pytest.mark.parametrize("name,M,N,K,rows", [
-    ("qkv", 128, 10240, 5120, 64), ("o_proj", 256, 5120, 8192, 64), ("down", 2048, 5120, 17408, 128),
+    ("qkv", 128, 10240, 5120, 64), ("o_proj", 256, 5120, 8192, 64), ("split2", 2304, 3840, 17408, 128),
     # 4-wavefront workgroups with token groups of more than 64 rows (5 to 8 token tiles a fragment)
     ("qkv", 160, 10240, 5120, 80), ("qkv", 192, 10240, 5120, 96), ("n1280", 1600, 1280, 5120, 128)])
 def test_w8a8_auto_exceptions(name, M, N, K, rows):
     """The automatic rule's exceptions (4-wavefront unsplit workgroups, also with 80- to 128-row token
-    groups; a split in two on down at M = 2048) against the restatement, on both layouts."""
+    groups; a split in two for a long K whose last round of 128-row workgroups is nearly empty) against
+    the restatement, on both layouts."""
     cfg = L.w8a8_pick_config(M, N, K)
-    if name != "down":
+    assert cfg.kernel == L.KERNEL_MFMA_W8A8, cfg.to_tuple()
+    if name == "split2":
+        assert cfg.split_k == 2, cfg.to_tuple()
+    else:
         assert cfg.waves == 4 and cfg.split_k == 1, cfg.to_tuple()
     assert w8a8_group_rows(cfg, M, N) == rows, cfg.to_tuple()
     x, w, s = random_case(M, N, K, M + N)
@@ -222,3 +226,78 @@ def test_rowmajor_m17_dispatch_uses_the_int8_kernel(oracle, monkeypatch):
         assert np.array_equal(bf16_bits(y), oracle.w8a8_linear(inp.x, inp.w, inp.s))
     finally:
         P._fallback_impl = None
+
+
+TILE_CFG = (L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 4, 1, 1, 1)
+
+
+def w8a8_into(x, w, s, layout, ldw, y, out_dtype, cfg):
+    """qf_w8a8_gemm into a caller's output y [M, ldy] (row stride ldy >= N), through the C ABI."""
+    import ctypes
+    lib = L.load()
+    M, K = x.shape
+    N = s.numel()
+    xq, s_a = qf.quantize_tokens_int8(x)
+    c = L.Config.from_seq(cfg)
+    dt = L.DTYPE_BF16 if out_dtype == torch.bfloat16 else L.DTYPE_F32
+    assert int(lib.qf_w8a8_workspace_bytes(M, N, K, layout, ctypes.byref(c))) == 0
+    rc = lib.qf_w8a8_gemm(xq.data_ptr(), K, s_a.data_ptr(), w.data_ptr(), ldw, layout, s.data_ptr(), y.data_ptr(),
+                          y.stride(0), dt, M, N, K, ctypes.byref(c), None, 0, torch.cuda.current_stream().cuda_stream)
+    L.check(rc, "qf_w8a8_gemm")
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 512, 1024), (300, 1000, 640), (520, 1004, 1024), (17, 4112, 5120),
+                                   (64, 2056, 512), (1000, 5120, 8192), (513, 16, 64)])
+def test_w8a8_tile_kernel_bitwise(M, N, K):
+    """The LDS-tiled kernel (explicit configuration) bit for bit against the restatement: token blocks and
+    channel blocks cut by M and N (N not a multiple of 8 or 16), TILED and row-major weights (also rows
+    64 bytes apart more than K), bf16 output staged through LDS (rows 16-byte aligned), bf16 rows not so
+    aligned (ldy % 8 == 4) and fp32 output stored from the registers, a padded output (ldy > N)."""
+    x, w, s = random_case(M, N, K, M * 7 + N)
+    ref = P.w8a8_reference(x, w.t(), s, None, torch.bfloat16)
+    ref32 = P.w8a8_reference(x, w.t(), s, None, torch.float32)
+    wt = qf.to_tiled(w.t())
+    wide = torch.zeros((N, K + 64), dtype=torch.int8, device=DEV)
+    wide[:, :K] = w
+    for layout, wp, ldw in ((qf.TILED, wt, 0), (qf.ROWMAJOR, w, K), (qf.ROWMAJOR, wide, K + 64)):
+        for ldy in (N, N + 8, N + 4):
+            y = torch.full((M, ldy), float("nan"), dtype=torch.bfloat16, device=DEV)
+            w8a8_into(x, wp, s, layout, ldw, y, torch.bfloat16, TILE_CFG)
+            torch.cuda.synchronize()
+            assert torch.equal(bits(y[:, :N]), bits(ref)), (M, N, K, layout, ldw, ldy)
+            if ldy > N:
+                assert torch.isnan(y[:, N:].float()).all(), (M, N, K, layout, ldy)  # nothing past N written
+        y32 = torch.empty((M, N), dtype=torch.float32, device=DEV)
+        w8a8_into(x, wp, s, layout, ldw, y32, torch.float32, TILE_CFG)
+        torch.cuda.synchronize()
+        assert torch.equal(bits(y32), bits(ref32)), (M, N, K, layout, ldw, "fp32")
+
+
+def test_w8a8_tile_kernel_against_oracle(oracle):
+    """The LDS-tiled kernel against the oracle's numpy restatement (oracle.w8a8_linear), bf16 and fp32."""
+    from helpers import bf16_bits
+    M, N, K = 300, 513, 1024
+    inp = oracle.gen_inputs(M, N, K, seed=11)
+    x, w, s = dev_inputs(inp, DEV)
+    y = qf.w8a8_mm(x, qf.to_tiled(w), s, torch.bfloat16, TILE_CFG)
+    y32 = qf.w8a8_mm(x, qf.to_tiled(w), s, torch.float32, TILE_CFG)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(y), oracle.w8a8_linear(inp.x, inp.w, inp.s))
+    assert np.array_equal(y32.cpu().numpy(), oracle.w8a8_linear(inp.x, inp.w, inp.s, out_f32=True))
+
+
+@pytest.mark.parametrize("name,M,N,K", [("gate_up", 2048, 34816, 5120), ("down", 2048, 5120, 17408),
+                                        ("qkv", 1024, 10240, 5120), ("o_proj", 2048, 5120, 8192),
+                                        ("gate_up", 768, 34816, 5120)])
+def test_w8a8_tile_kernel_auto_layer_shapes(name, M, N, K):
+    """Where the automatic rule picks the LDS-tiled kernel (the layer shapes at prefill widths), the
+    result equals the restatement bit for bit on both layouts."""
+    cfg = L.w8a8_pick_config(M, N, K)
+    assert cfg.kernel == L.KERNEL_MFMA_W8A8_TILE, cfg.to_tuple()
+    x, w, s = random_case(M, N, K, M + 3 * N)
+    ref = P.w8a8_reference(x, w.t(), s, None, torch.bfloat16)
+    y = qf.w8a8_mm(x, qf.to_tiled(w.t()), s, torch.bfloat16)
+    y_r = qf.w8a8_mm(x, w.t(), s, torch.bfloat16, layout=qf.ROWMAJOR)
+    torch.cuda.synchronize()
+    print(f"{name} M={M} cfg={cfg.to_tuple()}", flush=True)
+    assert torch.equal(bits(y), bits(ref)) and torch.equal(bits(y_r), bits(ref)), name
