@@ -580,6 +580,7 @@ def run_prefill(torch, qf, dev, args):
       MFMA), the dispatcher's default (QWEN_FAST_LINEAR_PREFILL=w8a8);
     * wide: the W8A16 wide-M kernel (the w8a16 setting up to TILED_WIDE_MAX_M rows);
     * widened: exact bf16 widening + hipBLASLt bf16 GEMM + one scale/cast pass (w8a16 above that)."""
+    from qwen_fastpath import _lib as QL
     from qwen_fastpath.patches import TILED_WIDE_MAX_M
     N, K = GEMMS["gate_up"]
     g = torch.Generator(device=dev)
@@ -622,7 +623,8 @@ def run_prefill(torch, qf, dev, args):
     del wrm
     roofline = {"bound": "mfma", "achieved": round(tops_k, 1), "peak": 5000.0, "unit": "TOPS",
                 "frac": round(tops_k / 5000.0, 4), "traffic": read_traffic(W8A8_PROFILE),
-                "kernel": f"w8a8_wide_kernel gate_up M=2048 N={N} K={K} (int8 MFMA, cfg {cfg.to_tuple()})",
+                "kernel": (f"{'w8a8_tile_kernel' if cfg.kernel == QL.KERNEL_MFMA_W8A8_TILE else 'w8a8_wide_kernel'} "
+                           f"gate_up M=2048 N={N} K={K} (int8 MFMA, cfg {cfg.to_tuple()})"),
                 "vendor_int8_gemm": {"us": round(us_v, 1), "TOPS": round(tops_v, 1),
                                      "what": "torch._int_mm (hipBLASLt) on row-major int8 weights, int32 output"}}
     line = {"metric": METRIC, "value": rows[2048]["TOPS"], "unit": "TOPS", "n_gpus": 1, "steps": 4, "warmup": 1,
