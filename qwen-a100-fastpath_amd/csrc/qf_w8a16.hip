@@ -2527,15 +2527,16 @@ bool auto_config_w8a8(int M, int N, int K, int layout, qf_w8a16_config* c) {
   c->waves = 8;
   c->depth = 4;
   // The LDS-tiled kernel once its 256 x 256 workgroups number 136 or more, unless they spill a few
-  // (<= 32) past a whole round of 256 (measured on the four layer shapes at M = 256 .. 4096: 10-33%
-  // faster there, e.g. gate_up M = 2048 377 against 420 us, down M = 2048 173 against 238 us; slower
-  // with fewer workgroups, where the shapes below split K, and at 272 workgroups, gate_up M = 512
-  // 152 against 137 us).  Its token blocks are 256 rows whatever M is, so it also needs M >= 256 with
-  // at most a quarter of the rows it computes past M.
+  // (<= 16) past a whole round of 256 (measured on the four layer shapes at M = 256 .. 4096: 10-33%
+  // faster there, e.g. gate_up M = 2048 377 against 420 us, down M = 2048 173 against 238 us, and
+  // gate_up M = 1024 (544 workgroups) 227 against 245 us; slower with fewer workgroups, where the
+  // shapes below split K, and at 272 workgroups, gate_up M = 512 152 against 137 us).  Its token
+  // blocks are 256 rows whatever M is, so it also needs M >= 256 with at most a quarter of the rows it
+  // computes past M.
   const int64_t twgs = w8a8_tile_workgroups(M, N);
   const int64_t tile_rows = (int64_t)ceil_div(M, kW8A8TileRows) * kW8A8TileRows;
   if (K < 132000 && M >= kW8A8TileRows && 4 * (int64_t)M >= 3 * tile_rows && twgs >= 136 &&
-      !(twgs > 256 && twgs % 256 != 0 && twgs % 256 <= 32)) {
+      !(twgs > 256 && twgs % 256 != 0 && twgs % 256 <= 16)) {
     c->kernel = QF_KERNEL_MFMA_W8A8_TILE;
     c->tiles_per_wave = 8;
     c->waves = 8;
