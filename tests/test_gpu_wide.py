@@ -110,8 +110,8 @@ def test_wide_layer_shapes_bitwise(name, N, K):
 def test_wide_and_widened_paths_in_a_graph():
     """The wide-M kernel with a K split (workspace + second-pass sum), without one, the widened-weights
     path (widening, library GEMM, scale/cast) and the W8A8 route (quantiser + int8 GEMM, with and
-    without a K split) captured in one graph: four replays with eager work and zeroed outputs between
-    them, each bitwise equal to the eager results."""
+    without a K split, and the LDS-tiled int8 kernel) captured in one graph: four replays with eager work
+    and zeroed outputs between them, each bitwise equal to the eager results."""
     cases = []
     for (M, N, K, seed) in ((40, 1000, 2048, 1), (300, 2000, 1024, 2)):
         wt, s, g = random_layer(N, K, seed)
@@ -128,6 +128,7 @@ def test_wide_and_widened_paths_in_a_graph():
         x, wt, s = cases[1]
         outs.append(qf.w8a16_mm_prefill(x, wt, s, torch.bfloat16, qf.TILED, chunk_rows=768))
         outs += [qf.w8a8_mm(x, wt, s, torch.bfloat16) for (x, wt, s) in cases]  # quantiser + int8 GEMM
+        outs.append(qf.w8a8_mm(x, wt, s, torch.bfloat16, (L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 4, 1, 1, 1)))
         return outs
 
     eager = [o.clone() for o in work()]
