@@ -82,7 +82,10 @@ typedef enum qf_kernel {
                                activations; tiles_per_wave 2 or 4, 4 or 8 waves, depth 2 or 4 */
   QF_KERNEL_MFMA_W8A8_TILE = 6 /* qf_w8a8_gemm only, either layout, picked for large M x N: 256-channel x
                                256-token workgroups, both operands staged in LDS by direct-to-LDS copies
-                               through a 4-stage ring; waves 8, tiles_per_wave 8, depth 4, split_k 1 */
+                               through a 4-stage ring; waves 8, tiles_per_wave 8, depth 4, split_k 1;
+                               reduce 0: a last round of at most 64 workgroups past whole rounds of 256
+                               runs its channels on the QF_KERNEL_MFMA_W8A8 kernel (a second launch),
+                               reduce 1: one launch */
 } qf_kernel;
 
 /* Launch configuration.  A zero field means "choose automatically". */

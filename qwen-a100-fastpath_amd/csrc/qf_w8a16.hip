@@ -2514,6 +2514,8 @@ int validate_w8a8(int M, int N, int K, int layout, const qf_w8a16_config& c) {
 // exceptions below.  Measured on the dense 27B-class layer's four shapes at M = 17 .. 2048 against
 // 2- and 4-tile, 4- and 8-wavefront shapes at depth 2 and 4 and splits of 1, 2 and 4: the best shape
 // or within 5% of it everywhere (down M = 512: 106.9 us against 101.7 split in four).
+bool auto_config_w8a8_wide(int M, int N, int K, int layout, qf_w8a16_config* c);
+
 bool auto_config_w8a8(int M, int N, int K, int layout, qf_w8a16_config* c) {
   if (M < 1 || N < 1 || K < QF_W8A16_K_ALIGN || K % QF_W8A16_K_ALIGN) return false;
   if (layout != QF_LAYOUT_TILED && layout != QF_LAYOUT_ROWMAJOR) return false;
@@ -2541,8 +2543,14 @@ bool auto_config_w8a8(int M, int N, int K, int layout, qf_w8a16_config* c) {
     c->tiles_per_wave = 8;
     c->waves = 8;
     c->depth = kW8A8TileStages;
+    c->reduce = 0;  // the tile kernel's tail rule (run_w8a8)
     return validate_w8a8(M, N, K, layout, *c) == QF_OK;
   }
+  return auto_config_w8a8_wide(M, N, K, layout, c);
+}
+
+// The automatic QF_KERNEL_MFMA_W8A8 shape (c holds the defaults set above).
+bool auto_config_w8a8_wide(int M, int N, int K, int layout, qf_w8a16_config* c) {
   int groups, rows;
   w8a8_groups(*c, M, N, groups, rows);
   const int64_t wgs = (int64_t)workgroups(*c, N) * groups;
@@ -2622,7 +2630,51 @@ int run_w8a8(const int8_t* xq, int64_t ldq, const float* s_a, const int8_t* w, i
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (c.kernel == QF_KERNEL_MFMA_W8A8_TILE) {
     KernelFn tf = layout == QF_LAYOUT_ROWMAJOR ? &w8a8_tile_kernel<QF_LAYOUT_ROWMAJOR> : &w8a8_tile_kernel<QF_LAYOUT_TILED>;
-    return launch(tf, dim3((unsigned)w8a8_tile_workgroups(M, N)), dim3(8 * kWave), kW8A8TileLds, s, a);
+    // Tail (reduce == 0): when the 256 x 256 workgroups fill whole rounds of 256 and then a quarter round
+    // or less, the channel blocks of the whole rounds run here and the remaining channels on the wide
+    // kernel, a second launch on the same stream (gate_up M = 2048: 1024 + 64 workgroups, 360 against
+    // 378 us in one launch).  Both write disjoint output columns; the sums are exact, so the result is
+    // the same.
+    const int nblocks = ceil_div(a.n_pad / kTileN, kW8A8TileTiles);
+    const int mblocks = ceil_div(M, kW8A8TileRows);
+    const int64_t twgs = (int64_t)nblocks * mblocks;
+    const int64_t whole = twgs / 256 * 256;
+    if (c.reduce == 0 && whole > 0 && twgs - whole <= 64 && whole % mblocks == 0) {
+      const int n_main = (int)(whole / mblocks) * kW8A8TileTiles * kTileN;  // < N: the tail holds N's last block
+      qf_w8a16_config ct = qf_w8a16_config{};
+      ct.kernel = QF_KERNEL_MFMA_W8A8;
+      ct.k_waves = 1;
+      ct.load_hint = 1;
+      ct.reduce = 1;
+      ct.split_k = 1;
+      ct.tiles_per_wave = 2;
+      ct.waves = 8;
+      ct.depth = 4;
+      const int n_tail = N - n_main;
+      if (auto_config_w8a8_wide(M, n_tail, K, layout, &ct)) {
+        ct.split_k = 1;  // no workspace: the tail runs unsplit
+        if (validate_w8a8(M, n_tail, K, layout, ct) == QF_OK) {
+          GemmArgs am = a;
+          am.N = n_main;
+          am.n_pad = n_main;
+          int st = launch(tf, dim3((unsigned)whole), dim3(8 * kWave), kW8A8TileLds, s, am);
+          if (st != QF_OK) return st;
+          GemmArgs at = a;
+          at.N = n_tail;
+          at.n_pad = round_up16(n_tail);
+          at.w = a.w + (layout == QF_LAYOUT_TILED ? (int64_t)(n_main / kTileN) * a.ksteps * kTileN * kStepK
+                                                  : (int64_t)n_main * a.ldw);
+          at.scale = a.scale + n_main;
+          at.y = reinterpret_cast<uint8_t*>(a.y) + (size_t)n_main * (a.out_f32 ? 4 : 2);
+          w8a8_groups(ct, M, n_tail, at.groups, at.group_rows);
+          KernelFn fn = select_w8a8(layout, ct.tiles_per_wave, at.group_rows / 16, ct.waves, ct.depth);
+          if (fn == nullptr) return QF_ERR_UNSUPPORTED;
+          return launch(fn, dim3(workgroups(ct, n_tail) * at.groups), dim3(ct.waves * kWave),
+                        w8a8_lds_bytes(ct, M, n_tail), s, at);
+        }
+      }
+    }
+    return launch(tf, dim3((unsigned)twgs), dim3(8 * kWave), kW8A8TileLds, s, a);
   }
   w8a8_groups(c, M, N, a.groups, a.group_rows);
   KernelFn fn = select_w8a8(layout, c.tiles_per_wave, a.group_rows / 16, c.waves, c.depth);

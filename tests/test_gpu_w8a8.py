@@ -301,3 +301,24 @@ def test_w8a8_tile_kernel_auto_layer_shapes(name, M, N, K):
     torch.cuda.synchronize()
     print(f"{name} M={M} cfg={cfg.to_tuple()}", flush=True)
     assert torch.equal(bits(y), bits(ref)) and torch.equal(bits(y_r), bits(ref)), name
+
+
+@pytest.mark.parametrize("N", [4352, 4344])
+def test_w8a8_tile_kernel_tail_split(N):
+    """reduce = 0 on the tile kernel: 17 channel blocks x 16 token blocks = 272 workgroups, so the first 16
+    channel blocks run on the tile kernel (one whole round) and the last block's channels (N ragged or
+    not) on the wide kernel, a second launch writing the same output at a column offset.  Bit for bit
+    equal to the single launch and to the restatement, on both layouts, bf16 and fp32 outputs."""
+    M, K = 4096, 256
+    x, w, s = random_case(M, N, K, N)
+    wt = qf.to_tiled(w.t())
+    split = (L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 4, 1, 1, 0)
+    for out_dtype in (torch.bfloat16, torch.float32):
+        ref = P.w8a8_reference(x, w.t(), s, None, out_dtype)
+        for layout, wp, ldw in ((qf.TILED, wt, 0), (qf.ROWMAJOR, w, K)):
+            for cfg in (split, TILE_CFG):
+                y = torch.full((M, N + 8), float("nan"), dtype=out_dtype, device=DEV)
+                w8a8_into(x, wp, s, layout, ldw, y, out_dtype, cfg)
+                torch.cuda.synchronize()
+                assert torch.equal(bits(y[:, :N]), bits(ref)), (N, out_dtype, layout, cfg)
+                assert torch.isnan(y[:, N:].float()).all(), (N, out_dtype, layout, cfg)
