@@ -203,6 +203,15 @@ int qf_w8a16_dequant_bf16(const int8_t* w, int64_t ldw, int layout, int N, int K
 int qf_scale_cast_bf16(const float* acc, int64_t lda, const float* scale, int M, int N,
                        uint16_t* y, int64_t ldy, void* stream);
 
+/* y[m, :] = bf16_rne(x[m, :] * (1 / sqrt(mean_k(x[m, k]^2) + eps))) for m < M: each row of a bf16 [M, N] matrix
+ * (row stride ldx) scaled to unit RMS, into y (row stride ldy; y may be x).  The sum of squares is formed in a
+ * fixed order, so results are reproducible; against torch's fp32 rms_norm of the same rows they differ by at
+ * most one bf16 ulp.  N % 8 == 0, N <= 8192, x and y 16-byte aligned, ldx % 8 == 0 and ldy % 8 == 0, else
+ * QF_ERR_UNSUPPORTED.  No reference counterpart: the re-normalisation between the layers of the 64-layer
+ * decode-step benchmark (each layer's output to unit RMS as the next layer's input), one launch per layer. */
+int qf_rms_norm_rows_bf16(const uint16_t* x, int64_t ldx, int M, int N, float eps, uint16_t* y, int64_t ldy,
+                          void* stream);
+
 /* ---- W8A8 path for M > 16: the reference's fallback arithmetic (dynamic per-token int8 activations, int8
  * weights, exact integer sums, fp32 scales), plugin/qwen_fastpath/patches.py:99-100, on MI355X's int8
  * MFMA, for weights in either layout (CUTLASS cannot read the TILED image). ---- */

@@ -1867,6 +1867,55 @@ __global__ void __launch_bounds__(kArgmaxSplitThreads) argmax_rows_split_kernel(
   }
 }
 
+// Row normalisation to unit RMS, bf16 in and out: y[m, :] = bf16_rne(x[m, :] * (1 / sqrt(mean(x[m, :]^2) +
+// eps))).  One workgroup per row; each thread keeps its 16-byte pieces in registers between the two
+// passes.  The sum of squares is formed in a fixed order (per thread over its pieces, a fixed butterfly
+// per wavefront, then the wavefronts in order), so results are reproducible.
+constexpr int kNormThreads = 256;
+constexpr int kNormPieces = 4;  // 16-byte pieces per thread: rows of up to 8192 elements
+
+__global__ void __launch_bounds__(kNormThreads) rms_norm_rows_kernel(const uint16_t* x, int64_t ldx, int N, float eps,
+                                                                    uint16_t* y, int64_t ldy) {
+  __shared__ float part[kNormThreads / kWave];
+  const uint16_t* xr = x + (int64_t)blockIdx.x * ldx;
+  uint16_t* yr = y + (int64_t)blockIdx.x * ldy;
+  const int npieces = N / 8;
+  u32x4_t v[kNormPieces];
+  float ss = 0.f;
+#pragma unroll
+  for (int p = 0; p < kNormPieces; ++p) {
+    const int idx = p * kNormThreads + (int)threadIdx.x;
+    if (idx < npieces) {
+      v[p] = *reinterpret_cast<const u32x4_t*>(xr + idx * 8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = __uint_as_float(v[p][e] << 16), hi = __uint_as_float(v[p][e] & 0xffff0000u);
+        ss += lo * lo;
+        ss += hi * hi;
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+  if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  float total = part[0];
+#pragma unroll
+  for (int w = 1; w < kNormThreads / kWave; ++w) total += part[w];
+  const float inv = 1.0f / __builtin_sqrtf(total / (float)N + eps);
+#pragma unroll
+  for (int p = 0; p < kNormPieces; ++p) {
+    const int idx = p * kNormThreads + (int)threadIdx.x;
+    if (idx < npieces) {
+      u32x4_t o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = pack_bf16_rne(__uint_as_float(v[p][e] << 16) * inv, __uint_as_float(v[p][e] & 0xffff0000u) * inv);
+      *reinterpret_cast<u32x4_t*>(yr + idx * 8) = o;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // Read-bandwidth probe: every byte of [buf, buf + bytes) read once with 16-byte loads, grid-stride.
 // One 32-bit xor per workgroup is written to sink so the loads cannot be dropped.
@@ -2853,6 +2902,16 @@ int qf_scale_cast_bf16(const float* acc, int64_t lda, const float* scale, int M,
   const int vec = aligned16(acc) && aligned16(scale) && aligned16(y) && lda % 4 == 0 && ldy % 8 == 0;
   hipLaunchKernelGGL(scale_cast_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), acc, lda, scale, M, N, cpr, y, ldy, vec);
+  return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
+}
+
+int qf_rms_norm_rows_bf16(const uint16_t* x, int64_t ldx, int M, int N, float eps, uint16_t* y, int64_t ldy,
+                          void* stream) {
+  if (x == nullptr || y == nullptr || M < 1 || N < 1 || ldx < N || ldy < N || !(eps >= 0.f)) return QF_ERR_INVALID_ARG;
+  if (N % 8 || N > kNormPieces * kNormThreads * 8 || !aligned16(x) || !aligned16(y) || ldx % 8 || ldy % 8)
+    return QF_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(rms_norm_rows_kernel, dim3((unsigned)M), dim3(kNormThreads), 0, reinterpret_cast<hipStream_t>(stream),
+                     x, ldx, N, eps, y, ldy);
   return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
 }
 

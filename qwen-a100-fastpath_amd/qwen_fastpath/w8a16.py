@@ -305,6 +305,25 @@ def scale_cast_bf16(acc: torch.Tensor, w_scale: torch.Tensor, out: torch.Tensor)
     return out
 
 
+def rms_norm_rows(x: torch.Tensor, eps: float = 2.0 ** -23, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Each row of a bf16 [M, N] tensor scaled to unit RMS in one launch (qf_rms_norm_rows_bf16):
+    bf16(x * (1 / sqrt(mean(x^2) + eps))), within one bf16 ulp of torch.nn.functional.rms_norm(x, (N,), eps=eps)
+    (whose default eps for a bf16 input is float32's epsilon, 2^-23, the default here too).  The glue between
+    the layers of the 64-layer decode-step benchmark; N % 8 == 0 and N <= 8192."""
+    if x.dim() != 2 or x.dtype != torch.bfloat16:
+        raise TypeError("x must be a 2-D bf16 tensor")
+    M, N = x.shape
+    if x.stride(1) != 1 or x.data_ptr() % 16 or (M > 1 and x.stride(0) % 8):
+        x = x.contiguous()
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device) if out is None else out
+    if M == 0:
+        return y
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    L.check(L.load().qf_rms_norm_rows_bf16(x.data_ptr(), x.stride(0) if M > 1 else N, M, N, float(eps), y.data_ptr(),
+                                           y.stride(0) if M > 1 else N, stream), "qf_rms_norm_rows_bf16")
+    return y
+
+
 def quantize_tokens_int8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Dynamic symmetric per-token int8 quantisation (qf_quantize_tokens_int8): s_a[m] = amax|x[m]| /
     127 (as the fp32 reciprocal product), xq = clamp(round_half_even(x / s_a), -128, 127), zero rows -> 0.

@@ -6,7 +6,7 @@
 * the gate_up M sweep (M = 1, 2, 3, 5, 8, 12, 16) on TILED weights;
 * the 64-layer decode-step stack at M = 5 (distinct seeded weights per layer, o_proj reading the first
   8192 qkv outputs, down the first 17408 gate_up outputs, each layer's output re-normalised to unit RMS
-  as the next input) captured as one graph: replays equal the eager step bit for bit, and for sampled
+  as the next input by qf_rms_norm_rows_bf16) captured as one graph: replays equal the eager step bit for bit, and for sampled
   layers every GEMM is checked against the oracle on the input it actually received.
 
 Each check applies oracle.check_w8a16 (every output within 1 bf16 ulp plus the fp32 floor of the exact
@@ -133,7 +133,7 @@ def _step(layers, x0, record=None):
         d = mm(ins["down"], "down")
         if record is not None and i in record:
             record[i] = ({n: t.clone() for n, t in ins.items()}, {"qkv": qkv, "o_proj": o, "gate_up": gu, "down": d})
-        h = torch.nn.functional.rms_norm(d, (d.shape[-1],))
+        h = qf.rms_norm_rows(d)  # unit RMS, torch's default eps for bf16 (2^-23), one launch
     return h
 
 
@@ -173,3 +173,29 @@ def test_stack64_graph_replay_and_sampled_layers(oracle):
             s = layers[i].s[name].cpu().numpy()
             _check(oracle, x_bits, w_rm, s, bf16_bits(outs[name]), f"stack64 layer {i} {name} M=5 tiled",
                    qf.resolve_config(M5, N, K, qf.TILED))
+
+
+@pytest.mark.parametrize("M,N", [(5, 5120), (1, 8), (7, 8192), (16, 4096), (3, 17408 // 8 * 8 // 4)])
+def test_rms_norm_rows(M, N):
+    """The stack's glue (qf_rms_norm_rows_bf16) against torch's fp32 restatement and torch's rms_norm (eps 2^-23,
+    torch's default for bf16 inputs), also with eps 2^-7: at most one bf16 ulp apart; reproducible; in place equal
+    to out of place."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(M * 131 + N)
+    scale = torch.exp2(torch.randint(-6, 7, (M, 1), device=DEV, generator=g).float())
+    x = (torch.randn(M, N, device=DEV, generator=g) * scale).to(torch.bfloat16)
+    y = qf.rms_norm_rows(x)
+    xf = x.float()
+    ref = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 2.0 ** -23)).to(torch.bfloat16)
+    tref = torch.nn.functional.rms_norm(x, (N,))
+    y7 = qf.rms_norm_rows(x, eps=2.0 ** -7)
+    ref7 = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 2.0 ** -7)).to(torch.bfloat16)
+    again = qf.rms_norm_rows(x)
+    inplace = x.clone()
+    qf.rms_norm_rows(inplace, out=inplace)
+    torch.cuda.synchronize()
+    yi = y.view(torch.int16).int()
+    assert (yi - ref.view(torch.int16).int()).abs().max().item() <= 1
+    assert (yi - tref.view(torch.int16).int()).abs().max().item() <= 1
+    assert (y7.view(torch.int16).int() - ref7.view(torch.int16).int()).abs().max().item() <= 1
+    assert torch.equal(y, again) and torch.equal(y, inplace)
