@@ -621,9 +621,14 @@ def run_prefill(torch, qf, dev, args):
     tops_v = 2.0 * M * N * K / us_v / 1e6
     log(f"  prefill gate_up M= 2048 vendor int8 GEMM (torch._int_mm): {us_v:.1f} us {tops_v:.1f} TOPS")
     del wrm
+    # The tile kernel's call is two launches when its workgroups pass whole rounds of 256 by at most 64
+    # (reduce 0): the whole rounds' channel blocks, then the rest on the wide kernel.
+    tile_wgs = -(-N // 256) * -(-M // 256)
+    tail = cfg.reduce == 0 and tile_wgs > 256 and 0 < tile_wgs % 256 <= 64 and (tile_wgs // 256 * 256) % -(-M // 256) == 0
+    tile_name = "w8a8_tile_kernel + w8a8_wide_kernel on the last channels" if tail else "w8a8_tile_kernel"
     roofline = {"bound": "mfma", "achieved": round(tops_k, 1), "peak": 5000.0, "unit": "TOPS",
                 "frac": round(tops_k / 5000.0, 4), "traffic": read_traffic(W8A8_PROFILE),
-                "kernel": (f"{'w8a8_tile_kernel' if cfg.kernel == QL.KERNEL_MFMA_W8A8_TILE else 'w8a8_wide_kernel'} "
+                "kernel": (f"{tile_name if cfg.kernel == QL.KERNEL_MFMA_W8A8_TILE else 'w8a8_wide_kernel'} "
                            f"gate_up M=2048 N={N} K={K} (int8 MFMA, cfg {cfg.to_tuple()})"),
                 "vendor_int8_gemm": {"us": round(us_v, 1), "TOPS": round(tops_v, 1),
                                      "what": "torch._int_mm (hipBLASLt) on row-major int8 weights, int32 output"}}
