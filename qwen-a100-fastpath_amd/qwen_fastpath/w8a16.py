@@ -129,9 +129,17 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+def _on_gpu(*tensors) -> None:
+    """Every tensor handed to the library must live on a GPU: a host pointer reaching a kernel faults the device."""
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise TypeError(f"expected a GPU tensor, got one on {t.device}")
+
+
 def _launch(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, layout: int, out_dtype: torch.dtype,
             config) -> torch.Tensor:
     lib = L.load()
+    _on_gpu(x, w, w_scale)
     if x.dim() != 2 or x.dtype != torch.bfloat16:
         raise TypeError(f"x must be a 2-D bf16 tensor, got {x.dtype} {tuple(x.shape)}")
     if w_scale.dtype != torch.float32:
@@ -200,6 +208,7 @@ def w8a16_mm_argmax(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, n_v
     ties: patches.py:160-166,178-185).  Returns the int64 ids [M] -- and the bf16 logits [M, N] when
     with_logits -- or None when the fused path does not serve this configuration (the caller then uses
     w8a16_mm and top_tokens)."""
+    _on_gpu(x, w, w_scale)
     lib = L.load()
     if x.dim() != 2 or x.dtype != torch.bfloat16 or w_scale.dtype != torch.float32:
         raise TypeError("x must be 2-D bf16 and w_scale fp32")
@@ -243,6 +252,7 @@ def to_tiled(w_t: torch.Tensor) -> torch.Tensor:
     x 64 k, tile (t, s) at byte ((t * K/64) + s) * 1024, lane l of the tile holding channel
     16 t + l % 16, k = 64 s + 16 (l // 16) .. +15.  Every 64-lane 16-byte load of the kernel then
     reads one contiguous KiB."""
+    _on_gpu(w_t)
     K, N = w_t.shape
     ldw = _weight_geometry(w_t, N, K, ROWMAJOR)
     out = torch.empty(tiled_numel(N, K), dtype=torch.int8, device=w_t.device)
@@ -253,6 +263,7 @@ def to_tiled(w_t: torch.Tensor) -> torch.Tensor:
 
 def from_tiled(w_tiled: torch.Tensor, N: int, K: int) -> torch.Tensor:
     """Inverse of to_tiled: returns the [K, N] stride-(1, K) view of a fresh [N, K] matrix."""
+    _on_gpu(w_tiled)
     out = torch.empty((N, K), dtype=torch.int8, device=w_tiled.device)
     stream = torch.cuda.current_stream(w_tiled.device).cuda_stream
     L.check(L.load().qf_w8a16_unpack(w_tiled.data_ptr(), out.data_ptr(), K, N, K, stream), "qf_w8a16_unpack")
@@ -275,6 +286,7 @@ def dequant_bf16(w: torch.Tensor, N: int, K: int, layout: int = ROWMAJOR, n0: in
                  out: torch.Tensor | None = None) -> torch.Tensor:
     """Exact bf16 copy [rows, K] of weight rows [n0, n0 + rows) (no scale), from a [K, N] stride-(1, K)
     view or from the TILED image."""
+    _on_gpu(w, out)
     rows = N - n0 if rows is None else rows
     ldw = _weight_geometry(w, N, K, layout)
     if out is None:
@@ -290,6 +302,7 @@ def dequant_bf16(w: torch.Tensor, N: int, K: int, layout: int = ROWMAJOR, n0: in
 def scale_cast_bf16(acc: torch.Tensor, w_scale: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
     """out[m, n] = bf16(acc[m, n] * w_scale[n]) in one pass (qf_scale_cast_bf16): acc fp32 [M, N] and
     out bf16 [M, N], both with unit column stride; bit-identical to (acc * w_scale).to(torch.bfloat16)."""
+    _on_gpu(acc, w_scale, out)
     M, N = acc.shape
     if acc.dtype != torch.float32 or out.dtype != torch.bfloat16 or w_scale.dtype != torch.float32:
         raise TypeError("acc and w_scale must be fp32, out bf16")
@@ -310,12 +323,20 @@ def rms_norm_rows(x: torch.Tensor, eps: float = 2.0 ** -23, out: torch.Tensor | 
     bf16(x * (1 / sqrt(mean(x^2) + eps))), within one bf16 ulp of torch.nn.functional.rms_norm(x, (N,), eps=eps)
     (whose default eps for a bf16 input is float32's epsilon, 2^-23, the default here too).  The glue between
     the layers of the 64-layer decode-step benchmark; N % 8 == 0 and N <= 8192."""
+    _on_gpu(x, out)
     if x.dim() != 2 or x.dtype != torch.bfloat16:
         raise TypeError("x must be a 2-D bf16 tensor")
     M, N = x.shape
     if x.stride(1) != 1 or x.data_ptr() % 16 or (M > 1 and x.stride(0) % 8):
         x = x.contiguous()
-    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device) if out is None else out
+    if out is None:
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    else:
+        y = out
+        if (y.dtype != torch.bfloat16 or y.dim() != 2 or tuple(y.shape) != (M, N) or y.device != x.device
+                or y.stride(1) != 1 or y.data_ptr() % 16 or (M > 1 and y.stride(0) % 8)):
+            raise ValueError(f"out must be a bf16 [{M}, {N}] tensor on {x.device} with unit column stride, 16-byte "
+                             f"aligned rows and a row stride that is a multiple of 8")
     if M == 0:
         return y
     stream = torch.cuda.current_stream(x.device).cuda_stream
@@ -329,6 +350,7 @@ def quantize_tokens_int8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     127 (as the fp32 reciprocal product), xq = clamp(round_half_even(x / s_a), -128, 127), zero rows -> 0.
     The arithmetic of vLLM's scaled_int8_quant(x, symmetric=True) at the reference's fallback
     (plugin/qwen_fastpath/patches.py:99).  x bf16 [M, K], K % 64 == 0.  Returns (xq int8 [M, K], s_a fp32 [M])."""
+    _on_gpu(x)
     if x.dim() != 2 or x.dtype != torch.bfloat16:
         raise TypeError("x must be a 2-D bf16 tensor")
     M, K = x.shape
@@ -350,6 +372,7 @@ def w8a8_mm(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, out_dtype: 
     int32 sums on the int8 MFMA: the arithmetic of the reference's M > 16 fallback, scaled_int8_quant +
     cutlass_scaled_mm (plugin/qwen_fastpath/patches.py:99-100).  w is the TILED image or the [K, N]
     stride-(1, K) view of the checkpoint's row-major weight (layout=ROWMAJOR).  Any M."""
+    _on_gpu(x, w, w_scale)
     lib = L.load()
     if w_scale.dtype != torch.float32:
         raise TypeError(f"w_scale must be fp32, got {w_scale.dtype}")

@@ -197,3 +197,19 @@ def test_repack_refuses_other_model_dtypes():
         params_dtype = torch.float16
 
     assert P.repack_layer_weight(Layer()) is False
+
+
+def test_library_wrappers_refuse_host_tensors():
+    """Every wrapper that hands pointers to the library refuses tensors in host memory before any call: a host
+    pointer reaching a kernel would fault the device."""
+    x = torch.zeros(5, 512, dtype=torch.bfloat16)
+    w = torch.zeros(1024, 512, dtype=torch.int8)
+    s = torch.ones(1024, dtype=torch.float32)
+    calls = [lambda: qf.rms_norm_rows(x), lambda: qf.quantize_tokens_int8(x), lambda: qf.to_tiled(w.t()),
+             lambda: qf.w8a8_mm(x, w.t(), s, torch.bfloat16, layout=qf.ROWMAJOR),
+             lambda: qf.dequant_bf16(w.t(), 1024, 512),
+             lambda: qf.scale_cast_bf16(torch.zeros(5, 1024), s, torch.zeros(5, 1024, dtype=torch.bfloat16)),
+             lambda: qf.w8a16_mm_argmax(x, w.t(), s, 1024)]
+    for call in calls:
+        with pytest.raises(TypeError, match="GPU tensor"):
+            call()
