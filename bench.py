@@ -543,22 +543,29 @@ def run_msweep(torch, qf, dev, args):
 
 
 def w8a8_gate_up_gemm(torch, qf, dev, g, M, sets):
-    """The W8A8 GEMM alone on gate_up at M rows (activations quantised once, beforehand): returns a
-    callable that runs it on weight set i, and its configuration."""
+    """The W8A8 GEMM alone on gate_up at M rows (activations quantised once, beforehand, in the layout
+    w8a8_mm gives that kernel): returns a callable that runs it on weight set i, and its configuration."""
     import ctypes
     from qwen_fastpath import _lib as QL
     N, K = GEMMS["gate_up"]
     x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
-    xq, s_a = qf.quantize_tokens_int8(x)
-    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     lib = QL.load()
     cfg = QL.w8a8_pick_config(M, N, K)
+    x_tiled = cfg.kernel == QL.KERNEL_MFMA_W8A8_TILE
+    xq, s_a = qf.quantize_tokens_int8(x, tiled=x_tiled)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     assert int(lib.qf_w8a8_workspace_bytes(M, N, K, qf.TILED, ctypes.byref(cfg))) == 0
 
     def gemm(i):
-        QL.check(lib.qf_w8a8_gemm(xq.data_ptr(), K, s_a.data_ptr(), sets[i][0].data_ptr(), 0, qf.TILED,
-                                  sets[i][1].data_ptr(), y.data_ptr(), N, QL.DTYPE_BF16, M, N, K, ctypes.byref(cfg),
-                                  None, 0, torch.cuda.current_stream().cuda_stream), "qf_w8a8_gemm")
+        st = torch.cuda.current_stream().cuda_stream
+        if x_tiled:
+            QL.check(lib.qf_w8a8_gemm_xt(xq.data_ptr(), s_a.data_ptr(), sets[i][0].data_ptr(), 0, qf.TILED,
+                                         sets[i][1].data_ptr(), y.data_ptr(), N, QL.DTYPE_BF16, M, N, K,
+                                         ctypes.byref(cfg), None, 0, st), "qf_w8a8_gemm_xt")
+        else:
+            QL.check(lib.qf_w8a8_gemm(xq.data_ptr(), K, s_a.data_ptr(), sets[i][0].data_ptr(), 0, qf.TILED,
+                                      sets[i][1].data_ptr(), y.data_ptr(), N, QL.DTYPE_BF16, M, N, K, ctypes.byref(cfg),
+                                      None, 0, st), "qf_w8a8_gemm")
     return gemm, cfg
 
 
@@ -625,7 +632,8 @@ def run_prefill(torch, qf, dev, args):
     # (reduce 0): the whole rounds' channel blocks, then the rest on the wide kernel.
     tile_wgs = -(-N // 256) * -(-M // 256)
     tail = cfg.reduce == 0 and tile_wgs > 256 and 0 < tile_wgs % 256 <= 64 and (tile_wgs // 256 * 256) % -(-M // 256) == 0
-    tile_name = "w8a8_tile_kernel + w8a8_wide_kernel on the last channels" if tail else "w8a8_tile_kernel"
+    tile_name = ("w8a8_tile_kernel + w8a8_wide_kernel on the last channels" if tail else "w8a8_tile_kernel") + \
+        ", token-tiled activations"
     roofline = {"bound": "mfma", "achieved": round(tops_k, 1), "peak": 5000.0, "unit": "TOPS",
                 "frac": round(tops_k / 5000.0, 4), "traffic": read_traffic(W8A8_PROFILE),
                 "kernel": (f"{tile_name if cfg.kernel == QL.KERNEL_MFMA_W8A8_TILE else 'w8a8_wide_kernel'} "

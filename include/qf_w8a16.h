@@ -25,6 +25,8 @@
  *   qf_w8a16_gemm_argmax     <- draft logits + pad mask + argmax in one launch   patches.py:160-166,178-185
  *   qf_quantize_tokens_int8  <- ops.scaled_int8_quant (dynamic, symmetric)   plugin/qwen_fastpath/patches.py:99
  *   qf_w8a8_gemm             <- ops.cutlass_scaled_mm on the int8 weights      plugin/qwen_fastpath/patches.py:100
+ *   qf_quantize_tokens_int8_tiled / qf_w8a8_gemm_xt / qf_tokens_tiled_bytes: the same two steps with the
+ *                              activations in a tiled layout (no reference counterpart; the library's own format)
  *   qf_w8a8_pick_config / qf_w8a8_workspace_bytes: its configuration and workspace (host only)
  *   qf_w8a16_repack / qf_w8a16_unpack: load-time weight layout change (no reference counterpart;
  *                              the reference streams the checkpoint layout as is, w8a16.py:1-7)
@@ -239,6 +241,24 @@ int qf_quantize_tokens_int8(const uint16_t* x, int64_t ldx, int M, int K, int8_t
 int qf_w8a8_gemm(const int8_t* xq, int64_t ldq, const float* s_a, const int8_t* w, int64_t ldw, int layout,
                  const float* scale, void* y, int64_t ldy, int out_dtype, int M, int N, int K,
                  const qf_w8a16_config* cfg, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The same quantisation written as the token-tiled image xt: the TILED weight layout applied to the
+ * [M, K] int8 activations.  Block (b, s) holds tokens 16b .. 16b+15 at k 64s .. 64s+63 and lies at byte
+ * (b * K/64 + s) * 1024; in it, token 16b + r at k 64s + 16g .. +15 sits at byte 16 * (16g + r).  The
+ * image has ceil(M/16) blocks of rows (qf_tokens_tiled_bytes(M, K) bytes); the rows past M are zeros.
+ * xt 16-byte aligned; the other requirements as qf_quantize_tokens_int8.  No reference counterpart: an
+ * activation layout of this library, read by qf_w8a8_gemm_xt with one contiguous KiB per fragment
+ * (row-major xq gives each copy 16 rows of 64 bytes). */
+size_t qf_tokens_tiled_bytes(int M, int K);
+int qf_quantize_tokens_int8_tiled(const uint16_t* x, int64_t ldx, int M, int K, int8_t* xt, float* s_a,
+                                  void* stream);
+
+/* qf_w8a8_gemm on the token-tiled image of qf_quantize_tokens_int8_tiled (same arguments without ldq; the
+ * same kernels, configurations, workspace and results, bit for bit).  Reference: the same call,
+ * ops.cutlass_scaled_mm at plugin/qwen_fastpath/patches.py:100. */
+int qf_w8a8_gemm_xt(const int8_t* xt, const float* s_a, const int8_t* w, int64_t ldw, int layout, const float* scale,
+                    void* y, int64_t ldy, int out_dtype, int M, int N, int K, const qf_w8a16_config* cfg,
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* Automatic configuration and workspace bytes of qf_w8a8_gemm (host only). */
 int qf_w8a8_pick_config(int M, int N, int K, int layout, qf_w8a16_config* cfg);

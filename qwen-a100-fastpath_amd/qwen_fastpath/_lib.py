@@ -61,6 +61,9 @@ EXPORTS = (
     "qf_read_probe",
     "qf_quantize_tokens_int8",
     "qf_w8a8_gemm",
+    "qf_tokens_tiled_bytes",
+    "qf_quantize_tokens_int8_tiled",
+    "qf_w8a8_gemm_xt",
     "qf_w8a8_pick_config",
     "qf_w8a8_workspace_bytes",
 )
@@ -159,6 +162,12 @@ def load() -> ctypes.CDLL:
     L.qf_quantize_tokens_int8.restype = i32
     L.qf_w8a8_gemm.argtypes = [p, i64, p, p, i64, i32, p, p, i64, i32, i32, i32, i32, ctypes.POINTER(Config), p, sz, p]
     L.qf_w8a8_gemm.restype = i32
+    L.qf_tokens_tiled_bytes.argtypes = [i32, i32]
+    L.qf_tokens_tiled_bytes.restype = sz
+    L.qf_quantize_tokens_int8_tiled.argtypes = [p, i64, i32, i32, p, p, p]
+    L.qf_quantize_tokens_int8_tiled.restype = i32
+    L.qf_w8a8_gemm_xt.argtypes = [p, p, p, i64, i32, p, p, i64, i32, i32, i32, i32, ctypes.POINTER(Config), p, sz, p]
+    L.qf_w8a8_gemm_xt.restype = i32
     L.qf_w8a8_pick_config.argtypes = [i32, i32, i32, i32, ctypes.POINTER(Config)]
     L.qf_w8a8_pick_config.restype = i32
     L.qf_w8a8_workspace_bytes.argtypes = [i32, i32, i32, i32, ctypes.POINTER(Config)]

@@ -345,33 +345,46 @@ def rms_norm_rows(x: torch.Tensor, eps: float = 2.0 ** -23, out: torch.Tensor | 
     return y
 
 
-def quantize_tokens_int8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+def quantize_tokens_int8(x: torch.Tensor, tiled: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
     """Dynamic symmetric per-token int8 quantisation (qf_quantize_tokens_int8): s_a[m] = amax|x[m]| /
     127 (as the fp32 reciprocal product), xq = clamp(round_half_even(x / s_a), -128, 127), zero rows -> 0.
     The arithmetic of vLLM's scaled_int8_quant(x, symmetric=True) at the reference's fallback
-    (plugin/qwen_fastpath/patches.py:99).  x bf16 [M, K], K % 64 == 0.  Returns (xq int8 [M, K], s_a fp32 [M])."""
+    (plugin/qwen_fastpath/patches.py:99).  x bf16 [M, K], K % 64 == 0.  Returns (xq int8 [M, K], s_a fp32 [M]);
+    with tiled=True xq is instead the token-tiled image (qf_quantize_tokens_int8_tiled), a flat int8 tensor
+    of ceil(M/16) * 16 * K bytes (the layout w8a8_mm hands the LDS-tiled kernel)."""
     _on_gpu(x)
     if x.dim() != 2 or x.dtype != torch.bfloat16:
         raise TypeError("x must be a 2-D bf16 tensor")
     M, K = x.shape
     if x.stride(1) != 1 or x.data_ptr() % 16 or (M > 1 and x.stride(0) % 8):
         x = x.clone(memory_format=torch.contiguous_format)
-    xq = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    if tiled:
+        xq = torch.empty(((M + 15) // 16 * 16 * K,), dtype=torch.int8, device=x.device)
+    else:
+        xq = torch.empty((M, K), dtype=torch.int8, device=x.device)
     s_a = torch.empty((M,), dtype=torch.float32, device=x.device)
     if M == 0:
         return xq, s_a
     stream = torch.cuda.current_stream(x.device).cuda_stream
-    L.check(L.load().qf_quantize_tokens_int8(x.data_ptr(), x.stride(0) if M > 1 else K, M, K, xq.data_ptr(), K,
-                                             s_a.data_ptr(), stream), "qf_quantize_tokens_int8")
+    ldx = x.stride(0) if M > 1 else K
+    if tiled:
+        L.check(L.load().qf_quantize_tokens_int8_tiled(x.data_ptr(), ldx, M, K, xq.data_ptr(), s_a.data_ptr(), stream),
+                "qf_quantize_tokens_int8_tiled")
+    else:
+        L.check(L.load().qf_quantize_tokens_int8(x.data_ptr(), ldx, M, K, xq.data_ptr(), K, s_a.data_ptr(), stream),
+                "qf_quantize_tokens_int8")
     return xq, s_a
 
 
 def w8a8_mm(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, out_dtype: torch.dtype, cfg=None,
-            layout: int = TILED) -> torch.Tensor:
+            layout: int = TILED, x_tiled: bool | None = None) -> torch.Tensor:
     """y = ((xq @ W^T) * s_a) * w_scale with per-token int8 activations (quantize_tokens_int8), exact
     int32 sums on the int8 MFMA: the arithmetic of the reference's M > 16 fallback, scaled_int8_quant +
     cutlass_scaled_mm (plugin/qwen_fastpath/patches.py:99-100).  w is the TILED image or the [K, N]
-    stride-(1, K) view of the checkpoint's row-major weight (layout=ROWMAJOR).  Any M."""
+    stride-(1, K) view of the checkpoint's row-major weight (layout=ROWMAJOR).  Any M.  x_tiled selects
+    the activations' layout between the two launches (qf_quantize_tokens_int8_tiled + qf_w8a8_gemm_xt, or
+    the row-major pair); None picks the tiled one when the call runs the LDS-tiled kernel.  The result is
+    the same either way."""
     _on_gpu(x, w, w_scale)
     lib = L.load()
     if w_scale.dtype != torch.float32:
@@ -383,7 +396,14 @@ def w8a8_mm(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, out_dtype: 
         raise TypeError(f"out_dtype must be bf16 or fp32, got {out_dtype}")
     if M == 0:
         return x.new_empty((0, N), dtype=out_dtype)
-    xq, s_a = quantize_tokens_int8(x)
+    c = _config_struct(AUTO if cfg is None else cfg)
+    if x_tiled is None:
+        kernel = c.kernel
+        if kernel == 0:
+            picked = L.w8a8_pick_config(M, N, K, layout)
+            kernel = picked.kernel if picked is not None else 0
+        x_tiled = kernel == L.KERNEL_MFMA_W8A8_TILE
+    xq, s_a = quantize_tokens_int8(x, tiled=x_tiled)
     s = w_scale.reshape(-1)
     if not s.is_contiguous() or s.data_ptr() % 16:
         s = s.clone(memory_format=torch.contiguous_format)
@@ -394,14 +414,17 @@ def w8a8_mm(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, out_dtype: 
     else:
         raise TypeError(f"out_dtype must be bf16 or fp32, got {out_dtype}")
     y = torch.empty((M, N), dtype=out_dtype, device=x.device)
-    c = _config_struct(AUTO if cfg is None else cfg)
     ws_bytes = int(lib.qf_w8a8_workspace_bytes(M, N, K, layout, ctypes.byref(c)))
     ws = _workspace(x.device, ws_bytes) if ws_bytes else None
     stream = torch.cuda.current_stream(x.device).cuda_stream
-    rc = lib.qf_w8a8_gemm(xq.data_ptr(), K, s_a.data_ptr(), w.data_ptr(), ldw, layout, s.data_ptr(), y.data_ptr(), N,
-                          dt, M, N, K, ctypes.byref(c), ws.data_ptr() if ws is not None else None,
-                          ws.numel() if ws is not None else 0, stream)
-    L.check(rc, f"qf_w8a8_gemm(M={M}, N={N}, K={K}, layout={layout})")
+    ws_ptr, ws_n = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
+    if x_tiled:
+        rc = lib.qf_w8a8_gemm_xt(xq.data_ptr(), s_a.data_ptr(), w.data_ptr(), ldw, layout, s.data_ptr(), y.data_ptr(),
+                                 N, dt, M, N, K, ctypes.byref(c), ws_ptr, ws_n, stream)
+    else:
+        rc = lib.qf_w8a8_gemm(xq.data_ptr(), K, s_a.data_ptr(), w.data_ptr(), ldw, layout, s.data_ptr(), y.data_ptr(),
+                              N, dt, M, N, K, ctypes.byref(c), ws_ptr, ws_n, stream)
+    L.check(rc, f"qf_w8a8_gemm{'_xt' if x_tiled else ''}(M={M}, N={N}, K={K}, layout={layout})")
     return y
 
 

@@ -231,28 +231,47 @@ def test_rowmajor_m17_dispatch_uses_the_int8_kernel(oracle, monkeypatch):
 TILE_CFG = (L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 4, 1, 1, 1)
 
 
-def w8a8_into(x, w, s, layout, ldw, y, out_dtype, cfg):
-    """qf_w8a8_gemm into a caller's output y [M, ldy] (row stride ldy >= N), through the C ABI."""
+def w8a8_into(x, w, s, layout, ldw, y, out_dtype, cfg, x_tiled=False):
+    """qf_w8a8_gemm (x_tiled: qf_quantize_tokens_int8_tiled + qf_w8a8_gemm_xt) into a caller's output
+    y [M, ldy] (row stride ldy >= N), through the C ABI."""
     import ctypes
     lib = L.load()
     M, K = x.shape
     N = s.numel()
-    xq, s_a = qf.quantize_tokens_int8(x)
+    xq, s_a = qf.quantize_tokens_int8(x, tiled=x_tiled)
     c = L.Config.from_seq(cfg)
     dt = L.DTYPE_BF16 if out_dtype == torch.bfloat16 else L.DTYPE_F32
-    assert int(lib.qf_w8a8_workspace_bytes(M, N, K, layout, ctypes.byref(c))) == 0
-    rc = lib.qf_w8a8_gemm(xq.data_ptr(), K, s_a.data_ptr(), w.data_ptr(), ldw, layout, s.data_ptr(), y.data_ptr(),
-                          y.stride(0), dt, M, N, K, ctypes.byref(c), None, 0, torch.cuda.current_stream().cuda_stream)
-    L.check(rc, "qf_w8a8_gemm")
+    need = int(lib.qf_w8a8_workspace_bytes(M, N, K, layout, ctypes.byref(c)))
+    ws = torch.zeros((max(need, 16),), dtype=torch.uint8, device=DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    if x_tiled:
+        rc = lib.qf_w8a8_gemm_xt(xq.data_ptr(), s_a.data_ptr(), w.data_ptr(), ldw, layout, s.data_ptr(), y.data_ptr(),
+                                 y.stride(0), dt, M, N, K, ctypes.byref(c), ws.data_ptr(), need, stream)
+    else:
+        rc = lib.qf_w8a8_gemm(xq.data_ptr(), K, s_a.data_ptr(), w.data_ptr(), ldw, layout, s.data_ptr(), y.data_ptr(),
+                              y.stride(0), dt, M, N, K, ctypes.byref(c), ws.data_ptr(), need, stream)
+    L.check(rc, "qf_w8a8_gemm_xt" if x_tiled else "qf_w8a8_gemm")
 
 
+def tile_tokens(xq):
+    """The token-tiled image of a row-major int8 [M, K] (rows padded with zeros to a multiple of 16): block
+    (b, s) at (b * K/64 + s) KiB, token 16 b + r at k 64 s + 16 g .. +15 at byte 16 (16 g + r) of it."""
+    M, K = xq.shape
+    Mp = (M + 15) // 16 * 16
+    pad = torch.zeros((Mp, K), dtype=torch.int8, device=xq.device)
+    pad[:M] = xq
+    return pad.view(Mp // 16, 16, K // 64, 4, 16).permute(0, 2, 3, 1, 4).reshape(-1)
+
+
+@pytest.mark.parametrize("x_tiled", [False, True])
 @pytest.mark.parametrize("M,N,K", [(256, 512, 1024), (300, 1000, 640), (520, 1004, 1024), (17, 4112, 5120),
                                    (64, 2056, 512), (1000, 5120, 8192), (513, 16, 64)])
-def test_w8a8_tile_kernel_bitwise(M, N, K):
+def test_w8a8_tile_kernel_bitwise(M, N, K, x_tiled):
     """The LDS-tiled kernel (explicit configuration) bit for bit against the restatement: token blocks and
     channel blocks cut by M and N (N not a multiple of 8 or 16), TILED and row-major weights (also rows
     64 bytes apart more than K), bf16 output staged through LDS (rows 16-byte aligned), bf16 rows not so
-    aligned (ldy % 8 == 4) and fp32 output stored from the registers, a padded output (ldy > N)."""
+    aligned (ldy % 8 == 4) and fp32 output stored from the registers, a padded output (ldy > N); row-major
+    and token-tiled activations."""
     x, w, s = random_case(M, N, K, M * 7 + N)
     ref = P.w8a8_reference(x, w.t(), s, None, torch.bfloat16)
     ref32 = P.w8a8_reference(x, w.t(), s, None, torch.float32)
@@ -262,13 +281,13 @@ def test_w8a8_tile_kernel_bitwise(M, N, K):
     for layout, wp, ldw in ((qf.TILED, wt, 0), (qf.ROWMAJOR, w, K), (qf.ROWMAJOR, wide, K + 64)):
         for ldy in (N, N + 8, N + 4):
             y = torch.full((M, ldy), float("nan"), dtype=torch.bfloat16, device=DEV)
-            w8a8_into(x, wp, s, layout, ldw, y, torch.bfloat16, TILE_CFG)
+            w8a8_into(x, wp, s, layout, ldw, y, torch.bfloat16, TILE_CFG, x_tiled)
             torch.cuda.synchronize()
             assert torch.equal(bits(y[:, :N]), bits(ref)), (M, N, K, layout, ldw, ldy)
             if ldy > N:
                 assert torch.isnan(y[:, N:].float()).all(), (M, N, K, layout, ldy)  # nothing past N written
         y32 = torch.empty((M, N), dtype=torch.float32, device=DEV)
-        w8a8_into(x, wp, s, layout, ldw, y32, torch.float32, TILE_CFG)
+        w8a8_into(x, wp, s, layout, ldw, y32, torch.float32, TILE_CFG, x_tiled)
         torch.cuda.synchronize()
         assert torch.equal(bits(y32), bits(ref32)), (M, N, K, layout, ldw, "fp32")
 
@@ -317,8 +336,65 @@ def test_w8a8_tile_kernel_tail_split(N):
         ref = P.w8a8_reference(x, w.t(), s, None, out_dtype)
         for layout, wp, ldw in ((qf.TILED, wt, 0), (qf.ROWMAJOR, w, K)):
             for cfg in (split, TILE_CFG):
-                y = torch.full((M, N + 8), float("nan"), dtype=out_dtype, device=DEV)
-                w8a8_into(x, wp, s, layout, ldw, y, out_dtype, cfg)
-                torch.cuda.synchronize()
-                assert torch.equal(bits(y[:, :N]), bits(ref)), (N, out_dtype, layout, cfg)
-                assert torch.isnan(y[:, N:].float()).all(), (N, out_dtype, layout, cfg)
+                for x_tiled in (False, True):
+                    y = torch.full((M, N + 8), float("nan"), dtype=out_dtype, device=DEV)
+                    w8a8_into(x, wp, s, layout, ldw, y, out_dtype, cfg, x_tiled)
+                    torch.cuda.synchronize()
+                    assert torch.equal(bits(y[:, :N]), bits(ref)), (N, out_dtype, layout, cfg, x_tiled)
+                    assert torch.isnan(y[:, N:].float()).all(), (N, out_dtype, layout, cfg, x_tiled)
+
+
+@pytest.mark.parametrize("M,K", [(1, 64), (15, 128), (16, 1024), (17, 5120), (300, 8192), (2048, 5120),
+                                 (33, 17408)])
+def test_quantize_tokens_tiled_image(M, K):
+    """qf_quantize_tokens_int8_tiled writes the same scales as the row-major quantiser and, byte for byte,
+    the token-tiled image of its xq (rows past M zero), over a buffer that starts filled with garbage."""
+    x, _, _ = random_case(M, 8, K, M + K)
+    x[M // 2] = 0
+    xq, s_a = qf.quantize_tokens_int8(x)
+    import ctypes
+    lib = L.load()
+    nbytes = int(lib.qf_tokens_tiled_bytes(M, K))
+    assert nbytes == (M + 15) // 16 * 16 * K
+    xt = torch.full((nbytes,), 85, dtype=torch.int8, device=DEV)
+    s_t = torch.full((M,), float("nan"), dtype=torch.float32, device=DEV)
+    L.check(lib.qf_quantize_tokens_int8_tiled(x.data_ptr(), K, M, K, xt.data_ptr(), s_t.data_ptr(),
+                                              torch.cuda.current_stream().cuda_stream), "tiled")
+    xt2, s_t2 = qf.quantize_tokens_int8(x, tiled=True)
+    torch.cuda.synchronize()
+    assert torch.equal(s_t, s_a) and torch.equal(s_t2, s_a)
+    assert torch.equal(xt, tile_tokens(xq)) and torch.equal(xt2, xt)
+    assert int(lib.qf_tokens_tiled_bytes(M, K + 1)) == 0 and int(lib.qf_tokens_tiled_bytes(0, K)) == 0
+
+
+@pytest.mark.parametrize("nt,waves,depth", W8A8_SHAPES)
+def test_w8a8_xt_wide_kernel_configs(nt, waves, depth):
+    """The wide kernel reads the token-tiled image as the row-major activations: every instantiated
+    shape, 1..8 token tiles, several groups, K splits, both weight layouts where served, bit for bit."""
+    N, K = 1000, 1024
+    x, w, s = random_case(300, N, K, 29 + nt + waves + depth)
+    wt = qf.to_tiled(w.t())
+    for M in (1, 16, 20, 100, 160, 300):
+        ref = P.w8a8_reference(x[:M], w.t(), s, None, torch.bfloat16)
+        for split in (1, 3):
+            cfg = (L.KERNEL_MFMA_W8A8, split, nt, waves, depth, 1, 1, 1)
+            y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+            w8a8_into(x[:M], wt, s, qf.TILED, 0, y, torch.bfloat16, cfg, True)
+            torch.cuda.synchronize()
+            assert torch.equal(bits(y), bits(ref)), (nt, waves, depth, M, split)
+    for M in (17, 128, 300):  # row-major weights: the automatic shape
+        ref = P.w8a8_reference(x[:M], w.t(), s, None, torch.float32)
+        y = torch.empty((M, N), dtype=torch.float32, device=DEV)
+        w8a8_into(x[:M], w, s, qf.ROWMAJOR, K, y, torch.float32, (0, 0, 0, 0, 0, 0, 0, 0), True)
+        torch.cuda.synchronize()
+        assert torch.equal(bits(y), bits(ref)), ("rowmajor", M)
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 34816, 5120), (17, 1000, 2048), (768, 34816, 5120), (333, 5120, 17408)])
+def test_w8a8_mm_activation_layouts_agree(M, N, K):
+    """w8a8_mm with the activations in either layout, and with the automatic choice, gives the same bits."""
+    x, w, s = random_case(M, N, K, M ^ N)
+    wt = qf.to_tiled(w.t())
+    ys = [qf.w8a8_mm(x, wt, s, torch.bfloat16, x_tiled=t) for t in (None, False, True)]
+    torch.cuda.synchronize()
+    assert all(torch.equal(bits(ys[0]), bits(y)) for y in ys[1:]), (M, N, K)
