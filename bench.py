@@ -629,11 +629,19 @@ def run_prefill(torch, qf, dev, args):
     log(f"  prefill gate_up M= 2048 vendor int8 GEMM (torch._int_mm): {us_v:.1f} us {tops_v:.1f} TOPS")
     del wrm
     # The tile kernel's call is two launches when its workgroups pass whole rounds of 256 by at most 64
-    # (reduce 0): the whole rounds' channel blocks, then the rest on the wide kernel.
-    tile_wgs = -(-N // 256) * -(-M // 256)
-    tail = cfg.reduce == 0 and tile_wgs > 256 and 0 < tile_wgs % 256 <= 64 and (tile_wgs // 256 * 256) % -(-M // 256) == 0
-    tile_name = ("w8a8_tile_kernel + w8a8_wide_kernel on the last channels" if tail else "w8a8_tile_kernel") + \
-        ", token-tiled activations"
+    # (reduce 0): the whole rounds' channel blocks, then the rest on 128 x 128 tile workgroups when they
+    # make one round of 128 to 256, else on the wide kernel.
+    mb = -(-M // 256)
+    tile_wgs = -(-N // 256) * mb
+    whole = tile_wgs // 256 * 256
+    tail = cfg.reduce == 0 and whole > 0 and 0 < tile_wgs - whole <= 64 and whole % mb == 0
+    tile_name = "w8a8_tile_kernel"
+    if tail:
+        n_tail = N - whole // mb * 256
+        small = -(-(-(-n_tail // 16)) // 8) * -(-M // 128)
+        tile_name += (f" + {small} 128x128 tile workgroups on the last {n_tail} channels" if 128 <= small <= 256
+                      else f" + w8a8_wide_kernel on the last {n_tail} channels")
+    tile_name += ", token-tiled activations"
     roofline = {"bound": "mfma", "achieved": round(tops_k, 1), "peak": 5000.0, "unit": "TOPS",
                 "frac": round(tops_k / 5000.0, 4), "traffic": read_traffic(W8A8_PROFILE),
                 "kernel": (f"{tile_name if cfg.kernel == QL.KERNEL_MFMA_W8A8_TILE else 'w8a8_wide_kernel'} "

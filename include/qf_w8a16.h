@@ -85,9 +85,11 @@ typedef enum qf_kernel {
   QF_KERNEL_MFMA_W8A8_TILE = 6 /* qf_w8a8_gemm only, either layout, picked for large M x N: 256-channel x
                                256-token workgroups, both operands staged in LDS by direct-to-LDS copies
                                through a 4-stage ring; waves 8, tiles_per_wave 8, depth 4, split_k 1;
-                               reduce 0: a last round of at most 64 workgroups past whole rounds of 256
-                               runs its channels on the QF_KERNEL_MFMA_W8A8 kernel (a second launch),
-                               reduce 1: one launch */
+                               past whole rounds of 256 workgroups, a last round of at most 64 runs its
+                               channels in a second launch: reduce 0 (automatic) on 128 x 128 workgroups
+                               of the same kernel where they make one round of 128 to 256, else on the
+                               QF_KERNEL_MFMA_W8A8 kernel; reduce 2 on the latter only; reduce 1: one
+                               launch */
 } qf_kernel;
 
 /* Launch configuration.  A zero field means "choose automatically". */

@@ -1208,17 +1208,37 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
-template <int LAYOUT>
+// Workgroup tile shapes: FA weight fragments by FB = FA / 2 activation fragments a wavefront, 8 wavefronts
+// in 2 channel x 4 token groups, so 32 FA channels x 32 FA tokens a workgroup: FA = 8 is the 256 x 256
+// main shape, FA = 4 the 128 x 128 shape that runs the channels past the main grid's whole rounds.
+template <int FA>
+struct TileShape {
+  static constexpr int FB = FA / 2;
+  static constexpr int tiles = 2 * FA;            // 16-channel weight tiles a workgroup
+  static constexpr int frags = 2 * FA;            // 16-token activation fragments a workgroup
+  static constexpr int rows = 16 * frags;         // tokens a workgroup
+  static constexpr int copies = FA / 2;           // fragments a wavefront copies a stage
+  static constexpr int stage_bytes = (tiles + frags) * 1024;
+  // 4 stages for the main shape; 6 for the small one, which also keeps it at one workgroup a CU
+  // (96 KiB), so that a grid of 256 spreads over all CUs.
+  static constexpr int stages = FA == 8 ? kW8A8TileStages : 6;
+  static constexpr int lds = stages * stage_bytes;
+};
+
+template <int LAYOUT, int FA>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
     w8a8_tile_kernel(const GemmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
-  constexpr int S = kW8A8TileStages;
+  using T = TileShape<FA>;
+  constexpr int FB = T::FB;
+  constexpr int S = T::stages;
+  constexpr int CP = T::copies;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int wn = wave & 1, wm = wave >> 1;
   const int g = lane >> 4, r = lane & 15;
   const int ntiles = a.n_pad / kTileN;
-  const int mblocks = (a.M + kW8A8TileRows - 1) / kW8A8TileRows;
+  const int mblocks = (a.M + T::rows - 1) / T::rows;
   // The hardware hands workgroup i to XCD i % kXcds; consecutive logical blocks share an XCD, so the
   // token blocks of one channel block run together and share its weights in that XCD's L2.
   int l;
@@ -1228,19 +1248,19 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int per = total / kXcds, rem = total % kXcds;
     l = xcd < rem ? xcd * (per + 1) + j : rem * (per + 1) + (xcd - rem) * per + j;
   }
-  const int tile0 = (l / mblocks) * kW8A8TileTiles;
-  const int m0 = (l % mblocks) * kW8A8TileRows;
+  const int tile0 = (l / mblocks) * T::tiles;
+  const int m0 = (l % mblocks) * T::rows;
   const int ksteps = a.ksteps;
 
-  // Wavefronts 0..3 copy the weight fragments 4 wave .. 4 wave + 3, wavefronts 4..7 the activation
-  // fragments 4 (wave - 4) .. + 3.  Channels and tokens past the matrix read its last row instead; their
-  // outputs are never stored.
-  const int8_t* src[4];
+  // Wavefronts 0..3 copy the weight fragments CP wave .. CP wave + CP - 1, wavefronts 4..7 the
+  // activation fragments CP (wave - 4) .. + CP - 1.  Channels and tokens past the matrix read its last
+  // row (block) instead; their outputs are never stored.
+  const int8_t* src[CP];
   int64_t adv;  // bytes between the same fragment of consecutive steps
   if (wave < 4) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = min(tile0 + 4 * wave + j, ntiles - 1);
+    for (int j = 0; j < CP; ++j) {
+      const int t = min(tile0 + CP * wave + j, ntiles - 1);
       if constexpr (LAYOUT == QF_LAYOUT_ROWMAJOR) {
         src[j] = a.w + (int64_t)min(t * kTileN + r, a.N - 1) * a.ldw + 16 * g;
       } else {
@@ -1251,15 +1271,15 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
   } else if (a.x_tiled) {  // uniform: one contiguous KiB per fragment, as the TILED weights
     const int last = (a.M - 1) >> 4;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int b = min((m0 >> 4) + 4 * (wave - 4) + j, last);
+    for (int j = 0; j < CP; ++j) {
+      const int b = min((m0 >> 4) + CP * (wave - 4) + j, last);
       src[j] = a.xq + ((int64_t)b * ksteps * kWave + lane) * 16;
     }
     adv = kTileN * kStepK;
   } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = min(m0 + 16 * (4 * (wave - 4) + j) + r, a.M - 1);
+    for (int j = 0; j < CP; ++j) {
+      const int row = min(m0 + 16 * (CP * (wave - 4) + j) + r, a.M - 1);
       src[j] = a.xq + (int64_t)row * a.ldx + 16 * g;
     }
     adv = kStepK;
@@ -1268,18 +1288,18 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
   // into a slot whose stage every wavefront has consumed, so every iteration issues exactly one group
   // and the vmcnt waits are constants.
   auto copy = [&](int s) {
-    uint8_t* slot = smem + (s % S) * kW8A8TileStageBytes + wave * 4 * 1024;
+    uint8_t* slot = smem + (s % S) * T::stage_bytes + wave * CP * 1024;
     const int64_t off = (int64_t)min(s, ksteps - 1) * adv;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < CP; ++j)
       __builtin_amdgcn_global_load_lds((glb_ptr_t)(src[j] + off), (lds_ptr_t)(slot + j * 1024), 16, 0, 0);
   };
-  auto read_frags = [&](int s, i32x4_t (&A)[8], i32x4_t (&B)[4]) {
-    const uint8_t* slot = smem + (s % S) * kW8A8TileStageBytes + lane * 16;
+  auto read_frags = [&](int s, i32x4_t (&A)[FA], i32x4_t (&B)[FB]) {
+    const uint8_t* slot = smem + (s % S) * T::stage_bytes + lane * 16;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) A[i] = *reinterpret_cast<const i32x4_t*>(slot + (8 * wn + i) * 1024);
+    for (int i = 0; i < FA; ++i) A[i] = *reinterpret_cast<const i32x4_t*>(slot + (FA * wn + i) * 1024);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) B[i] = *reinterpret_cast<const i32x4_t*>(slot + (16 + 4 * wm + i) * 1024);
+    for (int i = 0; i < FB; ++i) B[i] = *reinterpret_cast<const i32x4_t*>(slot + (T::tiles + FB * wm + i) * 1024);
   };
   // The ring barrier: every wavefront has waited for its own copies of the stage before it; the acquire
   // keeps the stage's reads after it.  (A release fence would wait for the copies still in flight, which
@@ -1289,31 +1309,31 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
   };
 
-  i32x4_t acc[8][4];
+  i32x4_t acc[FA][FB];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < FA; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = (i32x4_t){0, 0, 0, 0};
+    for (int j = 0; j < FB; ++j) acc[i][j] = (i32x4_t){0, 0, 0, 0};
 
 #pragma unroll
   for (int s = 0; s < S - 1; ++s) copy(s);
-  wait_vmcnt<4 * (S - 2)>();  // groups 1 .. S - 2 may still be in flight: stage 0 has landed
+  wait_vmcnt<CP * (S - 2)>();  // groups 1 .. S - 2 may still be in flight: stage 0 has landed
   ring_barrier();
-  i32x4_t fa[8], fb[4], ga[8], gb[4];
+  i32x4_t fa[FA], fb[FB], ga[FA], gb[FB];
   read_frags(0, fa, fb);
   // Step s: stage s + 1 becomes readable at the barrier (S - 3 groups were issued after its group), the
   // slot of stage s - 1 is refilled with group s + S - 1, the fragments of step s + 1 are read into
   // (na, nb) while the MFMAs of step s run on (ca, cb).  Unrolled by two so the fragment sets alternate
   // without copies.
-  auto step = [&](int s, i32x4_t (&ca)[8], i32x4_t (&cb)[4], i32x4_t (&na)[8], i32x4_t (&nb)[4]) {
-    wait_vmcnt<4 * (S - 3)>();
+  auto step = [&](int s, i32x4_t (&ca)[FA], i32x4_t (&cb)[FB], i32x4_t (&na)[FA], i32x4_t (&nb)[FB]) {
+    wait_vmcnt<CP * (S - 3)>();
     ring_barrier();
     copy(s + S - 1);
     read_frags(min(s + 1, ksteps - 1), na, nb);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < FA; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ca[i], cb[j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < FB; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ca[i], cb[j], acc[i][j], 0, 0, 0);
   };
   int s = 0;
   for (; s + 1 < ksteps; s += 2) {
@@ -1323,21 +1343,24 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
   if (s < ksteps) step(s, fa, fb, ga, gb);
   wait_vmcnt<0>();  // the last groups' copies have landed before LDS is reused or released
 
-  // Lane (g, r) holds C[n = 16 (tile0 + 8 wn + i) + 4 g + e][m = m0 + 64 wm + 16 j + r], e = 0..3.
+  // Lane (g, r) holds C[n = 16 (tile0 + FA wn + i) + 4 g + e][m = m0 + 16 FB wm + 16 j + r], e = 0..3.
   const bool staged = !a.out_f32 && a.vec_out && (a.ldy % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
   if (staged) {
-    // Each wavefront's 64 x 128 bf16 block goes to its own 16 KiB of LDS: row t, 16-byte chunk c at
-    // t * 256 + ((c ^ (t & 15)) << 4), so the 8-byte writes and the 16-byte reads are conflict-free.
+    // Each wavefront's 16 FB x 16 FA bf16 block goes to its own LDS: token row t (NC 16-byte chunks), chunk
+    // c at t * 16 NC + ((c ^ (t % NC)) << 4), so the 8-byte writes and 16-byte reads spread over the banks.
+    constexpr int NC = 2 * FA;                 // 16-byte chunks a token row
+    constexpr int BLK = 16 * FB * 16 * NC;     // bytes a wavefront
+    static_assert(8 * BLK <= T::lds, "epilogue staging fits the ring");
     __syncthreads();  // every wavefront is done with the ring
-    uint8_t* blk = smem + wave * 16384;
+    uint8_t* blk = smem + wave * BLK;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int n = (tile0 + 8 * wn + i) * kTileN + 4 * g;
+    for (int i = 0; i < FA; ++i) {
+      const int n = (tile0 + FA * wn + i) * kTileN + 4 * g;
       const f32x4_t sc = load_scale4(a.scale, a.N, min(n, a.n_pad - 4));
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < FB; ++j) {
         const int t = 16 * j + r;
-        const float st = a.s_tok[min(m0 + 64 * wm + t, a.M - 1)];
+        const float st = a.s_tok[min(m0 + 16 * FB * wm + t, a.M - 1)];
         const i32x4_t v = acc[i][j];
         const f32x4_t f = {(float)v.x, (float)v.y, (float)v.z, (float)v.w};
         const f32x4_t o = (f * st) * sc;
@@ -1345,37 +1368,40 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
         p.x = pack_bf16_rne(o.x, o.y);
         p.y = pack_bf16_rne(o.z, o.w);
         const int c = 2 * i + (g >> 1);
-        *reinterpret_cast<u32x2_t*>(blk + t * 256 + ((c ^ (t & 15)) << 4) + 8 * (g & 1)) = p;
+        *reinterpret_cast<u32x2_t*>(blk + t * 16 * NC + ((c ^ (t % NC)) << 4) + 8 * (g & 1)) = p;
       }
     }
-    const int c = lane & 15;
-    const int n0 = (tile0 + 8 * wn) * kTileN + 8 * c;  // the first of this lane's 8 channels
+    const int c = lane % NC;
+    const int n0 = (tile0 + FA * wn) * kTileN + 8 * c;  // the first of this lane's 8 channels
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int t = 4 * q + (lane >> 4);
-      const int m = m0 + 64 * wm + t;
-      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(blk + t * 256 + ((c ^ (t & 15)) << 4));
+    for (int q = 0; q < 16 * FB * NC / kWave; ++q) {
+      const int t = (kWave / NC) * q + lane / NC;
+      const int m = m0 + 16 * FB * wm + t;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(blk + t * 16 * NC + ((c ^ (t % NC)) << 4));
       if (m < a.M) {
         uint16_t* row = reinterpret_cast<uint16_t*>(a.y) + (int64_t)m * a.ldy + n0;
         if (n0 + 8 <= a.N) {
           *reinterpret_cast<u32x4_t*>(row) = v;
         } else if (n0 < a.N) {
-          const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
-          for (int k = 0; k < a.N - n0; ++k) row[k] = e[k];
+          const int cnt = a.N - n0;  // 1 .. 7
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {  // constant element indices: v stays in registers
+            if (k < cnt) row[k] = (uint16_t)(v[k >> 1] >> (16 * (k & 1)));
+          }
         }
       }
     }
     return;
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int tile = tile0 + 8 * wn + i;
+  for (int i = 0; i < FA; ++i) {
+    const int tile = tile0 + FA * wn + i;
     const int n = tile * kTileN + 4 * g;
     if (tile < ntiles && n < a.N) {
       const f32x4_t sc = load_scale4(a.scale, a.N, n);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int m = m0 + 64 * wm + 16 * j + r;
+      for (int j = 0; j < FB; ++j) {
+        const int m = m0 + 16 * FB * wm + 16 * j + r;
         if (m < a.M) {
           const i32x4_t v = acc[i][j];
           const f32x4_t f = {(float)v.x, (float)v.y, (float)v.z, (float)v.w};
@@ -2590,7 +2616,8 @@ int64_t w8a8_tile_workgroups(int M, int N) {
 int validate_w8a8(int M, int N, int K, int layout, const qf_w8a16_config& c) {
   const int ksteps = K / kStepK;
   if (c.kernel == QF_KERNEL_MFMA_W8A8_TILE) {
-    if (c.split_k != 1 || c.waves != 8 || c.tiles_per_wave != 8 || c.depth != kW8A8TileStages || c.k_waves != 1)
+    if (c.split_k != 1 || c.waves != 8 || c.tiles_per_wave != 8 || c.depth != kW8A8TileStages || c.k_waves != 1 ||
+        c.reduce < 0 || c.reduce > 2)
       return QF_ERR_INVALID_ARG;
     if ((layout != QF_LAYOUT_TILED && layout != QF_LAYOUT_ROWMAJOR) || K >= 132000) return QF_ERR_UNSUPPORTED;
     return w8a8_tile_workgroups(M, N) > 0x7fffffff ? QF_ERR_UNSUPPORTED : QF_OK;
@@ -2627,16 +2654,19 @@ bool auto_config_w8a8(int M, int N, int K, int layout, qf_w8a16_config* c) {
   c->waves = 8;
   c->depth = 4;
   // The LDS-tiled kernel once its 256 x 256 workgroups number 136 or more, unless they spill a few
-  // (<= 16) past a whole round of 256 (measured on the four layer shapes at M = 256 .. 4096: 10-33%
-  // faster there, e.g. gate_up M = 2048 377 against 420 us, down M = 2048 173 against 238 us, and
-  // gate_up M = 1024 (544 workgroups) 227 against 245 us; slower with fewer workgroups, where the
-  // shapes below split K, and at 272 workgroups, gate_up M = 512 152 against 137 us).  Its token
-  // blocks are 256 rows whatever M is, so it also needs M >= 256 with at most a quarter of the rows it
-  // computes past M.
+  // (<= 16) past a whole round of 256 that the second launch of run_w8a8 cannot take (measured on the
+  // four layer shapes at M = 256 .. 4096 with token-tiled activations against the shapes below: gate_up
+  // M = 512 (272 workgroups, the last 16 on the wide kernel) 107 against 148 us, M = 2048 301 against
+  // 420; slower with fewer workgroups, where the shapes below split K: down M = 1024 (80) 172 against
+  // 152, o_proj M = 1536 (120) 91 against 87).  Its token blocks are 256 rows whatever M is, so it also
+  // needs M >= 256 with under a quarter of the rows it computes past M (gate_up M = 384: 109 against 102).
   const int64_t twgs = w8a8_tile_workgroups(M, N);
-  const int64_t tile_rows = (int64_t)ceil_div(M, kW8A8TileRows) * kW8A8TileRows;
-  if (K < 132000 && M >= kW8A8TileRows && 4 * (int64_t)M >= 3 * tile_rows && twgs >= 136 &&
-      !(twgs > 256 && twgs % 256 != 0 && twgs % 256 <= 16)) {
+  const int mblocks = ceil_div(M, kW8A8TileRows);
+  const int64_t tile_rows = (int64_t)mblocks * kW8A8TileRows;
+  const int64_t rest = twgs % 256, whole = twgs - rest;
+  const bool second_launch = whole > 0 && rest <= 64 && whole % mblocks == 0;
+  if (K < 132000 && M >= kW8A8TileRows && 4 * (int64_t)M > 3 * tile_rows && twgs >= 136 &&
+      !(whole > 0 && rest != 0 && rest <= 16 && !second_launch)) {
     c->kernel = QF_KERNEL_MFMA_W8A8_TILE;
     c->tiles_per_wave = 8;
     c->waves = 8;
@@ -2730,18 +2760,33 @@ int run_w8a8(const int8_t* xq, int64_t ldq, int x_tiled, const float* s_a, const
   a.vec_out = (ldy % 4) == 0;
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (c.kernel == QF_KERNEL_MFMA_W8A8_TILE) {
-    KernelFn tf = layout == QF_LAYOUT_ROWMAJOR ? &w8a8_tile_kernel<QF_LAYOUT_ROWMAJOR> : &w8a8_tile_kernel<QF_LAYOUT_TILED>;
-    // Tail (reduce == 0): when the 256 x 256 workgroups fill whole rounds of 256 and then a quarter round
-    // or less, the channel blocks of the whole rounds run here and the remaining channels on the wide
-    // kernel, a second launch on the same stream (gate_up M = 2048: 1024 + 64 workgroups, 360 against
-    // 378 us in one launch).  Both write disjoint output columns; the sums are exact, so the result is
-    // the same.
+    const bool rm = layout == QF_LAYOUT_ROWMAJOR;
+    KernelFn tf = rm ? &w8a8_tile_kernel<QF_LAYOUT_ROWMAJOR, 8> : &w8a8_tile_kernel<QF_LAYOUT_TILED, 8>;
+    // Tail (reduce 0 or 2): when the 256 x 256 workgroups fill whole rounds of 256 and then a quarter round
+    // or less, the channel blocks of the whole rounds run here and the remaining channels in a second
+    // launch on the same stream: one round of 128 x 128 workgroups of the same kernel where they number 128
+    // to 256 (reduce 0), else (or with reduce 2) the wide kernel.  Token-tiled activations, gate_up
+    // M = 2048 (1024 workgroups, 2048 channels left): 304.5 us, 323.1 with the wide kernel's tail, 316.3 in
+    // one launch; qkv M = 2048: 92.1 / 112.9 / 111.9 us.  Past a quarter round one launch is faster (gate_up
+    // M = 4096, 128 past 2048: 600 us, 613 with two rounds of 128 x 128 workgroups).
+    // Both launches write disjoint output columns; the sums are exact, so the result is the same.
     const int nblocks = ceil_div(a.n_pad / kTileN, kW8A8TileTiles);
     const int mblocks = ceil_div(M, kW8A8TileRows);
     const int64_t twgs = (int64_t)nblocks * mblocks;
     const int64_t whole = twgs / 256 * 256;
-    if (c.reduce == 0 && whole > 0 && twgs - whole <= 64 && whole % mblocks == 0) {
+    if (c.reduce != 1 && whole > 0 && twgs - whole <= 64 && whole % mblocks == 0) {
       const int n_main = (int)(whole / mblocks) * kW8A8TileTiles * kTileN;  // < N: the tail holds N's last block
+      const int n_tail = N - n_main;
+      GemmArgs at = a;
+      at.N = n_tail;
+      at.n_pad = round_up16(n_tail);
+      at.w = a.w + (layout == QF_LAYOUT_TILED ? (int64_t)(n_main / kTileN) * a.ksteps * kTileN * kStepK
+                                              : (int64_t)n_main * a.ldw);
+      at.scale = a.scale + n_main;
+      at.y = reinterpret_cast<uint8_t*>(a.y) + (size_t)n_main * (a.out_f32 ? 4 : 2);
+      using Small = TileShape<4>;
+      const int64_t small = (int64_t)ceil_div(at.n_pad / kTileN, Small::tiles) * ceil_div(M, Small::rows);
+      const bool use_small = c.reduce == 0 && small >= 128 && small <= 256;
       qf_w8a16_config ct = qf_w8a16_config{};
       ct.kernel = QF_KERNEL_MFMA_W8A8;
       ct.k_waves = 1;
@@ -2751,28 +2796,25 @@ int run_w8a8(const int8_t* xq, int64_t ldq, int x_tiled, const float* s_a, const
       ct.tiles_per_wave = 2;
       ct.waves = 8;
       ct.depth = 4;
-      const int n_tail = N - n_main;
-      if (auto_config_w8a8_wide(M, n_tail, K, layout, &ct)) {
+      bool use_wide = false;
+      if (!use_small && auto_config_w8a8_wide(M, n_tail, K, layout, &ct)) {
         ct.split_k = 1;  // no workspace: the tail runs unsplit
-        if (validate_w8a8(M, n_tail, K, layout, ct) == QF_OK) {
-          GemmArgs am = a;
-          am.N = n_main;
-          am.n_pad = n_main;
-          int st = launch(tf, dim3((unsigned)whole), dim3(8 * kWave), kW8A8TileLds, s, am);
-          if (st != QF_OK) return st;
-          GemmArgs at = a;
-          at.N = n_tail;
-          at.n_pad = round_up16(n_tail);
-          at.w = a.w + (layout == QF_LAYOUT_TILED ? (int64_t)(n_main / kTileN) * a.ksteps * kTileN * kStepK
-                                                  : (int64_t)n_main * a.ldw);
-          at.scale = a.scale + n_main;
-          at.y = reinterpret_cast<uint8_t*>(a.y) + (size_t)n_main * (a.out_f32 ? 4 : 2);
-          w8a8_groups(ct, M, n_tail, at.groups, at.group_rows);
-          KernelFn fn = select_w8a8(layout, ct.tiles_per_wave, at.group_rows / 16, ct.waves, ct.depth);
-          if (fn == nullptr) return QF_ERR_UNSUPPORTED;
-          return launch(fn, dim3(workgroups(ct, n_tail) * at.groups), dim3(ct.waves * kWave),
-                        w8a8_lds_bytes(ct, M, n_tail), s, at);
-        }
+        use_wide = validate_w8a8(M, n_tail, K, layout, ct) == QF_OK;
+      }
+      if (use_small || use_wide) {
+        GemmArgs am = a;
+        am.N = n_main;
+        am.n_pad = n_main;
+        const int st = launch(tf, dim3((unsigned)whole), dim3(8 * kWave), kW8A8TileLds, s, am);
+        if (st != QF_OK) return st;
+        if (use_small)
+          return launch(rm ? &w8a8_tile_kernel<QF_LAYOUT_ROWMAJOR, 4> : &w8a8_tile_kernel<QF_LAYOUT_TILED, 4>,
+                        dim3((unsigned)small), dim3(8 * kWave), Small::lds, s, at);
+        w8a8_groups(ct, M, n_tail, at.groups, at.group_rows);
+        KernelFn fn = select_w8a8(layout, ct.tiles_per_wave, at.group_rows / 16, ct.waves, ct.depth);
+        if (fn == nullptr) return QF_ERR_UNSUPPORTED;
+        return launch(fn, dim3(workgroups(ct, n_tail) * at.groups), dim3(ct.waves * kWave),
+                      w8a8_lds_bytes(ct, M, n_tail), s, at);
       }
     }
     return launch(tf, dim3((unsigned)twgs), dim3(8 * kWave), kW8A8TileLds, s, a);

@@ -268,11 +268,13 @@ def test_w8a8_configs_host_only():
                     assert c.kernel == L.KERNEL_MFMA_W8A8, (M, N, K, layout)
                     if layout == 0:
                         assert c.to_tuple()[2:5] == (2, 8, 4), (M, N, K)
-    # The tile kernel's rule: 136 or more workgroups, not 1-16 past a whole round, M >= 256 with at most
-    # a quarter of the computed rows past M.
+    # The tile kernel's rule: 136 or more workgroups, not 1-16 past a whole round unless the second launch
+    # takes them, M >= 256 with under a quarter of the computed rows past M.
     assert L.w8a8_pick_config(256, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8_TILE      # 136 workgroups
     assert L.w8a8_pick_config(255, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8           # M < 256
-    assert L.w8a8_pick_config(512, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8           # 272 = 256 + 16
+    assert L.w8a8_pick_config(384, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8           # 384 of 512 rows
+    assert L.w8a8_pick_config(512, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8_TILE      # 272 = 256 + 16, split
+    assert L.w8a8_pick_config(3328, 10240, 5120).kernel == L.KERNEL_MFMA_W8A8          # 520 = 512 + 8, 13 blocks
     assert L.w8a8_pick_config(768, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8_TILE      # 408
     assert L.w8a8_pick_config(1024, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8_TILE     # 544 = 512 + 32
     assert L.w8a8_pick_config(513, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8           # 513 of 768 rows

@@ -322,26 +322,33 @@ def test_w8a8_tile_kernel_auto_layer_shapes(name, M, N, K):
     assert torch.equal(bits(y), bits(ref)) and torch.equal(bits(y_r), bits(ref)), name
 
 
-@pytest.mark.parametrize("N", [4352, 4344])
-def test_w8a8_tile_kernel_tail_split(N):
-    """reduce = 0 on the tile kernel: 17 channel blocks x 16 token blocks = 272 workgroups, so the first 16
-    channel blocks run on the tile kernel (one whole round) and the last block's channels (N ragged or
-    not) on the wide kernel, a second launch writing the same output at a column offset.  Bit for bit
-    equal to the single launch and to the restatement, on both layouts, bf16 and fp32 outputs."""
-    M, K = 4096, 256
-    x, w, s = random_case(M, N, K, N)
+@pytest.mark.parametrize("N,K", [(4352, 256), (4344, 256), (4700, 128), (4616, 192)])
+def test_w8a8_tile_kernel_tail_split(N, K):
+    """The tile kernel's second launch past whole rounds of 256 workgroups (M = 4096: 16 token blocks).
+    N = 4352 / 4344: 17 channel blocks, 272 workgroups; the last block's channels (ragged or not) run on
+    the wide kernel (reduce 0 and 2: too few for 128 x 128 workgroups).  N = 4700 / 4616: 19 blocks, 304
+    workgroups; the 604 / 520 channels past the first 16 blocks run on 128 x 128 workgroups of the tile
+    kernel (reduce 0, 160 of them; N = 4700 ends in a partial chunk of 8 channels) or on the wide kernel
+    (reduce 2).
+    Each writes the same output at a column offset.  Bit for bit equal to the single launch (reduce 1)
+    and to the restatement, on both layouts, row-major and token-tiled activations, bf16 rows staged
+    (ldy % 8 == 0) or not, and fp32 outputs."""
+    M = 4096
+    x, w, s = random_case(M, N, K, N + K)
     wt = qf.to_tiled(w.t())
-    split = (L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 4, 1, 1, 0)
+    cfgs = [(L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 4, 1, 1, red) for red in (0, 2)] + [TILE_CFG]
     for out_dtype in (torch.bfloat16, torch.float32):
         ref = P.w8a8_reference(x, w.t(), s, None, out_dtype)
         for layout, wp, ldw in ((qf.TILED, wt, 0), (qf.ROWMAJOR, w, K)):
-            for cfg in (split, TILE_CFG):
+            for cfg in cfgs:
                 for x_tiled in (False, True):
-                    y = torch.full((M, N + 8), float("nan"), dtype=out_dtype, device=DEV)
-                    w8a8_into(x, wp, s, layout, ldw, y, out_dtype, cfg, x_tiled)
-                    torch.cuda.synchronize()
-                    assert torch.equal(bits(y[:, :N]), bits(ref)), (N, out_dtype, layout, cfg, x_tiled)
-                    assert torch.isnan(y[:, N:].float()).all(), (N, out_dtype, layout, cfg, x_tiled)
+                    for pad in ((8, 4) if out_dtype == torch.bfloat16 else (8,)):
+                        y = torch.full((M, N + pad), float("nan"), dtype=out_dtype, device=DEV)
+                        w8a8_into(x, wp, s, layout, ldw, y, out_dtype, cfg, x_tiled)
+                        torch.cuda.synchronize()
+                        case = (N, K, out_dtype, layout, cfg, x_tiled, pad)
+                        assert torch.equal(bits(y[:, :N]), bits(ref)), case
+                        assert torch.isnan(y[:, N:].float()).all(), case
 
 
 @pytest.mark.parametrize("M,K", [(1, 64), (15, 128), (16, 1024), (17, 5120), (300, 8192), (2048, 5120),
