@@ -322,18 +322,17 @@ def test_w8a8_tile_kernel_auto_layer_shapes(name, M, N, K):
     assert torch.equal(bits(y), bits(ref)) and torch.equal(bits(y_r), bits(ref)), name
 
 
-@pytest.mark.parametrize("N,K", [(4352, 256), (4344, 256), (4700, 128), (4616, 192)])
-def test_w8a8_tile_kernel_tail_split(N, K):
+@pytest.mark.parametrize("M,N,K", [(4096, 4352, 256), (4096, 4344, 256), (4096, 4700, 128), (4000, 4616, 192)])
+def test_w8a8_tile_kernel_tail_split(M, N, K):
     """The tile kernel's second launch past whole rounds of 256 workgroups (M = 4096: 16 token blocks).
     N = 4352 / 4344: 17 channel blocks, 272 workgroups; the last block's channels (ragged or not) run on
     the wide kernel (reduce 0 and 2: too few for 128 x 128 workgroups).  N = 4700 / 4616: 19 blocks, 304
     workgroups; the 604 / 520 channels past the first 16 blocks run on 128 x 128 workgroups of the tile
     kernel (reduce 0, 160 of them; N = 4700 ends in a partial chunk of 8 channels) or on the wide kernel
     (reduce 2).
-    Each writes the same output at a column offset.  Bit for bit equal to the single launch (reduce 1)
-    and to the restatement, on both layouts, row-major and token-tiled activations, bf16 rows staged
-    (ldy % 8 == 0) or not, and fp32 outputs."""
-    M = 4096
+    Each writes the same output at a column offset.  M = 4000 leaves the last token blocks of both shapes
+    partial.  Bit for bit equal to the single launch (reduce 1) and to the restatement, on both layouts,
+    row-major and token-tiled activations, bf16 rows staged (ldy % 8 == 0) or not, and fp32 outputs."""
     x, w, s = random_case(M, N, K, N + K)
     wt = qf.to_tiled(w.t())
     cfgs = [(L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 4, 1, 1, red) for red in (0, 2)] + [TILE_CFG]
@@ -346,7 +345,7 @@ def test_w8a8_tile_kernel_tail_split(N, K):
                         y = torch.full((M, N + pad), float("nan"), dtype=out_dtype, device=DEV)
                         w8a8_into(x, wp, s, layout, ldw, y, out_dtype, cfg, x_tiled)
                         torch.cuda.synchronize()
-                        case = (N, K, out_dtype, layout, cfg, x_tiled, pad)
+                        case = (M, N, K, out_dtype, layout, cfg, x_tiled, pad)
                         assert torch.equal(bits(y[:, :N]), bits(ref)), case
                         assert torch.isnan(y[:, N:].float()).all(), case
 
