@@ -84,7 +84,10 @@ typedef enum qf_kernel {
                                activations; tiles_per_wave 2 or 4, 4 or 8 waves, depth 2 or 4 */
   QF_KERNEL_MFMA_W8A8_TILE = 6 /* qf_w8a8_gemm only, either layout, picked for large M x N: 256-channel x
                                256-token workgroups, both operands staged in LDS by direct-to-LDS copies
-                               through a 4-stage ring; waves 8, tiles_per_wave 8, depth 4, split_k 1;
+                               through a 4-stage ring; waves 8, tiles_per_wave 8, depth 4; split_k 1 to 8
+                               (at most K/64): split_k copies of the grid each sum a K range and the last
+                               of a tile's copies to arrive adds the others' int32 partials (workspace:
+                               256 KiB a workgroup) and writes the output, one launch; with split_k 1,
                                past whole rounds of 256 workgroups, a last round of at most 64 runs its
                                channels in a second launch: reduce 0 (automatic) on 128 x 128 workgroups
                                of the same kernel where they make one round of 128 to 256, else on the
@@ -236,8 +239,9 @@ int qf_quantize_tokens_int8(const uint16_t* x, int64_t ldx, int M, int K, int8_t
  * QF_KERNEL_MFMA_W8A8 shape only: 2 tiles, 8 waves, depth 4);
  * xq / s_a as written by qf_quantize_tokens_int8 (xq 16-byte aligned, ldq % 16 == 0); any M >= 1.
  * cfg may be NULL (automatic); its kernel must be QF_KERNEL_MFMA_W8A8, QF_KERNEL_MFMA_W8A8_TILE or AUTO.  Workspace
- * (qf_w8a8_workspace_bytes, 0 without a K split): the int32 split partials after the counter prefix, which
- * this path does not use; calls that may run at the same time need distinct workspaces.
+ * (qf_w8a8_workspace_bytes, 0 without a K split): the int32 split partials after the counter prefix; the
+ * counters (used by QF_KERNEL_MFMA_W8A8_TILE with a K split) must be zero before the first call and are
+ * left at zero by every call; calls that may run at the same time need distinct workspaces.
  * Reference: ops.cutlass_scaled_mm(x_q, w_q, scale_a, scale_b, out_dtype, bias=None) at
  * plugin/qwen_fastpath/patches.py:100 (the bias is added by the caller). */
 int qf_w8a8_gemm(const int8_t* xq, int64_t ldq, const float* s_a, const int8_t* w, int64_t ldw, int layout,

@@ -1200,6 +1200,7 @@ constexpr int kW8A8TileRows = 256;                        // tokens per workgrou
 constexpr int kW8A8TileTiles = 16;                        // 16-channel weight tiles per workgroup
 constexpr int kW8A8TileStageBytes = 32 * 1024;            // 16 weight + 16 activation fragments
 constexpr int kW8A8TileLds = kW8A8TileStages * kW8A8TileStageBytes;
+constexpr int kW8A8TileMaxSplit = 8;                      // K splits of the tile kernel (fused reduction)
 
 // s_waitcnt with vmcnt = n (0..63) and the other counters unconstrained.
 template <int N>
@@ -1229,6 +1230,7 @@ template <int LAYOUT, int FA>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
     w8a8_tile_kernel(const GemmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ int last_arrival;
   using T = TileShape<FA>;
   constexpr int FB = T::FB;
   constexpr int S = T::stages;
@@ -1248,6 +1250,14 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int per = total / kXcds, rem = total % kXcds;
     l = xcd < rem ? xcd * (per + 1) + j : rem * (per + 1) + (xcd - rem) * per + j;
   }
+  // split_k > 1: the grid is split_k copies of the tile grid, copy `split` computing k-steps
+  // [s_begin, s_end) of every tile.
+  const int tiles_grid = gridDim.x / a.split_k;
+  const int split = l / tiles_grid;
+  l -= split * tiles_grid;
+  int s_begin = 0, s_end = a.ksteps;
+  if (a.split_k > 1) split_range(split, a.split_k, a.ksteps, s_begin, s_end);
+  const int nsteps = s_end - s_begin;  // >= 1: split_k <= ksteps
   const int tile0 = (l / mblocks) * T::tiles;
   const int m0 = (l % mblocks) * T::rows;
   const int ksteps = a.ksteps;
@@ -1284,12 +1294,14 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
     adv = kStepK;
   }
+#pragma unroll
+  for (int j = 0; j < CP; ++j) src[j] += (int64_t)s_begin * adv;
   // Copy group s: stage min(s, ksteps - 1) into slot s % S.  Groups past the last stage copy it again
   // into a slot whose stage every wavefront has consumed, so every iteration issues exactly one group
   // and the vmcnt waits are constants.
   auto copy = [&](int s) {
     uint8_t* slot = smem + (s % S) * T::stage_bytes + wave * CP * 1024;
-    const int64_t off = (int64_t)min(s, ksteps - 1) * adv;
+    const int64_t off = (int64_t)min(s, nsteps - 1) * adv;
 #pragma unroll
     for (int j = 0; j < CP; ++j)
       __builtin_amdgcn_global_load_lds((glb_ptr_t)(src[j] + off), (lds_ptr_t)(slot + j * 1024), 16, 0, 0);
@@ -1329,19 +1341,72 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     wait_vmcnt<CP * (S - 3)>();
     ring_barrier();
     copy(s + S - 1);
-    read_frags(min(s + 1, ksteps - 1), na, nb);
+    read_frags(min(s + 1, nsteps - 1), na, nb);
 #pragma unroll
     for (int i = 0; i < FA; ++i)
 #pragma unroll
       for (int j = 0; j < FB; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ca[i], cb[j], acc[i][j], 0, 0, 0);
   };
   int s = 0;
-  for (; s + 1 < ksteps; s += 2) {
+  for (; s + 1 < nsteps; s += 2) {
     step(s, fa, fb, ga, gb);
     step(s + 1, ga, gb, fa, fb);
   }
-  if (s < ksteps) step(s, fa, fb, ga, gb);
+  if (s < nsteps) step(s, fa, fb, ga, gb);
   wait_vmcnt<0>();  // the last groups' copies have landed before LDS is reused or released
+
+  if (a.split_k > 1) {
+    // The splits of a tile meet through the workspace: each stores its int32 accumulators lane for lane
+    // (wavefront w's block of FA x FB fragments at slot (tile, split, w)) with device-scope stores and
+    // waits for them to complete; then one thread counts the arrival.  The last split to arrive reads the
+    // others' slots with device-scope loads, issued after its increment returned, adds them (exact in any
+    // order) and runs the epilogue; it returns the counter to zero.  The ordering is the hardware's, as in
+    // the decode kernel's fused split-K.
+    // A fragment's slot is 1 KiB: the lanes' (x, y) words in its first 512 bytes, their (z, w) words in the
+    // second, so each 8-byte-a-lane store or load covers 512 contiguous bytes (a 16-byte lane stride, half
+    // of every line per instruction: down 5120 x 17408 at M = 1024 in 3 splits 122.1 against 113.2 us).
+    // Plain stores with an agent-scope release fence and an acquire fence on the last arrival (an L2
+    // write-back and invalidate each) measured far slower: 157.6 us.
+    constexpr int kSlot = FA * FB * kWave * 4;  // int32 a wavefront
+    uint64_t* const tile_slots = reinterpret_cast<uint64_t*>(a.partial) + (int64_t)l * a.split_k * 8 * (kSlot / 2);
+    {
+      uint64_t* mine = tile_slots + ((int64_t)split * 8 + wave) * (kSlot / 2) + lane;
+#pragma unroll
+      for (int i = 0; i < FA; ++i)
+#pragma unroll
+        for (int j = 0; j < FB; ++j) {
+          uint64_t* p = mine + (i * FB + j) * 2 * kWave;
+          const i32x4_t v = acc[i][j];
+          __hip_atomic_store(p, (uint64_t)(uint32_t)v.x | ((uint64_t)(uint32_t)v.y << 32), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(p + kWave, (uint64_t)(uint32_t)v.z | ((uint64_t)(uint32_t)v.w << 32),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const unsigned prev = __hip_atomic_fetch_add(a.counters + l, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last_arrival = prev == (unsigned)(a.split_k - 1);
+    }
+    __syncthreads();
+    if (!last_arrival) return;
+    for (int o = 0; o < a.split_k; ++o) {
+      if (o == split) continue;
+      const uint64_t* theirs = tile_slots + ((int64_t)o * 8 + wave) * (kSlot / 2) + lane;
+#pragma unroll
+      for (int i = 0; i < FA; ++i)
+#pragma unroll
+        for (int j = 0; j < FB; ++j) {
+          const uint64_t* p = theirs + (i * FB + j) * 2 * kWave;
+          const uint64_t lo = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const uint64_t hi = __hip_atomic_load(p + kWave, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          acc[i][j] += (i32x4_t){(int)(uint32_t)lo, (int)(uint32_t)(lo >> 32), (int)(uint32_t)hi,
+                                 (int)(uint32_t)(hi >> 32)};
+        }
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(a.counters + l, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 
   // Lane (g, r) holds C[n = 16 (tile0 + FA wn + i) + 4 g + e][m = m0 + 16 FB wm + 16 j + r], e = 0..3.
   const bool staged = !a.out_f32 && a.vec_out && (a.ldy % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
@@ -2166,6 +2231,9 @@ int workgroups(const qf_w8a16_config& c, int N) {
 // land on memory an earlier call used for partial sums), then the split partials.
 size_t workspace_for(const qf_w8a16_config& c, int M, int N) {
   if (c.split_k <= 1) return 0;
+  if (c.kernel == QF_KERNEL_MFMA_W8A8_TILE)  // a 256 KiB int32 slot per (tile, split): 8 wavefronts x 32 KiB
+    return QF_W8A16_COUNTER_BYTES + (size_t)ceil_div(round_up16(N) / kTileN, kW8A8TileTiles) *
+                                        ceil_div(M, kW8A8TileRows) * c.split_k * (size_t)(256 * 1024);
   return QF_W8A16_COUNTER_BYTES + (size_t)c.split_k * (size_t)M * (size_t)round_up16(N) * sizeof(float);
 }
 
@@ -2616,11 +2684,15 @@ int64_t w8a8_tile_workgroups(int M, int N) {
 int validate_w8a8(int M, int N, int K, int layout, const qf_w8a16_config& c) {
   const int ksteps = K / kStepK;
   if (c.kernel == QF_KERNEL_MFMA_W8A8_TILE) {
-    if (c.split_k != 1 || c.waves != 8 || c.tiles_per_wave != 8 || c.depth != kW8A8TileStages || c.k_waves != 1 ||
-        c.reduce < 0 || c.reduce > 2)
+    if (c.split_k < 1 || c.split_k > kW8A8TileMaxSplit || c.waves != 8 || c.tiles_per_wave != 8 ||
+        c.depth != kW8A8TileStages || c.k_waves != 1 || c.reduce < 0 || c.reduce > 2)
       return QF_ERR_INVALID_ARG;
     if ((layout != QF_LAYOUT_TILED && layout != QF_LAYOUT_ROWMAJOR) || K >= 132000) return QF_ERR_UNSUPPORTED;
-    return w8a8_tile_workgroups(M, N) > 0x7fffffff ? QF_ERR_UNSUPPORTED : QF_OK;
+    const int64_t twgs = w8a8_tile_workgroups(M, N);
+    if (twgs * c.split_k > 0x7fffffff) return QF_ERR_UNSUPPORTED;
+    // A K split needs a step per split and one arrival counter per tile.
+    if (c.split_k > 1 && (c.split_k > ksteps || twgs * 4 > QF_W8A16_COUNTER_BYTES)) return QF_ERR_UNSUPPORTED;
+    return QF_OK;
   }
   if (c.kernel != QF_KERNEL_MFMA_W8A8) return QF_ERR_INVALID_ARG;
   if (c.split_k < 1 || c.split_k > ksteps || c.waves < 1 || c.k_waves < 1 || c.tiles_per_wave < 1)
@@ -2673,6 +2745,28 @@ bool auto_config_w8a8(int M, int N, int K, int layout, qf_w8a16_config* c) {
     c->depth = kW8A8TileStages;
     c->reduce = 0;  // the tile kernel's tail rule (run_w8a8)
     return validate_w8a8(M, N, K, layout, *c) == QF_OK;
+  }
+  // 40 to 128 256 x 256 workgroups (measured from 40), with two or more token blocks: the tile kernel with K split
+  // s = min(4, K / 2560, 256 / workgroups) ways (at least 40 k-steps a split) and the fused reduction.  Each
+  // split moves a 256 KiB int32 partial through memory, so short K and one token block stay below
+  // (token-tiled activations against the shapes below, us: down 5120 x 17408 at M = 512 / 768 / 1024 / 1536
+  // 77.3 / 97.0 / 113.2 / 146.3 against 106.5 / 110.4 / 149.8 / 169.4; o_proj 5120 x 8192 53.6 / 57.7 / 68.8
+  // / 81.3 against 55.9 / 56.7 / 79.4 / 87.0; qkv 10240 x 5120 at M = 512 / 768 49.8 / 59.6 against 54.5 /
+  // 59.4; at M = 256 the shapes below win: down 67 against 68, o_proj 43 against 48, qkv 38 against 43).
+  const int64_t sk = std::min<int64_t>(std::min(4, K / 2560), twgs > 0 ? 256 / twgs : 0);
+  if (K < 132000 && mblocks >= 2 && 4 * (int64_t)M > 3 * tile_rows && twgs >= 40 && twgs <= 128 && sk >= 2) {
+    c->kernel = QF_KERNEL_MFMA_W8A8_TILE;
+    c->split_k = (int)sk;
+    c->tiles_per_wave = 8;
+    c->waves = 8;
+    c->depth = kW8A8TileStages;
+    c->reduce = 0;
+    if (validate_w8a8(M, N, K, layout, *c) == QF_OK) return true;
+    c->split_k = 1;
+    c->kernel = QF_KERNEL_MFMA_W8A8;
+    c->tiles_per_wave = 2;
+    c->depth = 4;
+    c->reduce = 1;
   }
   return auto_config_w8a8_wide(M, N, K, layout, c);
 }
@@ -2747,6 +2841,7 @@ int run_w8a8(const int8_t* xq, int64_t ldq, int x_tiled, const float* s_a, const
   a.y = y;
   a.partial = need > 0 ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + QF_W8A16_COUNTER_BYTES)
                        : nullptr;
+  a.counters = need > 0 ? reinterpret_cast<unsigned*>(workspace) : nullptr;
   a.ldx = ldq;
   a.ldw = ldw;
   a.ldy = ldy;
@@ -2773,6 +2868,8 @@ int run_w8a8(const int8_t* xq, int64_t ldq, int x_tiled, const float* s_a, const
     const int nblocks = ceil_div(a.n_pad / kTileN, kW8A8TileTiles);
     const int mblocks = ceil_div(M, kW8A8TileRows);
     const int64_t twgs = (int64_t)nblocks * mblocks;
+    if (c.split_k > 1)  // K split with the fused last-arrival reduction: one launch
+      return launch(tf, dim3((unsigned)(twgs * c.split_k)), dim3(8 * kWave), kW8A8TileLds, s, a);
     const int64_t whole = twgs / 256 * 256;
     if (c.reduce != 1 && whole > 0 && twgs - whole <= 64 && whole % mblocks == 0) {
       const int n_main = (int)(whole / mblocks) * kW8A8TileTiles * kTileN;  // < N: the tail holds N's last block

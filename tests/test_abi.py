@@ -280,7 +280,23 @@ def test_w8a8_configs_host_only():
     assert L.w8a8_pick_config(513, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8           # 513 of 768 rows
     assert L.w8a8_pick_config(600, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8_TILE      # 600 of 768 rows
     assert L.w8a8_pick_config(1024, 10240, 5120).kernel == L.KERNEL_MFMA_W8A8_TILE     # 160
-    assert L.w8a8_pick_config(1536, 5120, 8192).kernel == L.KERNEL_MFMA_W8A8           # 120
+    # 40 to 128 workgroups of 256 x 256 with two or more token blocks: the tile kernel with a K split of
+    # min(4, K / 2560, 256 / workgroups), at least 2; M = 256 (one token block), short K and fewer
+    # workgroups stay below.
+    assert L.w8a8_pick_config(1536, 5120, 8192).to_tuple()[:5] == (L.KERNEL_MFMA_W8A8_TILE, 2, 8, 8, 4)  # 120
+    assert L.w8a8_pick_config(1024, 5120, 17408).to_tuple()[:5] == (L.KERNEL_MFMA_W8A8_TILE, 3, 8, 8, 4)  # 80
+    assert L.w8a8_pick_config(512, 5120, 17408).to_tuple()[:5] == (L.KERNEL_MFMA_W8A8_TILE, 4, 8, 8, 4)  # 40
+    assert L.w8a8_pick_config(512, 5120, 8192).to_tuple()[:5] == (L.KERNEL_MFMA_W8A8_TILE, 3, 8, 8, 4)  # 40
+    assert L.w8a8_pick_config(768, 10240, 5120, 0).to_tuple()[:5] == (L.KERNEL_MFMA_W8A8_TILE, 2, 8, 8, 4)
+    assert L.w8a8_pick_config(256, 5120, 17408).kernel == L.KERNEL_MFMA_W8A8          # one token block
+    assert L.w8a8_pick_config(1600, 1280, 5120).kernel == L.KERNEL_MFMA_W8A8          # 35 workgroups
+    assert L.w8a8_pick_config(1024, 5120, 2048).kernel == L.KERNEL_MFMA_W8A8          # K / 2560 = 0
+    assert L.w8a8_pick_config(2048, 3840, 17408).to_tuple()[:2] == (L.KERNEL_MFMA_W8A8_TILE, 2)  # 15 x 8
+    for M, N, K in ((1536, 5120, 8192), (1024, 5120, 17408), (512, 5120, 17408)):
+        c = L.w8a8_pick_config(M, N, K)
+        tiles = -(-N // 256) * -(-M // 256)
+        ws = lib.qf_w8a8_workspace_bytes(M, N, K, 1, ctypes.byref(c))
+        assert ws == 65536 + tiles * c.split_k * 256 * 1024, (M, N, K)
     # The automatic rule's two exceptions: 4-wavefront workgroups, unsplit, where 8-wavefront ones
     # would be under 128 (TILED only), and a split in two for a long K whose last round of 128-row
     # workgroups would leave the CUs at most a quarter busy.
@@ -288,8 +304,7 @@ def test_w8a8_configs_host_only():
     assert L.w8a8_pick_config(128, 10240, 5120, 0).to_tuple()[1:5] == (2, 2, 8, 4)
     assert L.w8a8_pick_config(256, 5120, 8192).to_tuple()[1:5] == (1, 2, 4, 4)
     assert L.w8a8_pick_config(2304, 3840, 17408).to_tuple()[1:5] == (2, 2, 8, 4)
-    assert L.w8a8_pick_config(1024, 5120, 17408).to_tuple()[1:5] == (1, 2, 8, 4)
-    assert L.w8a8_pick_config(2048, 3072, 5120).to_tuple()[1:5] == (1, 2, 8, 4)
+    assert L.w8a8_pick_config(2048, 3072, 4096).to_tuple()[1:5] == (1, 2, 8, 4)
     fake = 1 << 20
     def call(layout=1, cfg=None, M=40, K=1024, ldq=1024):
         return lib.qf_w8a8_gemm(fake, ldq, fake, fake, 0, layout, fake, fake, 1000, 0, M, 1000, K,

@@ -251,6 +251,7 @@ def w8a8_into(x, w, s, layout, ldw, y, out_dtype, cfg, x_tiled=False):
         rc = lib.qf_w8a8_gemm(xq.data_ptr(), K, s_a.data_ptr(), w.data_ptr(), ldw, layout, s.data_ptr(), y.data_ptr(),
                               y.stride(0), dt, M, N, K, ctypes.byref(c), ws.data_ptr(), need, stream)
     L.check(rc, "qf_w8a8_gemm_xt" if x_tiled else "qf_w8a8_gemm")
+    return ws
 
 
 def tile_tokens(xq):
@@ -307,12 +308,17 @@ def test_w8a8_tile_kernel_against_oracle(oracle):
 
 @pytest.mark.parametrize("name,M,N,K", [("gate_up", 2048, 34816, 5120), ("down", 2048, 5120, 17408),
                                         ("qkv", 1024, 10240, 5120), ("o_proj", 2048, 5120, 8192),
-                                        ("gate_up", 768, 34816, 5120)])
+                                        ("gate_up", 768, 34816, 5120), ("down", 512, 5120, 17408),
+                                        ("down", 1024, 5120, 17408), ("down", 1536, 5120, 17408),
+                                        ("o_proj", 768, 5120, 8192), ("qkv", 640, 10240, 5120)])
 def test_w8a8_tile_kernel_auto_layer_shapes(name, M, N, K):
-    """Where the automatic rule picks the LDS-tiled kernel (the layer shapes at prefill widths), the
-    result equals the restatement bit for bit on both layouts."""
+    """Where the automatic rule picks the LDS-tiled kernel (the layer shapes at prefill widths, and with a
+    K split and the fused reduction where the tile grid is under a round), the result equals the
+    restatement bit for bit on both layouts."""
     cfg = L.w8a8_pick_config(M, N, K)
     assert cfg.kernel == L.KERNEL_MFMA_W8A8_TILE, cfg.to_tuple()
+    tiles = -(-N // 256) * -(-M // 256)
+    assert (cfg.split_k > 1) == (tiles <= 128), cfg.to_tuple()
     x, w, s = random_case(M, N, K, M + 3 * N)
     ref = P.w8a8_reference(x, w.t(), s, None, torch.bfloat16)
     y = qf.w8a8_mm(x, qf.to_tiled(w.t()), s, torch.bfloat16)
@@ -348,6 +354,31 @@ def test_w8a8_tile_kernel_tail_split(M, N, K):
                         case = (M, N, K, out_dtype, layout, cfg, x_tiled, pad)
                         assert torch.equal(bits(y[:, :N]), bits(ref)), case
                         assert torch.isnan(y[:, N:].float()).all(), case
+
+
+@pytest.mark.parametrize("M,N,K,split", [(300, 1000, 640, 2), (300, 1000, 640, 3), (1000, 5120, 8192, 3),
+                                         (520, 1004, 1024, 4), (256, 512, 128, 2), (17, 4112, 5120, 8),
+                                         (513, 16, 192, 3), (2048, 1280, 17408, 5)])
+def test_w8a8_tile_kernel_split_k(M, N, K, split):
+    """The tile kernel with K split across workgroups and the fused reduction (the last split of a tile to
+    arrive adds the others' int32 slots): bit for bit equal to the restatement on both layouts, row-major and
+    token-tiled activations, staged and unstaged bf16 rows and fp32; every arrival counter back at zero.
+    Uneven split ranges (K / 64 not a multiple of the split) and a single split per step (K = 128, 2 splits)."""
+    x, w, s = random_case(M, N, K, M * 3 + N + split)
+    ref = P.w8a8_reference(x, w.t(), s, None, torch.bfloat16)
+    ref32 = P.w8a8_reference(x, w.t(), s, None, torch.float32)
+    wt = qf.to_tiled(w.t())
+    cfg = (L.KERNEL_MFMA_W8A8_TILE, split, 8, 8, 4, 1, 1, 1)
+    for layout, wp, ldw in ((qf.TILED, wt, 0), (qf.ROWMAJOR, w, K)):
+        for x_tiled in (False, True):
+            for out_dtype, pad in ((torch.bfloat16, 8), (torch.bfloat16, 4), (torch.float32, 4)):
+                y = torch.full((M, N + pad), float("nan"), dtype=out_dtype, device=DEV)
+                ws = w8a8_into(x, wp, s, layout, ldw, y, out_dtype, cfg, x_tiled)
+                torch.cuda.synchronize()
+                case = (M, N, K, split, layout, x_tiled, out_dtype, pad)
+                assert torch.equal(bits(y[:, :N]), bits(ref if out_dtype == torch.bfloat16 else ref32)), case
+                assert torch.isnan(y[:, N:].float()).all(), case
+                assert int(ws[:L.COUNTER_BYTES].view(torch.int32).abs().sum()) == 0, case
 
 
 @pytest.mark.parametrize("M,K", [(1, 64), (15, 128), (16, 1024), (17, 5120), (300, 8192), (2048, 5120),

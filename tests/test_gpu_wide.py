@@ -129,6 +129,7 @@ def test_wide_and_widened_paths_in_a_graph():
         outs.append(qf.w8a16_mm_prefill(x, wt, s, torch.bfloat16, qf.TILED, chunk_rows=768))
         outs += [qf.w8a8_mm(x, wt, s, torch.bfloat16) for (x, wt, s) in cases]  # quantiser + int8 GEMM
         outs.append(qf.w8a8_mm(x, wt, s, torch.bfloat16, (L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 4, 1, 1, 1)))
+        outs.append(qf.w8a8_mm(x, wt, s, torch.bfloat16, (L.KERNEL_MFMA_W8A8_TILE, 3, 8, 8, 4, 1, 1, 1)))  # fused K split
         return outs
 
     eager = [o.clone() for o in work()]
