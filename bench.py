@@ -18,6 +18,8 @@ line on stdout.
 Other modes, one JSON line each: --workload stack64 (64 distinct layers, one hipGraph per decode
 step, the layer output re-normalised to unit RMS as the next layer's input); --workload msweep (gate_up at M = 1..16);
 --workload lm_head (int8 draft head 151936x5120 + pad-masked argmax at M = 1, 4);
+--workload prefill (gate_up at M = 64 .. 2048 through the three M > 16 routes, the W8A8 GEMM alone at
+M = 2048 beside the vendor int8 GEMM, and the layer's four GEMMs through the W8A8 route at M = 512, 1024, 2048);
 --workload spec_attn (split-KV verification attention of one full-attention layer, H=24, H_kv=4,
 D=256, 800-position pages, at the reference's contexts and batch shapes);
 --profile-gemm NAME --iters N (only that GEMM, for rocprofv3); --profile-w8a8 M --iters N (only the
@@ -579,6 +581,32 @@ def prefill_weight_sets(torch, qf, dev, g, count=2):
     return sets
 
 
+def prefill_layer_rows(torch, qf, dev, g, widths=(512, 1024, 2048)):
+    """The layer's four GEMMs through the W8A8 route the dispatcher takes for M > 16 on TILED weights
+    (quantiser + int8 GEMM, as w8a8_mm runs them), two weight sets per shape rotated: µs, int8 TOPS and the
+    configuration the automatic rule picks (a K split on the narrow-N shapes at the smaller widths)."""
+    from qwen_fastpath import _lib as QL
+    out = {}
+    for name in ("qkv", "o_proj", "gate_up", "down"):
+        N, K = GEMMS[name]
+        sets = []
+        for _ in range(2):
+            w = qf.to_tiled(torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g).t())
+            sets.append((w, (torch.randn(N, device=dev, generator=g).abs() * 0.002 + 1e-4).float()))
+        for M in widths:
+            x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+            f = lambda i: qf.w8a8_mm(x, sets[i][0], sets[i][1], torch.bfloat16)  # noqa: E731
+            us = min(time_graph(torch, lambda: [f(i) for _ in range(2) for i in range(2)], 4, reps=5)
+                     for _ in range(2))
+            tops = 2.0 * M * N * K / us / 1e6
+            cfg = QL.w8a8_pick_config(M, N, K)
+            out[f"{name} M={M}"] = {"N": N, "K": K, "M": M, "us": round(us, 1), "TOPS": round(tops, 1),
+                                    "pct_int8_mfma_peak": round(100 * tops / 5000.0, 1), "config": cfg.to_tuple()}
+            log(f"  prefill {name:7s} M={M:5d}: w8a8 {us:8.1f} us {tops:7.1f} TOPS cfg {cfg.to_tuple()}")
+        del sets
+    return out
+
+
 def run_prefill(torch, qf, dev, args):
     """gate_up (N=34816, K=5120) at prefill widths M = 64 ... 2048 on TILED weights, two weight sets
     rotated (356 MB, past the 256 MB last-level cache), three routes timed interleaved (best of 2
@@ -653,6 +681,8 @@ def run_prefill(torch, qf, dev, args):
             "vs_baseline": None, "dtype": "int8", "data": "synthetic (seeded int8 weights, fp32 scales, bf16 activations)",
             "config": {"workload": "gate_up 34816x5120 prefill widths on TILED weights, W8A8 (value = M=2048 TOPS)"},
             "per_m": rows, "roofline": roofline}
+    del sets
+    line["layer_w8a8"] = prefill_layer_rows(torch, qf, dev, g)
     if not args.no_cpu:
         line["cpu_baseline"] = prefill_cpu_baseline()
     print(json.dumps(line), flush=True)
