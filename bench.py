@@ -22,8 +22,8 @@ step, the layer output re-normalised to unit RMS as the next layer's input); --w
 M = 2048 beside the vendor int8 GEMM, and the layer's four GEMMs through the W8A8 route at M = 512, 1024, 2048);
 --workload spec_attn (split-KV verification attention of one full-attention layer, H=24, H_kv=4,
 D=256, 800-position pages, at the reference's contexts and batch shapes);
---profile-gemm NAME --iters N (only that GEMM, for rocprofv3); --profile-w8a8 M --iters N (only the
-W8A8 GEMM on gate_up at M rows, activations quantised beforehand); --copy-probe (a plain device copy
+--profile-gemm NAME --iters N (only that GEMM, for rocprofv3); --profile-w8a8 M [--w8a8-gemm NAME] --iters N
+(only the W8A8 GEMM on gate_up or NAME at M rows, activations quantised beforehand); --copy-probe (a plain device copy
 of known size, for counter calibration).
 """
 from __future__ import annotations
@@ -188,7 +188,9 @@ def main():
                     help="only that GEMM at M=5 (single: the 5120x5120 linear at M=1), --iters launches, weights "
                          "rotating past the MALL (for rocprofv3)")
     ap.add_argument("--profile-w8a8", type=int, default=None, metavar="M",
-                    help="only the W8A8 GEMM on gate_up at M rows, --iters launches (for rocprofv3)")
+                    help="only the W8A8 GEMM on --w8a8-gemm at M rows, --iters launches (for rocprofv3)")
+    ap.add_argument("--w8a8-gemm", choices=list(GEMMS), default="gate_up",
+                    help="the layer GEMM of --profile-w8a8 (default gate_up)")
     ap.add_argument("--iters", type=int, default=200)
     ap.add_argument("--copy-probe", action="store_true")
     ap.add_argument("--read-probe", action="store_true", help="only the library's read probe over the dominant GEMM's bytes")
@@ -230,12 +232,13 @@ def main():
         M = args.profile_w8a8
         g = torch.Generator(device=dev)
         g.manual_seed(13)
-        sets = prefill_weight_sets(torch, qf, dev, g)
-        gemm, cfg = w8a8_gate_up_gemm(torch, qf, dev, g, M, sets)
+        name = args.w8a8_gemm
+        sets = prefill_weight_sets(torch, qf, dev, g, name=name)
+        gemm, cfg = w8a8_gate_up_gemm(torch, qf, dev, g, M, sets, name)
         for i in range(args.iters):
             gemm(i % 2)
         torch.cuda.synchronize()
-        log(f"profile: {args.iters} launches of the W8A8 GEMM on gate_up M={M} cfg={cfg.to_tuple()}")
+        log(f"profile: {args.iters} launches of the W8A8 GEMM on {name} M={M} cfg={cfg.to_tuple()}")
         return
 
     if args.profile_gemm == "single":
@@ -544,36 +547,40 @@ def run_msweep(torch, qf, dev, args):
     print(json.dumps(line), flush=True)
 
 
-def w8a8_gate_up_gemm(torch, qf, dev, g, M, sets):
-    """The W8A8 GEMM alone on gate_up at M rows (activations quantised once, beforehand, in the layout
-    w8a8_mm gives that kernel): returns a callable that runs it on weight set i, and its configuration."""
+def w8a8_gate_up_gemm(torch, qf, dev, g, M, sets, name="gate_up"):
+    """The W8A8 GEMM alone on a layer GEMM (gate_up by default) at M rows (activations quantised once,
+    beforehand, in the layout w8a8_mm gives that kernel; a K split gets its own workspace): returns a callable
+    that runs it on weight set i, and its configuration."""
     import ctypes
     from qwen_fastpath import _lib as QL
-    N, K = GEMMS["gate_up"]
+    N, K = GEMMS[name]
     x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
     lib = QL.load()
     cfg = QL.w8a8_pick_config(M, N, K)
     x_tiled = cfg.kernel == QL.KERNEL_MFMA_W8A8_TILE
     xq, s_a = qf.quantize_tokens_int8(x, tiled=x_tiled)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-    assert int(lib.qf_w8a8_workspace_bytes(M, N, K, qf.TILED, ctypes.byref(cfg))) == 0
+    need = int(lib.qf_w8a8_workspace_bytes(M, N, K, qf.TILED, ctypes.byref(cfg)))
+    ws = torch.zeros(max(need, 16), dtype=torch.uint8, device=dev)  # arrival counters start at zero
+    ws_ptr = ws.data_ptr() if need else None
 
     def gemm(i):
         st = torch.cuda.current_stream().cuda_stream
         if x_tiled:
             QL.check(lib.qf_w8a8_gemm_xt(xq.data_ptr(), s_a.data_ptr(), sets[i][0].data_ptr(), 0, qf.TILED,
                                          sets[i][1].data_ptr(), y.data_ptr(), N, QL.DTYPE_BF16, M, N, K,
-                                         ctypes.byref(cfg), None, 0, st), "qf_w8a8_gemm_xt")
+                                         ctypes.byref(cfg), ws_ptr, need, st), "qf_w8a8_gemm_xt")
         else:
             QL.check(lib.qf_w8a8_gemm(xq.data_ptr(), K, s_a.data_ptr(), sets[i][0].data_ptr(), 0, qf.TILED,
                                       sets[i][1].data_ptr(), y.data_ptr(), N, QL.DTYPE_BF16, M, N, K, ctypes.byref(cfg),
-                                      None, 0, st), "qf_w8a8_gemm")
+                                      ws_ptr, need, st), "qf_w8a8_gemm")
     return gemm, cfg
 
 
-def prefill_weight_sets(torch, qf, dev, g, count=2):
-    """gate_up int8 weights in the TILED layout with fp32 scales, `count` distinct sets."""
-    N, K = GEMMS["gate_up"]
+def prefill_weight_sets(torch, qf, dev, g, count=2, name="gate_up"):
+    """A layer GEMM's (gate_up by default) int8 weights in the TILED layout with fp32 scales, `count`
+    distinct sets."""
+    N, K = GEMMS[name]
     sets = []
     for _ in range(count):
         w = qf.to_tiled(torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g).t())
