@@ -14,6 +14,7 @@ import pytest
 import torch
 
 import qwen_fastpath as qf
+from qwen_fastpath import _lib as L
 from qwen_fastpath import patches as P
 from helpers import bf16_bits, dev_inputs
 
@@ -137,6 +138,33 @@ def test_two_streams_overlap_with_own_workspaces(oracle):
     ref = torch.argmax(torch.where(torch.arange(40000, device=DEV) < 40000 - 7, logits[0].float(),
                                    torch.tensor(float("-inf"), device=DEV)), dim=-1) + 100
     assert torch.equal(want_i[0], ref)
+
+
+def test_two_streams_w8a8_tile_split_overlap():
+    """W8A8 calls on the LDS-tiled kernel with its K split three ways (the last split of each tile adds the
+    others' int32 partials through the stream's workspace) issued on two same-priority streams without
+    synchronisation between them equal the same calls run in order, and the restatement."""
+    M, N, K = 512, 1024, 8192
+    w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=DEV)
+    wt = qf.to_tiled(w.t())
+    s = torch.rand(N, device=DEV) * 0.002 + 1e-4
+    cfg = (L.KERNEL_MFMA_W8A8_TILE, 3, 8, 8, 4, 1, 1, 0)
+    xs = [torch.randn(M, K, device=DEV).to(torch.bfloat16) for _ in range(6)]
+    want = [qf.w8a8_mm(x, wt, s, torch.bfloat16, cfg) for x in xs]
+    ref0 = P.w8a8_reference(xs[0], w.t(), s, None, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(want[0].view(torch.int16), ref0.view(torch.int16))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    got = [None] * 6
+    for rep in range(3):
+        for j in range(6):
+            with torch.cuda.stream(streams[j % 2]):
+                got[j] = qf.w8a8_mm(xs[j], wt, s, torch.bfloat16, cfg)
+        torch.cuda.synchronize()
+        for j in range(6):
+            assert torch.equal(got[j].view(torch.int16), want[j].view(torch.int16)), f"rep {rep} call {j}"
 
 
 def test_capture_without_warmup(oracle):
