@@ -2731,14 +2731,17 @@ bool auto_config_w8a8(int M, int N, int K, int layout, qf_w8a16_config* c) {
   // M = 512 (272 workgroups, the last 16 on the wide kernel) 107 against 148 us, M = 2048 301 against
   // 420; slower with fewer workgroups, where the shapes below split K: down M = 1024 (80) 172 against
   // 152, o_proj M = 1536 (120) 91 against 87).  Its token blocks are 256 rows whatever M is, so it also
-  // needs M >= 256 with under a quarter of the rows it computes past M (gate_up M = 384: 109 against 102).
+  // needs M >= 256 with under a quarter of the rows it computes past M (gate_up M = 384: 109 against 102),
+  // or one token block above 128 rows, where the shapes below go to two token groups a channel block
+  // (gate_up M = 129 / 160 / 208 / 255: 61.9 / 63.0 / 67.4 / 68.1 us against 76.0 / 77.9 / 93.5 / 100.3;
+  // M = 112: 66.1 against 52.1).
   const int64_t twgs = w8a8_tile_workgroups(M, N);
   const int mblocks = ceil_div(M, kW8A8TileRows);
   const int64_t tile_rows = (int64_t)mblocks * kW8A8TileRows;
   const int64_t rest = twgs % 256, whole = twgs - rest;
   const bool second_launch = whole > 0 && rest <= 64 && whole % mblocks == 0;
-  if (K < 132000 && M >= kW8A8TileRows && 4 * (int64_t)M > 3 * tile_rows && twgs >= 136 &&
-      !(whole > 0 && rest != 0 && rest <= 16 && !second_launch)) {
+  const bool rows_ok = (M >= kW8A8TileRows && 4 * (int64_t)M > 3 * tile_rows) || (mblocks == 1 && M > 128);
+  if (K < 132000 && rows_ok && twgs >= 136 && !(whole > 0 && rest != 0 && rest <= 16 && !second_launch)) {
     c->kernel = QF_KERNEL_MFMA_W8A8_TILE;
     c->tiles_per_wave = 8;
     c->waves = 8;

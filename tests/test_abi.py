@@ -269,9 +269,12 @@ def test_w8a8_configs_host_only():
                     if layout == 0:
                         assert c.to_tuple()[2:5] == (2, 8, 4), (M, N, K)
     # The tile kernel's rule: 136 or more workgroups, not 1-16 past a whole round unless the second launch
-    # takes them, M >= 256 with under a quarter of the computed rows past M.
+    # takes them, M >= 256 with under a quarter of the computed rows past M, or one token block above 128 rows.
     assert L.w8a8_pick_config(256, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8_TILE      # 136 workgroups
-    assert L.w8a8_pick_config(255, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8           # M < 256
+    assert L.w8a8_pick_config(128, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8           # one 128-row group
+    assert L.w8a8_pick_config(129, 34816, 5120).to_tuple()[:2] == (L.KERNEL_MFMA_W8A8_TILE, 1)  # one block
+    assert L.w8a8_pick_config(255, 34816, 5120).to_tuple()[:2] == (L.KERNEL_MFMA_W8A8_TILE, 1)
+    assert L.w8a8_pick_config(192, 10240, 5120).kernel == L.KERNEL_MFMA_W8A8           # 40 workgroups
     assert L.w8a8_pick_config(384, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8           # 384 of 512 rows
     assert L.w8a8_pick_config(512, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8_TILE      # 272 = 256 + 16, split
     assert L.w8a8_pick_config(3328, 10240, 5120).kernel == L.KERNEL_MFMA_W8A8          # 520 = 512 + 8, 13 blocks
