@@ -92,7 +92,8 @@ typedef enum qf_kernel {
                                channels in a second launch: reduce 0 (automatic) on 128 x 128 workgroups
                                of the same kernel where they make one round of 128 to 256, else on the
                                QF_KERNEL_MFMA_W8A8 kernel; reduce 2 on the latter only; reduce 1: one
-                               launch */
+                               launch; reduce 3 (split_k 1): one launch of 256-channel x 128-token
+                               workgroups */
 } qf_kernel;
 
 /* Launch configuration.  A zero field means "choose automatically". */

@@ -1209,16 +1209,19 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
-// Workgroup tile shapes: FA weight fragments by FB = FA / 2 activation fragments a wavefront, 8 wavefronts
-// in 2 channel x 4 token groups, so 32 FA channels x 32 FA tokens a workgroup: FA = 8 is the 256 x 256
-// main shape, FA = 4 the 128 x 128 shape that runs the channels past the main grid's whole rounds.
-template <int FA>
+// Workgroup tile shapes: FA weight fragments by FB activation fragments a wavefront, 8 wavefronts in 2
+// channel x 4 token groups, so 32 FA channels x 64 FB tokens a workgroup: (8, 4) is the 256 x 256 main
+// shape, (4, 2) the 128 x 128 shape that runs the channels past the main grid's whole rounds, (8, 2) the
+// 256-channel x 128-token shape of reduce 3.  A stage's fragments, weights first, are spread evenly over
+// the 8 wavefronts.
+template <int FA, int FB_ = FA / 2>
 struct TileShape {
-  static constexpr int FB = FA / 2;
+  static constexpr int FB = FB_;
   static constexpr int tiles = 2 * FA;            // 16-channel weight tiles a workgroup
-  static constexpr int frags = 2 * FA;            // 16-token activation fragments a workgroup
+  static constexpr int frags = 4 * FB;            // 16-token activation fragments a workgroup
   static constexpr int rows = 16 * frags;         // tokens a workgroup
-  static constexpr int copies = FA / 2;           // fragments a wavefront copies a stage
+  static constexpr int copies = (tiles + frags) / 8;  // fragments a wavefront copies a stage
+  static_assert((tiles + frags) % 8 == 0, "the stage's fragments spread evenly over the 8 wavefronts");
   static constexpr int stage_bytes = (tiles + frags) * 1024;
   // 4 stages for the main shape; 6 for the small one, which also keeps it at one workgroup a CU
   // (96 KiB), so that a grid of 256 spreads over all CUs.
@@ -1226,12 +1229,12 @@ struct TileShape {
   static constexpr int lds = stages * stage_bytes;
 };
 
-template <int LAYOUT, int FA>
+template <int LAYOUT, int FA, int FB_ = FA / 2>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
     w8a8_tile_kernel(const GemmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ int last_arrival;
-  using T = TileShape<FA>;
+  using T = TileShape<FA, FB_>;
   constexpr int FB = T::FB;
   constexpr int S = T::stages;
   constexpr int CP = T::copies;
@@ -1262,49 +1265,44 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int m0 = (l % mblocks) * T::rows;
   const int ksteps = a.ksteps;
 
-  // Wavefronts 0..3 copy the weight fragments CP wave .. CP wave + CP - 1, wavefronts 4..7 the
-  // activation fragments CP (wave - 4) .. + CP - 1.  Channels and tokens past the matrix read its last
-  // row (block) instead; their outputs are never stored.
+  // Wavefront w copies fragments CP w .. CP w + CP - 1 of the stage: the T::tiles weight fragments first, then
+  // the T::frags activation fragments (with 256-token workgroups, wavefronts 0..3 copy weights and 4..7
+  // activations).  Channels and tokens past the matrix read its last row (block) instead; their outputs are
+  // never stored.
   const int8_t* src[CP];
-  int64_t adv;  // bytes between the same fragment of consecutive steps
-  if (wave < 4) {
+  int64_t adv[CP];  // bytes between the same fragment of consecutive steps
 #pragma unroll
-    for (int j = 0; j < CP; ++j) {
-      const int t = min(tile0 + CP * wave + j, ntiles - 1);
+  for (int j = 0; j < CP; ++j) {
+    const int f = CP * wave + j;  // uniform
+    if (f < T::tiles) {
+      const int t = min(tile0 + f, ntiles - 1);
       if constexpr (LAYOUT == QF_LAYOUT_ROWMAJOR) {
         src[j] = a.w + (int64_t)min(t * kTileN + r, a.N - 1) * a.ldw + 16 * g;
       } else {
         src[j] = a.w + ((int64_t)t * ksteps * kWave + lane) * 16;
       }
-    }
-    adv = LAYOUT == QF_LAYOUT_ROWMAJOR ? kStepK : kTileN * kStepK;
-  } else if (a.x_tiled) {  // uniform: one contiguous KiB per fragment, as the TILED weights
-    const int last = (a.M - 1) >> 4;
-#pragma unroll
-    for (int j = 0; j < CP; ++j) {
-      const int b = min((m0 >> 4) + CP * (wave - 4) + j, last);
+      adv[j] = LAYOUT == QF_LAYOUT_ROWMAJOR ? kStepK : kTileN * kStepK;
+    } else if (a.x_tiled) {  // one contiguous KiB per fragment, as the TILED weights
+      const int b = min((m0 >> 4) + f - T::tiles, (a.M - 1) >> 4);
       src[j] = a.xq + ((int64_t)b * ksteps * kWave + lane) * 16;
-    }
-    adv = kTileN * kStepK;
-  } else {
-#pragma unroll
-    for (int j = 0; j < CP; ++j) {
-      const int row = min(m0 + 16 * (CP * (wave - 4) + j) + r, a.M - 1);
+      adv[j] = kTileN * kStepK;
+    } else {
+      const int row = min(m0 + 16 * (f - T::tiles) + r, a.M - 1);
       src[j] = a.xq + (int64_t)row * a.ldx + 16 * g;
+      adv[j] = kStepK;
     }
-    adv = kStepK;
   }
 #pragma unroll
-  for (int j = 0; j < CP; ++j) src[j] += (int64_t)s_begin * adv;
+  for (int j = 0; j < CP; ++j) src[j] += (int64_t)s_begin * adv[j];
   // Copy group s: stage min(s, ksteps - 1) into slot s % S.  Groups past the last stage copy it again
   // into a slot whose stage every wavefront has consumed, so every iteration issues exactly one group
   // and the vmcnt waits are constants.
   auto copy = [&](int s) {
     uint8_t* slot = smem + (s % S) * T::stage_bytes + wave * CP * 1024;
-    const int64_t off = (int64_t)min(s, nsteps - 1) * adv;
+    const int64_t st = min(s, nsteps - 1);
 #pragma unroll
     for (int j = 0; j < CP; ++j)
-      __builtin_amdgcn_global_load_lds((glb_ptr_t)(src[j] + off), (lds_ptr_t)(slot + j * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((glb_ptr_t)(src[j] + st * adv[j]), (lds_ptr_t)(slot + j * 1024), 16, 0, 0);
   };
   auto read_frags = [&](int s, i32x4_t (&A)[FA], i32x4_t (&B)[FB]) {
     const uint8_t* slot = smem + (s % S) * T::stage_bytes + lane * 16;
@@ -2685,7 +2683,7 @@ int validate_w8a8(int M, int N, int K, int layout, const qf_w8a16_config& c) {
   const int ksteps = K / kStepK;
   if (c.kernel == QF_KERNEL_MFMA_W8A8_TILE) {
     if (c.split_k < 1 || c.split_k > kW8A8TileMaxSplit || c.waves != 8 || c.tiles_per_wave != 8 ||
-        c.depth != kW8A8TileStages || c.k_waves != 1 || c.reduce < 0 || c.reduce > 2)
+        c.depth != kW8A8TileStages || c.k_waves != 1 || c.reduce < 0 || c.reduce > 3 || (c.reduce == 3 && c.split_k != 1))
       return QF_ERR_INVALID_ARG;
     if ((layout != QF_LAYOUT_TILED && layout != QF_LAYOUT_ROWMAJOR) || K >= 132000) return QF_ERR_UNSUPPORTED;
     const int64_t twgs = w8a8_tile_workgroups(M, N);
@@ -2747,6 +2745,18 @@ bool auto_config_w8a8(int M, int N, int K, int layout, qf_w8a16_config* c) {
     c->waves = 8;
     c->depth = kW8A8TileStages;
     c->reduce = 0;  // the tile kernel's tail rule (run_w8a8)
+    return validate_w8a8(M, N, K, layout, *c) == QF_OK;
+  }
+  // 289 to 384 rows, where two token blocks of 256 would be under three-quarters full and three of 128 are
+  // not, on grids of 136 or more 256 x 256 workgroups: 256-channel x 128-token workgroups (reduce 3; gate_up
+  // M = 320 / 352 / 384 93.3 / 95.0 / 96.5 us against 102.1 / 111.6 / 112.3 on the shapes below; M = 272
+  // 95.0 against 90.9, M = 416 131.9 against 112.1 on the 256-token kernel).
+  if (K < 132000 && M > 288 && M <= 384 && twgs >= 136) {
+    c->kernel = QF_KERNEL_MFMA_W8A8_TILE;
+    c->tiles_per_wave = 8;
+    c->waves = 8;
+    c->depth = kW8A8TileStages;
+    c->reduce = 3;
     return validate_w8a8(M, N, K, layout, *c) == QF_OK;
   }
   // 40 to 128 256 x 256 workgroups (measured from 40), with two or more token blocks: the tile kernel with K split
@@ -2873,6 +2883,12 @@ int run_w8a8(const int8_t* xq, int64_t ldq, int x_tiled, const float* s_a, const
     const int64_t twgs = (int64_t)nblocks * mblocks;
     if (c.split_k > 1)  // K split with the fused last-arrival reduction: one launch
       return launch(tf, dim3((unsigned)(twgs * c.split_k)), dim3(8 * kWave), kW8A8TileLds, s, a);
+    if (c.reduce == 3) {  // 256-channel x 128-token workgroups, one launch
+      using Half = TileShape<8, 2>;
+      const int64_t hwgs = (int64_t)nblocks * ceil_div(M, Half::rows);
+      return launch(rm ? &w8a8_tile_kernel<QF_LAYOUT_ROWMAJOR, 8, 2> : &w8a8_tile_kernel<QF_LAYOUT_TILED, 8, 2>,
+                    dim3((unsigned)hwgs), dim3(8 * kWave), Half::lds, s, a);
+    }
     const int64_t whole = twgs / 256 * 256;
     if (c.reduce != 1 && whole > 0 && twgs - whole <= 64 && whole % mblocks == 0) {
       const int n_main = (int)(whole / mblocks) * kW8A8TileTiles * kTileN;  // < N: the tail holds N's last block

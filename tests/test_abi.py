@@ -259,11 +259,14 @@ def test_w8a8_configs_host_only():
     for M in (1, 17, 64, 300, 2048):
         for (N, K) in ((34816, 5120), (5120, 17408), (1000, 1024), (16, 64)):
             tile = M == 2048 and N >= 5120  # 1088 and 160 workgroups of 256 x 256
+            tile128 = M == 300 and N == 34816  # 136 x 3 workgroups of 256 x 128
             for layout in (1, 0):  # TILED, row-major (the automatic 2-tile shape or the tile kernel)
                 c = L.w8a8_pick_config(M, N, K, layout)
                 assert c is not None and c.k_waves == 1, (M, N, K, layout)
                 if tile:
                     assert c.to_tuple()[:5] == (L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 4), (M, N, K, layout)
+                elif tile128:
+                    assert c.to_tuple() == (L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 4, 1, 1, 3), (M, N, K, layout)
                 else:
                     assert c.kernel == L.KERNEL_MFMA_W8A8, (M, N, K, layout)
                     if layout == 0:
@@ -275,7 +278,12 @@ def test_w8a8_configs_host_only():
     assert L.w8a8_pick_config(129, 34816, 5120).to_tuple()[:2] == (L.KERNEL_MFMA_W8A8_TILE, 1)  # one block
     assert L.w8a8_pick_config(255, 34816, 5120).to_tuple()[:2] == (L.KERNEL_MFMA_W8A8_TILE, 1)
     assert L.w8a8_pick_config(192, 10240, 5120).kernel == L.KERNEL_MFMA_W8A8           # 40 workgroups
-    assert L.w8a8_pick_config(384, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8           # 384 of 512 rows
+    # 289..384 rows on a grid of 136 or more: 256-channel x 128-token workgroups (reduce 3)
+    assert L.w8a8_pick_config(384, 34816, 5120).to_tuple() == (L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 4, 1, 1, 3)
+    assert L.w8a8_pick_config(289, 34816, 5120).to_tuple()[::7] == (L.KERNEL_MFMA_W8A8_TILE, 3)
+    assert L.w8a8_pick_config(288, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8           # 2 x 128 rows + 32
+    assert L.w8a8_pick_config(385, 34816, 5120).to_tuple()[::7] == (L.KERNEL_MFMA_W8A8_TILE, 0)
+    assert L.w8a8_pick_config(320, 10240, 5120).kernel == L.KERNEL_MFMA_W8A8           # 80 workgroups
     assert L.w8a8_pick_config(512, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8_TILE      # 272 = 256 + 16, split
     assert L.w8a8_pick_config(3328, 10240, 5120).kernel == L.KERNEL_MFMA_W8A8          # 520 = 512 + 8, 13 blocks
     assert L.w8a8_pick_config(768, 34816, 5120).kernel == L.KERNEL_MFMA_W8A8_TILE      # 408

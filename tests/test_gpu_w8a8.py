@@ -311,7 +311,8 @@ def test_w8a8_tile_kernel_against_oracle(oracle):
                                         ("gate_up", 768, 34816, 5120), ("down", 512, 5120, 17408),
                                         ("down", 1024, 5120, 17408), ("down", 1536, 5120, 17408),
                                         ("o_proj", 768, 5120, 8192), ("qkv", 640, 10240, 5120),
-                                        ("gate_up", 129, 34816, 5120), ("gate_up", 200, 34816, 5120)])
+                                        ("gate_up", 129, 34816, 5120), ("gate_up", 200, 34816, 5120),
+                                        ("gate_up", 320, 34816, 5120), ("gate_up", 384, 34816, 5120)])
 def test_w8a8_tile_kernel_auto_layer_shapes(name, M, N, K):
     """Where the automatic rule picks the LDS-tiled kernel (the layer shapes at prefill widths, and with a
     K split and the fused reduction where the tile grid is under a round), the result equals the
@@ -380,6 +381,29 @@ def test_w8a8_tile_kernel_split_k(M, N, K, split):
                 assert torch.equal(bits(y[:, :N]), bits(ref if out_dtype == torch.bfloat16 else ref32)), case
                 assert torch.isnan(y[:, N:].float()).all(), case
                 assert int(ws[:L.COUNTER_BYTES].view(torch.int32).abs().sum()) == 0, case
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 1000, 640), (17, 4112, 1024), (129, 520, 192), (384, 2064, 5120),
+                                   (1000, 16, 128), (257, 34816, 1024)])
+def test_w8a8_tile_kernel_128_token_workgroups(M, N, K):
+    """The tile kernel's 256-channel x 128-token workgroups (reduce 3; a stage's 24 fragments, weights first,
+    3 to a wavefront, so wavefront 5 copies one weight and two activation fragments): bit for bit equal to
+    the restatement on both layouts, row-major and token-tiled activations, staged and unstaged bf16 rows
+    and fp32; ragged M and N, one channel tile, one k-step pair."""
+    x, w, s = random_case(M, N, K, M * 7 + N + K)
+    ref = P.w8a8_reference(x, w.t(), s, None, torch.bfloat16)
+    ref32 = P.w8a8_reference(x, w.t(), s, None, torch.float32)
+    wt = qf.to_tiled(w.t())
+    cfg = (L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 4, 1, 1, 3)
+    for layout, wp, ldw in ((qf.TILED, wt, 0), (qf.ROWMAJOR, w, K)):
+        for x_tiled in (False, True):
+            for out_dtype, pad in ((torch.bfloat16, 8), (torch.bfloat16, 4), (torch.float32, 4)):
+                y = torch.full((M, N + pad), float("nan"), dtype=out_dtype, device=DEV)
+                w8a8_into(x, wp, s, layout, ldw, y, out_dtype, cfg, x_tiled)
+                torch.cuda.synchronize()
+                case = (M, N, K, layout, x_tiled, out_dtype, pad)
+                assert torch.equal(bits(y[:, :N]), bits(ref if out_dtype == torch.bfloat16 else ref32)), case
+                assert torch.isnan(y[:, N:].float()).all(), case
 
 
 @pytest.mark.parametrize("M,K", [(1, 64), (15, 128), (16, 1024), (17, 5120), (300, 8192), (2048, 5120),
