@@ -2777,7 +2777,11 @@ bool auto_config_w8a8(int M, int N, int K, int layout, qf_w8a16_config* c) {
   // / 81.3 against 55.9 / 56.7 / 79.4 / 87.0; qkv 10240 x 5120 at M = 512 / 768 49.8 / 59.6 against 54.5 /
   // 59.4; at M = 256 the shapes below win: down 67 against 68, o_proj 43 against 48, qkv 38 against 43).
   const int64_t sk = std::min<int64_t>(std::min(4, K / 2560), twgs > 0 ? 256 / twgs : 0);
-  if (K < 132000 && mblocks >= 2 && 4 * (int64_t)M > 3 * tile_rows && twgs >= 40 && twgs <= 128 && sk >= 2) {
+  // Three or more token blocks at most three-quarters full take it too when K is long (>= 10240), where the
+  // shapes below would run every workgroup over the whole K: down M = 520 / 544 / 576 87.0 / 89.8 / 89.2 us
+  // against 113.9 / 113.9 / 113.8 (o_proj 56-60 against 58-59, qkv 57-60 against 52-58 stay below).
+  const bool split_rows = 4 * (int64_t)M > 3 * tile_rows || (mblocks >= 3 && K >= 10240);
+  if (K < 132000 && mblocks >= 2 && split_rows && twgs >= 40 && twgs <= 128 && sk >= 2) {
     c->kernel = QF_KERNEL_MFMA_W8A8_TILE;
     c->split_k = (int)sk;
     c->tiles_per_wave = 8;

@@ -300,6 +300,9 @@ def test_w8a8_configs_host_only():
     assert L.w8a8_pick_config(512, 5120, 8192).to_tuple()[:5] == (L.KERNEL_MFMA_W8A8_TILE, 3, 8, 8, 4)  # 40
     assert L.w8a8_pick_config(768, 10240, 5120, 0).to_tuple()[:5] == (L.KERNEL_MFMA_W8A8_TILE, 2, 8, 8, 4)
     assert L.w8a8_pick_config(256, 5120, 17408).kernel == L.KERNEL_MFMA_W8A8          # one token block
+    assert L.w8a8_pick_config(544, 5120, 17408).to_tuple()[:2] == (L.KERNEL_MFMA_W8A8_TILE, 4)  # long K, 3 blocks
+    assert L.w8a8_pick_config(544, 5120, 8192).kernel == L.KERNEL_MFMA_W8A8           # 3 blocks, K < 10240
+    assert L.w8a8_pick_config(384, 5120, 17408).kernel == L.KERNEL_MFMA_W8A8          # 2 blocks, 384 of 512
     assert L.w8a8_pick_config(1600, 1280, 5120).kernel == L.KERNEL_MFMA_W8A8          # 35 workgroups
     assert L.w8a8_pick_config(1024, 5120, 2048).kernel == L.KERNEL_MFMA_W8A8          # K / 2560 = 0
     assert L.w8a8_pick_config(2048, 3840, 17408).to_tuple()[:2] == (L.KERNEL_MFMA_W8A8_TILE, 2)  # 15 x 8

@@ -312,7 +312,8 @@ def test_w8a8_tile_kernel_against_oracle(oracle):
                                         ("down", 1024, 5120, 17408), ("down", 1536, 5120, 17408),
                                         ("o_proj", 768, 5120, 8192), ("qkv", 640, 10240, 5120),
                                         ("gate_up", 129, 34816, 5120), ("gate_up", 200, 34816, 5120),
-                                        ("gate_up", 320, 34816, 5120), ("gate_up", 384, 34816, 5120)])
+                                        ("gate_up", 320, 34816, 5120), ("gate_up", 384, 34816, 5120),
+                                        ("down", 544, 5120, 17408)])
 def test_w8a8_tile_kernel_auto_layer_shapes(name, M, N, K):
     """Where the automatic rule picks the LDS-tiled kernel (the layer shapes at prefill widths, and with a
     K split and the fused reduction where the tile grid is under a round), the result equals the
