@@ -271,6 +271,14 @@ int qf_w8a8_gemm_xt(const int8_t* xt, const float* s_a, const int8_t* w, int64_t
 int qf_w8a8_pick_config(int M, int N, int K, int layout, qf_w8a16_config* cfg);
 size_t qf_w8a8_workspace_bytes(int M, int N, int K, int layout, const qf_w8a16_config* cfg);
 
+/* The kernel launches qf_w8a8_gemm makes for (M, N, K, layout, cfg), in stream order (host only; no
+ * reference counterpart: it exposes the launch plan so that it can be checked without a GPU).  Writes
+ * *count (1 or 2) rows of four int64 to out[0 .. 8): kind (0: tile kernel, 256 x 256 workgroups; 1: tile
+ * kernel, 256 x 128; 2: tile kernel, 128 x 128; 3: wide kernel; 4: split-K reduction), workgroups, and the
+ * first output channel and channel count of the launch.  The launches' channel ranges are disjoint and
+ * cover [0, N). */
+int qf_w8a8_launch_plan(int M, int N, int K, int layout, const qf_w8a16_config* cfg, int64_t* out, int* count);
+
 /* Per-row symmetric int8 quantisation of a bf16 [V, H] matrix (row stride ldw elements):
  *   s[v] = max(max_h |w[v,h]|, 1e-8) / 127   (fp32, IEEE division)
  *   q[v,h] = clamp(round_half_even(w[v,h] / s[v]), -127, 127)

@@ -2690,6 +2690,7 @@ int64_t w8a8_tile_workgroups(int M, int N) {
 }
 
 int validate_w8a8(int M, int N, int K, int layout, const qf_w8a16_config& c) {
+  if (M < 1 || N < 1 || K < QF_W8A16_K_ALIGN) return QF_ERR_INVALID_ARG;
   const int ksteps = K / kStepK;
   if (c.kernel == QF_KERNEL_MFMA_W8A8_TILE) {
     if (c.split_k < 1 || c.split_k > kW8A8TileMaxSplit || c.waves != 8 || c.tiles_per_wave != 8 ||
@@ -2747,7 +2748,8 @@ bool auto_config_w8a8(int M, int N, int K, int layout, qf_w8a16_config* c) {
   const int mblocks = ceil_div(M, kW8A8TileRows);
   const int64_t tile_rows = (int64_t)mblocks * kW8A8TileRows;
   const int64_t rest = twgs % 256, whole = twgs - rest;
-  const bool second_launch = whole > 0 && rest <= 64 && whole % mblocks == 0;
+  // A second launch only takes a true remainder: 0 < rest <= 64 workgroups past whole rounds.
+  const bool second_launch = whole > 0 && rest > 0 && rest <= 64 && whole % mblocks == 0;
   const bool rows_ok = (M >= kW8A8TileRows && 4 * (int64_t)M > 3 * tile_rows) || (mblocks == 1 && M > 128);
   if (K < 132000 && rows_ok && twgs >= 136 && !(whole > 0 && rest != 0 && rest <= 16 && !second_launch)) {
     c->kernel = QF_KERNEL_MFMA_W8A8_TILE;
@@ -2800,6 +2802,7 @@ bool auto_config_w8a8(int M, int N, int K, int layout, qf_w8a16_config* c) {
 
 // The automatic QF_KERNEL_MFMA_W8A8 shape (c holds the defaults set above).
 bool auto_config_w8a8_wide(int M, int N, int K, int layout, qf_w8a16_config* c) {
+  if (M < 1 || N < 1 || K < QF_W8A16_K_ALIGN) return false;
   int groups, rows;
   w8a8_groups(*c, M, N, groups, rows);
   const int64_t wgs = (int64_t)workgroups(*c, N) * groups;
@@ -2839,6 +2842,90 @@ int resolve_w8a8(int M, int N, int K, int layout, const qf_w8a16_config* in, qf_
   if (rc != QF_OK) return rc;
   *out = c;
   return QF_OK;
+}
+
+// The launches of one W8A8 call, in stream order.  Each covers output channels [n0, n0 + n) of the call
+// (all token rows), so the launches of a call write disjoint columns; the sums are exact integer sums, so
+// how the channels are divided does not change the result.
+enum W8a8LaunchKind {
+  kW8a8Tile = 0,         // w8a8_tile_kernel, 256 x 256 workgroups (n a multiple of 256 when a tail follows)
+  kW8a8TileHalf = 1,     // w8a8_tile_kernel, 256-channel x 128-token workgroups (reduce 3)
+  kW8a8TileSmall = 2,    // w8a8_tile_kernel, 128 x 128 workgroups (the tail round)
+  kW8a8Wide = 3,         // w8a8_wide_kernel with the launch's own cfg
+  kW8a8SplitReduce = 4,  // splitk_reduce_w8a8_kernel after a K-split wide launch
+};
+struct W8a8Launch {
+  int kind;
+  int64_t grid;  // workgroups
+  int n0, n;     // output channels of this launch
+  qf_w8a16_config cfg;
+};
+
+// Fills out[0..1] with the call's launches and returns their number (1 or 2), or -(qf_status).
+int w8a8_plan(int M, int N, int K, int layout, const qf_w8a16_config& c, W8a8Launch out[2]) {
+  if (M < 1 || N < 1 || K < QF_W8A16_K_ALIGN) return -QF_ERR_INVALID_ARG;
+  const int n_pad = round_up16(N);
+  out[0] = W8a8Launch{kW8a8Tile, 0, 0, N, c};
+  if (c.kernel == QF_KERNEL_MFMA_W8A8_TILE) {
+    // Tail (reduce 0 or 2): when the 256 x 256 workgroups fill whole rounds of 256 and then a quarter round
+    // or less, the channel blocks of the whole rounds run in the first launch and the remaining channels in
+    // a second launch on the same stream: one round of 128 x 128 workgroups of the same kernel where they
+    // number 128 to 256 (reduce 0), else (or with reduce 2) the wide kernel.  Token-tiled activations,
+    // gate_up M = 2048 (1024 workgroups, 2048 channels left): 304.5 us, 323.1 with the wide kernel's tail,
+    // 316.3 in one launch; qkv M = 2048: 92.1 / 112.9 / 111.9 us.  Past a quarter round one launch is
+    // faster (gate_up M = 4096, 128 past 2048: 600 us, 613 with two rounds of 128 x 128 workgroups).
+    const int nblocks = ceil_div(n_pad / kTileN, kW8A8TileTiles);
+    const int mblocks = ceil_div(M, kW8A8TileRows);
+    const int64_t twgs = (int64_t)nblocks * mblocks;
+    if (c.split_k > 1) {  // K split with the fused last-arrival reduction: one launch
+      out[0].grid = twgs * c.split_k;
+      return 1;
+    }
+    if (c.reduce == 3) {  // 256-channel x 128-token workgroups, one launch
+      out[0].kind = kW8a8TileHalf;
+      out[0].grid = (int64_t)nblocks * ceil_div(M, TileShape<8, 2>::rows);
+      return 1;
+    }
+    out[0].grid = twgs;
+    const int64_t whole = twgs / 256 * 256;
+    // Only a true remainder (0 < rest <= 64) is split off: with rest == 0 the whole rounds already hold
+    // every channel block, and their channel count nblocks * 256 may exceed N.
+    const int64_t rest = twgs - whole;
+    if (c.reduce == 1 || whole == 0 || rest == 0 || rest > 64 || whole % mblocks != 0) return 1;
+    const int n_main = (int)(whole / mblocks) * kW8A8TileTiles * kTileN;  // < N: the tail holds N's last block
+    const int n_tail = N - n_main;
+    if (n_main <= 0 || n_tail <= 0) return 1;  // not reached when rest > 0: one launch covers N
+    using Small = TileShape<4>;
+    const int64_t small = (int64_t)ceil_div(round_up16(n_tail) / kTileN, Small::tiles) * ceil_div(M, Small::rows);
+    W8a8Launch tail{kW8a8TileSmall, small, n_main, n_tail, c};
+    if (!(c.reduce == 0 && small >= 128 && small <= 256)) {
+      qf_w8a16_config ct = qf_w8a16_config{};
+      ct.kernel = QF_KERNEL_MFMA_W8A8;
+      ct.k_waves = 1;
+      ct.load_hint = 1;
+      ct.reduce = 1;
+      ct.split_k = 1;
+      ct.tiles_per_wave = 2;
+      ct.waves = 8;
+      ct.depth = 4;
+      if (!auto_config_w8a8_wide(M, n_tail, K, layout, &ct)) return 1;
+      ct.split_k = 1;  // no workspace: the tail runs unsplit
+      if (validate_w8a8(M, n_tail, K, layout, ct) != QF_OK) return 1;
+      int groups, rows;
+      w8a8_groups(ct, M, n_tail, groups, rows);
+      tail = W8a8Launch{kW8a8Wide, (int64_t)workgroups(ct, n_tail) * groups, n_main, n_tail, ct};
+    }
+    out[0].grid = whole;
+    out[0].n = n_main;
+    out[1] = tail;
+    return 2;
+  }
+  int groups, rows;
+  w8a8_groups(c, M, N, groups, rows);
+  out[0] = W8a8Launch{kW8a8Wide, (int64_t)workgroups(c, N) * groups * c.split_k, 0, N, c};
+  if (c.split_k == 1) return 1;
+  out[1] = W8a8Launch{kW8a8SplitReduce, ceil_div(M * (n_pad / 4), 256), 0, N, c};
+  return 2;
 }
 
 // x_tiled: xq is the token-tiled image (ldq unused).
@@ -2881,81 +2968,52 @@ int run_w8a8(const int8_t* xq, int64_t ldq, int x_tiled, const float* s_a, const
   a.out_f32 = out_dtype == QF_DTYPE_F32;
   a.vec_out = (ldy % 4) == 0;
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (c.kernel == QF_KERNEL_MFMA_W8A8_TILE) {
-    const bool rm = layout == QF_LAYOUT_ROWMAJOR;
-    KernelFn tf = rm ? &w8a8_tile_kernel<QF_LAYOUT_ROWMAJOR, 8> : &w8a8_tile_kernel<QF_LAYOUT_TILED, 8>;
-    // Tail (reduce 0 or 2): when the 256 x 256 workgroups fill whole rounds of 256 and then a quarter round
-    // or less, the channel blocks of the whole rounds run here and the remaining channels in a second
-    // launch on the same stream: one round of 128 x 128 workgroups of the same kernel where they number 128
-    // to 256 (reduce 0), else (or with reduce 2) the wide kernel.  Token-tiled activations, gate_up
-    // M = 2048 (1024 workgroups, 2048 channels left): 304.5 us, 323.1 with the wide kernel's tail, 316.3 in
-    // one launch; qkv M = 2048: 92.1 / 112.9 / 111.9 us.  Past a quarter round one launch is faster (gate_up
-    // M = 4096, 128 past 2048: 600 us, 613 with two rounds of 128 x 128 workgroups).
-    // Both launches write disjoint output columns; the sums are exact, so the result is the same.
-    const int nblocks = ceil_div(a.n_pad / kTileN, kW8A8TileTiles);
-    const int mblocks = ceil_div(M, kW8A8TileRows);
-    const int64_t twgs = (int64_t)nblocks * mblocks;
-    if (c.split_k > 1)  // K split with the fused last-arrival reduction: one launch
-      return launch(tf, dim3((unsigned)(twgs * c.split_k)), dim3(8 * kWave), kW8A8TileLds, s, a);
-    if (c.reduce == 3) {  // 256-channel x 128-token workgroups, one launch
-      using Half = TileShape<8, 2>;
-      const int64_t hwgs = (int64_t)nblocks * ceil_div(M, Half::rows);
-      return launch(rm ? &w8a8_tile_kernel<QF_LAYOUT_ROWMAJOR, 8, 2> : &w8a8_tile_kernel<QF_LAYOUT_TILED, 8, 2>,
-                    dim3((unsigned)hwgs), dim3(8 * kWave), Half::lds, s, a);
+  W8a8Launch plan[2];
+  const int nl = w8a8_plan(M, N, K, layout, c, plan);
+  if (nl < 1) return nl < 0 ? -nl : QF_ERR_UNSUPPORTED;
+  const bool rm = layout == QF_LAYOUT_ROWMAJOR;
+  for (int i = 0; i < nl; ++i) {
+    const W8a8Launch& p = plan[i];
+    GemmArgs al = a;
+    if (p.n0 != 0 || p.n != N) {  // a channel range of the call: its weights, scales and output columns
+      al.N = p.n;
+      al.n_pad = p.kind == kW8a8Tile ? p.n : round_up16(p.n);
+      al.w = a.w + (layout == QF_LAYOUT_TILED ? (int64_t)(p.n0 / kTileN) * a.ksteps * kTileN * kStepK
+                                              : (int64_t)p.n0 * a.ldw);
+      al.scale = a.scale + p.n0;
+      al.y = reinterpret_cast<uint8_t*>(a.y) + (size_t)p.n0 * (a.out_f32 ? 4 : 2);
     }
-    const int64_t whole = twgs / 256 * 256;
-    if (c.reduce != 1 && whole > 0 && twgs - whole <= 64 && whole % mblocks == 0) {
-      const int n_main = (int)(whole / mblocks) * kW8A8TileTiles * kTileN;  // < N: the tail holds N's last block
-      const int n_tail = N - n_main;
-      GemmArgs at = a;
-      at.N = n_tail;
-      at.n_pad = round_up16(n_tail);
-      at.w = a.w + (layout == QF_LAYOUT_TILED ? (int64_t)(n_main / kTileN) * a.ksteps * kTileN * kStepK
-                                              : (int64_t)n_main * a.ldw);
-      at.scale = a.scale + n_main;
-      at.y = reinterpret_cast<uint8_t*>(a.y) + (size_t)n_main * (a.out_f32 ? 4 : 2);
-      using Small = TileShape<4>;
-      const int64_t small = (int64_t)ceil_div(at.n_pad / kTileN, Small::tiles) * ceil_div(M, Small::rows);
-      const bool use_small = c.reduce == 0 && small >= 128 && small <= 256;
-      qf_w8a16_config ct = qf_w8a16_config{};
-      ct.kernel = QF_KERNEL_MFMA_W8A8;
-      ct.k_waves = 1;
-      ct.load_hint = 1;
-      ct.reduce = 1;
-      ct.split_k = 1;
-      ct.tiles_per_wave = 2;
-      ct.waves = 8;
-      ct.depth = 4;
-      bool use_wide = false;
-      if (!use_small && auto_config_w8a8_wide(M, n_tail, K, layout, &ct)) {
-        ct.split_k = 1;  // no workspace: the tail runs unsplit
-        use_wide = validate_w8a8(M, n_tail, K, layout, ct) == QF_OK;
-      }
-      if (use_small || use_wide) {
-        GemmArgs am = a;
-        am.N = n_main;
-        am.n_pad = n_main;
-        const int st = launch(tf, dim3((unsigned)whole), dim3(8 * kWave), kW8A8TileLds, s, am);
-        if (st != QF_OK) return st;
-        if (use_small)
-          return launch(rm ? &w8a8_tile_kernel<QF_LAYOUT_ROWMAJOR, 4> : &w8a8_tile_kernel<QF_LAYOUT_TILED, 4>,
-                        dim3((unsigned)small), dim3(8 * kWave), Small::lds, s, at);
-        w8a8_groups(ct, M, n_tail, at.groups, at.group_rows);
-        KernelFn fn = select_w8a8(layout, ct.tiles_per_wave, at.group_rows / 16, ct.waves, ct.depth);
+    int st = QF_ERR_UNSUPPORTED;
+    switch (p.kind) {
+      case kW8a8Tile:
+        st = launch(rm ? &w8a8_tile_kernel<QF_LAYOUT_ROWMAJOR, 8> : &w8a8_tile_kernel<QF_LAYOUT_TILED, 8>,
+                    dim3((unsigned)p.grid), dim3(8 * kWave), kW8A8TileLds, s, al);
+        break;
+      case kW8a8TileHalf:
+        st = launch(rm ? &w8a8_tile_kernel<QF_LAYOUT_ROWMAJOR, 8, 2> : &w8a8_tile_kernel<QF_LAYOUT_TILED, 8, 2>,
+                    dim3((unsigned)p.grid), dim3(8 * kWave), TileShape<8, 2>::lds, s, al);
+        break;
+      case kW8a8TileSmall:
+        st = launch(rm ? &w8a8_tile_kernel<QF_LAYOUT_ROWMAJOR, 4> : &w8a8_tile_kernel<QF_LAYOUT_TILED, 4>,
+                    dim3((unsigned)p.grid), dim3(8 * kWave), TileShape<4>::lds, s, al);
+        break;
+      case kW8a8Wide: {
+        w8a8_groups(p.cfg, M, p.n, al.groups, al.group_rows);
+        KernelFn fn = select_w8a8(layout, p.cfg.tiles_per_wave, al.group_rows / 16, p.cfg.waves, p.cfg.depth);
         if (fn == nullptr) return QF_ERR_UNSUPPORTED;
-        return launch(fn, dim3(workgroups(ct, n_tail) * at.groups), dim3(ct.waves * kWave),
-                      w8a8_lds_bytes(ct, M, n_tail), s, at);
+        al.split_k = p.cfg.split_k;
+        st = launch(fn, dim3((unsigned)p.grid), dim3(p.cfg.waves * kWave), w8a8_lds_bytes(p.cfg, M, p.n), s, al);
+        break;
       }
+      case kW8a8SplitReduce:
+        st = launch(&splitk_reduce_w8a8_kernel, dim3((unsigned)p.grid), dim3(256), 0, s, al);
+        break;
+      default:
+        return QF_ERR_UNSUPPORTED;
     }
-    return launch(tf, dim3((unsigned)twgs), dim3(8 * kWave), kW8A8TileLds, s, a);
+    if (st != QF_OK) return st;
   }
-  w8a8_groups(c, M, N, a.groups, a.group_rows);
-  KernelFn fn = select_w8a8(layout, c.tiles_per_wave, a.group_rows / 16, c.waves, c.depth);
-  if (fn == nullptr) return QF_ERR_UNSUPPORTED;
-  int st = launch(fn, dim3(workgroups(c, N) * a.groups * c.split_k), dim3(c.waves * kWave), w8a8_lds_bytes(c, M, N),
-                  s, a);
-  if (st != QF_OK || c.split_k == 1) return st;
-  return launch(&splitk_reduce_w8a8_kernel, dim3(ceil_div(M * (a.n_pad / 4), 256)), dim3(256), 0, s, a);
+  return QF_OK;
 }
 
 int argmax_rows(const uint16_t* logits, int64_t ld, int M, int N, int n_valid, int64_t index_offset, int64_t* out,
@@ -3186,6 +3244,27 @@ int qf_quantize_tokens_int8_tiled(const uint16_t* x, int64_t ldx, int M, int K, 
 int qf_w8a8_pick_config(int M, int N, int K, int layout, qf_w8a16_config* cfg) {
   if (cfg == nullptr) return QF_ERR_INVALID_ARG;
   return auto_config_w8a8(M, N, K, layout, cfg) ? QF_OK : QF_ERR_UNSUPPORTED;
+}
+
+int qf_w8a8_launch_plan(int M, int N, int K, int layout, const qf_w8a16_config* cfg, int64_t* out, int* count) {
+  if (out == nullptr || count == nullptr) return QF_ERR_INVALID_ARG;
+  *count = 0;
+  if (M < 1 || N < 1 || K < 1) return QF_ERR_INVALID_ARG;
+  if (K % QF_W8A16_K_ALIGN) return QF_ERR_UNSUPPORTED;
+  qf_w8a16_config c;
+  const int rc = qf::resolve_w8a8(M, N, K, layout, cfg, &c);
+  if (rc != QF_OK) return rc;
+  qf::W8a8Launch plan[2];
+  const int nl = qf::w8a8_plan(M, N, K, layout, c, plan);
+  if (nl < 1) return nl < 0 ? -nl : QF_ERR_UNSUPPORTED;
+  for (int i = 0; i < nl; ++i) {
+    out[4 * i + 0] = plan[i].kind;
+    out[4 * i + 1] = plan[i].grid;
+    out[4 * i + 2] = plan[i].n0;
+    out[4 * i + 3] = plan[i].n;
+  }
+  *count = nl;
+  return QF_OK;
 }
 
 size_t qf_w8a8_workspace_bytes(int M, int N, int K, int layout, const qf_w8a16_config* cfg) {

@@ -66,6 +66,7 @@ EXPORTS = (
     "qf_w8a8_gemm_xt",
     "qf_w8a8_pick_config",
     "qf_w8a8_workspace_bytes",
+    "qf_w8a8_launch_plan",
 )
 
 
@@ -172,6 +173,9 @@ def load() -> ctypes.CDLL:
     L.qf_w8a8_pick_config.restype = i32
     L.qf_w8a8_workspace_bytes.argtypes = [i32, i32, i32, i32, ctypes.POINTER(Config)]
     L.qf_w8a8_workspace_bytes.restype = sz
+    L.qf_w8a8_launch_plan.argtypes = [i32, i32, i32, i32, ctypes.POINTER(Config), ctypes.POINTER(i64),
+                                      ctypes.POINTER(ctypes.c_int)]
+    L.qf_w8a8_launch_plan.restype = i32
     L.qf_read_probe.argtypes = [p, sz, p, i32, p]
     L.qf_read_probe.restype = i32
     v = L.qf_abi_version()
@@ -209,6 +213,19 @@ def w8a8_pick_config(M: int, N: int, K: int, layout: int = LAYOUT_TILED) -> Conf
         return None
     check(rc, "qf_w8a8_pick_config")
     return c
+
+
+W8A8_LAUNCH_KINDS = ("tile", "tile_256x128", "tile_128x128", "wide", "split_reduce")
+
+
+def w8a8_launch_plan(M: int, N: int, K: int, layout: int = LAYOUT_TILED, cfg: Config | None = None) -> list[tuple]:
+    """The launches qf_w8a8_gemm makes, in stream order: (kind name, workgroups, first channel, channels)."""
+    out = (ctypes.c_int64 * 8)()
+    count = ctypes.c_int(0)
+    check(load().qf_w8a8_launch_plan(M, N, K, layout, ctypes.byref(cfg) if cfg is not None else None, out,
+                                     ctypes.byref(count)), "qf_w8a8_launch_plan")
+    return [(W8A8_LAUNCH_KINDS[out[4 * i]], int(out[4 * i + 1]), int(out[4 * i + 2]), int(out[4 * i + 3]))
+            for i in range(count.value)]
 
 
 def capture_id(stream_handle: int) -> int:

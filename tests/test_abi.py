@@ -252,6 +252,59 @@ def test_prefill_arithmetic_switch(monkeypatch):
         P.prefill_arithmetic()
 
 
+def test_w8a8_launch_plan_host_only():
+    """The launches qf_w8a8_gemm makes: their channel ranges are disjoint and cover [0, N) in order, every
+    grid is non-empty, and a second launch is taken only for a true remainder of 1 to 64 workgroups past whole
+    rounds of 256.  Grids that are whole rounds (rest 0) run in one launch, including N not a multiple of
+    256 (N = 8000 at M = 2048: 32 x 8 = 256 workgroups), where a split would give the first launch more
+    channels than N."""
+    def check_plan(M, N, K, layout=1, cfg=None):
+        plan = L.w8a8_launch_plan(M, N, K, layout, cfg)
+        assert 1 <= len(plan) <= 2, (M, N, K, plan)
+        n = 0
+        for kind, grid, n0, cnt in plan:
+            if kind == "split_reduce":
+                assert (n0, cnt) == (0, N) and grid > 0, (M, N, K, plan)
+                continue
+            assert grid > 0 and cnt > 0 and n0 == n, (M, N, K, plan)
+            n += cnt
+        assert n == N, (M, N, K, plan)
+        return plan
+    tile = L.Config.from_seq((L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 4, 1, 1, 0))
+    tile2 = L.Config.from_seq((L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 4, 1, 1, 2))
+    # whole rounds, rest 0: one launch over all N (the automatic rule and the explicit tile configs)
+    for M, N, K in ((8192, 10240, 5120), (8192, 34816, 5120), (16384, 5120, 8192), (16384, 5120, 17408),
+                    (2048, 8000, 128), (2048, 8192, 128), (4096, 8000, 5120)):
+        for layout in (1, 0):
+            for cfg in (None, tile, tile2):
+                plan = check_plan(M, N, K, layout, cfg)
+                assert len(plan) == 1 and plan[0][0] == "tile", (M, N, K, layout, plan)
+                assert plan[0][1] == -(-N // 256) * -(-M // 256), (M, N, K, plan)
+    # a true remainder: whole rounds on the 256 x 256 kernel, the rest on 128 x 128 workgroups or the wide kernel
+    plan = check_plan(2048, 34816, 5120)  # 1088 = 4 x 256 + 64
+    assert plan == [("tile", 1024, 0, 32768), ("tile_128x128", 256, 32768, 2048)], plan
+    plan = check_plan(4096, 4352, 256, 1, tile)  # 272 = 256 + 16: the last block on the wide kernel
+    assert [p[0] for p in plan] == ["tile", "wide"] and plan[0][3] == 4096, plan
+    plan = check_plan(4096, 4700, 128, 1, tile2)
+    assert [p[0] for p in plan] == ["tile", "wide"], plan
+    # the other kinds
+    assert check_plan(384, 34816, 5120)[0][0] == "tile_256x128"
+    assert [p[0] for p in check_plan(17, 5120, 17408)] == ["wide", "split_reduce"]
+    assert [p[0] for p in check_plan(1024, 5120, 17408)] == ["tile"]  # K split, fused reduction
+    # a sweep of shapes around whole rounds
+    for N in (4096, 4100, 8000, 8192, 8200, 10240, 12288, 16384, 34816):
+        for M in (256, 512, 1000, 1024, 2048, 4096, 8192):
+            for layout in (1, 0):
+                check_plan(M, N, 128, layout)
+                check_plan(M, N, 128, layout, tile)
+                check_plan(M, N, 128, layout, tile2)
+    out = (ctypes.c_int64 * 8)()
+    cnt = ctypes.c_int(7)
+    assert L.load().qf_w8a8_launch_plan(40, 0, 1024, 1, None, out, ctypes.byref(cnt)) == L.ERR_INVALID_ARG
+    assert cnt.value == 0
+    assert L.load().qf_w8a8_launch_plan(40, 100, 1000, 1, None, out, ctypes.byref(cnt)) == L.ERR_UNSUPPORTED
+
+
 def test_w8a8_configs_host_only():
     """qf_w8a8_gemm: either layout (row-major: the automatic shape only), its own kernel kind, any M;
     refused before any launch otherwise."""

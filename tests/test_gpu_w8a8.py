@@ -359,6 +359,27 @@ def test_w8a8_tile_kernel_tail_split(M, N, K):
                         assert torch.isnan(y[:, N:].float()).all(), case
 
 
+@pytest.mark.parametrize("M,N,K", [(2048, 8192, 128), (2048, 8000, 128)])
+def test_w8a8_tile_kernel_whole_rounds(M, N, K):
+    """Tile grids that are whole rounds of 256 workgroups (rest 0: 32 channel blocks x 8 token blocks) run in
+    one launch: N = 8192, and N = 8000, whose blocks hold 8192 channel slots.  Bit for bit against the
+    restatement with reduce 0, 2 and 1 and the automatic configuration, on both layouts, with nothing written
+    past N."""
+    x, w, s = random_case(M, N, K, N + 5 * K)
+    wt = qf.to_tiled(w.t())
+    ref = P.w8a8_reference(x, w.t(), s, None, torch.bfloat16)
+    cfgs = [(L.KERNEL_MFMA_W8A8_TILE, 1, 8, 8, 4, 1, 1, red) for red in (0, 2, 1)]
+    for layout, wp, ldw in ((qf.TILED, wt, 0), (qf.ROWMAJOR, w, K)):
+        auto = L.w8a8_pick_config(M, N, K, layout).to_tuple()
+        for cfg in cfgs + [auto]:
+            print(f"whole rounds M={M} N={N} K={K} layout={layout} cfg={cfg}", flush=True)
+            y = torch.full((M, N + 8), float("nan"), dtype=torch.bfloat16, device=DEV)
+            w8a8_into(x, wp, s, layout, ldw, y, torch.bfloat16, cfg)
+            torch.cuda.synchronize()
+            assert torch.equal(bits(y[:, :N]), bits(ref)), (M, N, K, layout, cfg)
+            assert torch.isnan(y[:, N:].float()).all(), (M, N, K, layout, cfg)
+
+
 @pytest.mark.parametrize("M,N,K,split", [(300, 1000, 640, 2), (300, 1000, 640, 3), (1000, 5120, 8192, 3),
                                          (520, 1004, 1024, 4), (256, 512, 128, 2), (17, 4112, 5120, 8),
                                          (513, 16, 192, 3), (2048, 1280, 17408, 5)])
