@@ -99,12 +99,16 @@ def _weight_geometry(w: torch.Tensor, N: int, K: int, layout: int) -> int:
 # different streams never do, so they may overlap.  The library's arrival counters at the front of a
 # workspace must be zero when a call starts and every call leaves them zero, so:
 # * an eager workspace is allocated zeroed, grown by doubling, and reused by every later call on its
-#   stream;
-# * inside a graph capture, calls get a workspace of that capture (keyed by the capture id), whose
-#   counters are cleared by a fill kernel recorded into the graph ahead of its first use: each replay
-#   starts from zero, whatever ran on the stream before.  It stays allocated with the graph's memory.
+#   stream; it is kept for the life of the process (one per stream that ran the op);
+# * inside a graph capture, calls get a workspace allocated during that capture (so from the graph's
+#   memory pool), whose counters are cleared by a fill kernel recorded into the graph ahead of its first
+#   use: each replay starts from zero, whatever ran on the stream before.  This module holds it only while
+#   the capture is the latest one on its stream; a later capture there releases it, and the graph keeps
+#   the memory as it keeps its other intermediates (graphs that share a memory pool may then reuse it,
+#   which torch already requires to be replayed one at a time).  So the held capture memory is at most one
+#   capture's largest workspace per capture stream, not one per captured size.
 _workspaces: dict[tuple, torch.Tensor] = {}
-_capture_keep: list[torch.Tensor] = []  # superseded capture workspaces still referenced by their graph
+_capture_ws: dict[tuple, tuple[int, list[torch.Tensor]]] = {}  # (device, stream) -> (capture id, buffers)
 _WS_MIN = 8 << 20
 
 
@@ -112,15 +116,19 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     dev = device.index if device.index is not None else torch.cuda.current_device()
     handle = torch.cuda.current_stream(device).cuda_stream
     if torch.cuda.is_current_stream_capturing():
-        key = (dev, handle, L.capture_id(handle))
-        ws = _workspaces.get(key)
-        if ws is None or ws.numel() < nbytes:
-            if ws is not None:
-                _capture_keep.append(ws)
+        cid = L.capture_id(handle)
+        entry = _capture_ws.get((dev, handle))
+        if entry is None or entry[0] != cid:
+            entry = (cid, [])  # a new capture on this stream: the previous capture's buffers are released
+            _capture_ws[(dev, handle)] = entry
+        bufs = entry[1]
+        if not bufs or bufs[-1].numel() < nbytes:
+            # a larger buffer for the rest of this capture; the earlier ones stay held until it ends, since
+            # launches already recorded use them
             ws = torch.empty(max(nbytes, L.COUNTER_BYTES), dtype=torch.uint8, device=device)
             ws[:L.COUNTER_BYTES].zero_()
-            _workspaces[key] = ws
-        return ws
+            bufs.append(ws)
+        return bufs[-1]
     key = (dev, handle)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:

@@ -186,3 +186,40 @@ def test_capture_without_warmup(oracle):
         assert torch.equal(y, eager)
         qf.w8a16_mm(x, img, s, cfg, torch.bfloat16, qf.TILED)  # eager call between replays
     assert oracle.check_w8a16(bf16_bits(eager), inp.x, inp.w, inp.s).ok
+
+
+def test_capture_workspaces_released_between_captures(oracle):
+    """A capture's workspace is held by the package only while that capture is the latest on its stream.
+    Three graphs captured one after another on one stream (split-K calls of three widths, whose workspaces
+    differ in size; the third shares the second's memory pool) replay correctly, in any order and with
+    eager calls between replays, after the earlier captures' workspaces were released; the package then
+    holds the buffers of the last capture only."""
+    from qwen_fastpath import w8a16 as W
+    N, K = 1024, 17408
+    inp, x16, w, s = _inputs(oracle, 16, N, K, 21)
+    img = qf.to_tiled(w)
+    cfg = qf.W8A16Config(2, 4, 1, 8, 4, 1, 2, 0)  # fused four-way K split: partials sized by M
+    st = torch.cuda.Stream()
+    graphs, outs, want = [], [], []
+    for i, M in enumerate((5, 16, 9)):
+        x = x16[:M]
+        want.append(qf.w8a16_mm(x, img, s, cfg, torch.bfloat16, qf.TILED))
+        g = torch.cuda.CUDAGraph()
+        pool = graphs[1].pool() if i == 2 else None
+        with torch.cuda.graph(g, stream=st, pool=pool):
+            outs.append(qf.w8a16_mm(x, img, s, cfg, torch.bfloat16, qf.TILED))
+        graphs.append(g)
+        held = [k for k in W._capture_ws if k[1] == st.cuda_stream]
+        assert len(held) == 1 and len(W._capture_ws[held[0]][1]) == 1, W._capture_ws
+    torch.cuda.synchronize()
+    junk = [torch.randn(1 << 20, device=DEV) for _ in range(8)]  # allocations between capture and replay
+    for rep, order in enumerate(((0, 1, 2), (2, 0, 1), (1, 2, 0))):
+        for j in order:
+            outs[j].zero_()
+            graphs[j].replay()
+            torch.cuda.synchronize()
+            assert torch.equal(outs[j], want[j]), (rep, j)
+            qf.w8a16_mm(x16[:7], img, s, cfg, torch.bfloat16, qf.TILED)  # eager call between replays
+    del junk
+    for M, y in zip((5, 16, 9), want):
+        assert oracle.check_w8a16(bf16_bits(y), inp.x[:M], inp.w, inp.s).ok

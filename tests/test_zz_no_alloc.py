@@ -43,6 +43,35 @@ def _case(M, N, K, seed):
     return x, img, s
 
 
+def test_noalloc_first_call_inside_graph_capture():
+    """The file's first test, so that in a fresh process the library's first no-alloc call on the device
+    happens inside a graph capture: the scratch address is fetched there and its counter-clearing kernel is
+    recorded into the graph.  The graph, replayed three times with eager calls of both entry points between
+    the replays, equals qf_w8a16_gemm bit for bit (a fused four-way K split, whose counters must start at zero
+    on every replay)."""
+    lib = L.load()
+    M, N, K, cfg = 5, 1024, 17408, (2, 4, 1, 8, 4, 1, 2, 0)
+    x, img, s = _case(M, N, K, 7)
+    c = L.Config.from_seq(cfg)
+    y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=DEV)
+    st = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    print("noalloc: capturing the first call", flush=True)
+    with torch.cuda.graph(g, stream=st):
+        rc = lib.qf_w8a16_gemm_noalloc(x.data_ptr(), K, img.data_ptr(), K, L.LAYOUT_TILED, s.data_ptr(),
+                                       y.data_ptr(), N, L.DTYPE_BF16, M, N, K, ctypes.byref(c),
+                                       torch.cuda.current_stream().cuda_stream)
+    L.check(rc, "noalloc inside capture")
+    want = _gemm(lib, x, img, s, N, K, cfg, noalloc=False)
+    for rep in range(3):
+        y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), want.view(torch.int16)), rep
+        eager = _gemm(lib, x, img, s, N, K, cfg, noalloc=True)
+        assert torch.equal(eager.view(torch.int16), want.view(torch.int16)), rep
+
+
 # (M, N, K, config): the first call of each pair is the larger one
 PAIRS = [
     ((5, 5120, 17408, (2, 3, 1, 8, 4, 1, 2, 0)), (3, 1024, 8192, (2, 4, 1, 8, 4, 1, 2, 0))),   # fused split
