@@ -82,7 +82,7 @@ typedef enum qf_kernel {
                                with 4 waves at depth 2 */
   QF_KERNEL_MFMA_W8A8 = 5,  /* qf_w8a8_gemm only: the same tiling on v_mfma_i32_16x16x64_i8 with int8
                                activations; tiles_per_wave 2 or 4, 4 or 8 waves, depth 2 or 4 */
-  QF_KERNEL_MFMA_W8A8_TILE = 6 /* qf_w8a8_gemm only, either layout, picked for large M x N: 256-channel x
+  QF_KERNEL_MFMA_W8A8_TILE = 6, /* qf_w8a8_gemm only, either layout, picked for large M x N: 256-channel x
                                256-token workgroups, both operands staged in LDS by direct-to-LDS copies
                                through a 4-stage ring; waves 8, tiles_per_wave 8, depth 4; split_k 1 to 8
                                (at most K/64): split_k copies of the grid each sum a K range and the last
@@ -94,6 +94,10 @@ typedef enum qf_kernel {
                                QF_KERNEL_MFMA_W8A8 kernel; reduce 2 on the latter only; reduce 1: one
                                launch; reduce 3 (split_k 1): one launch of 256-channel x 128-token
                                workgroups */
+  QF_KERNEL_MFMA_STREAM = 7 /* TILED layout, M <= 16: one workgroup per CU, each over a contiguous run of
+                               16-row tiles and the whole K range; its waves (8, or 16 at depth 8) all split
+                               K (k_waves == waves) with a depth-step prefetch ring (8, 12 or 16) that runs
+                               across tile boundaries; split_k 1, tiles_per_wave 1, load_hint 1 */
 } qf_kernel;
 
 /* Launch configuration.  A zero field means "choose automatically". */

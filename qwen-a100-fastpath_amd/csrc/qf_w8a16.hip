@@ -685,6 +685,128 @@ __global__ void __launch_bounds__(WN * WK * kWave)
 }
 
 // ---------------------------------------------------------------------------------------------
+// Stream kernel (QF_KERNEL_MFMA_STREAM), TILED layout, M <= 16: the whole weight image in one resident
+// round of workgroups.
+//
+// The grid is G workgroups, one per CU (G = the device's CU count), so every workgroup starts at once and
+// none stages x after another has begun streaming.  Workgroup b owns the contiguous run of 16-row tiles
+// [b * ntiles / G, (b + 1) * ntiles / G).  Its W wavefronts interleave over k: wavefront v takes the k-steps
+// v, v + W, v + 2 W, ... of every tile of the run, tile after tile, as one stream, with a DEPTH-step prefetch
+// ring that runs across tile boundaries (W * DEPTH KiB of weight loads in flight per CU).  At any moment the
+// W wavefronts read W adjacent KiB of one tile.  x (the whole [M, K] slice) is staged in LDS once, with the
+// first DEPTH steps of weights requested before the barrier.
+//
+// Sums, in a fixed order: wavefront v sums its k-steps of a tile in increasing k (two MFMAs a step); when it
+// leaves the tile it writes that partial tile to LDS ([tile][wavefront] slots, 1 KiB each).  After the run,
+// wavefront v reduces tiles v, v + W, ...: the W partials in wavefront order, then the scale, then one bf16
+// rounding.  Results are bitwise reproducible; they differ from w8a16_mfma_kernel's (whose k-slices are
+// interleaved four ways) only in fp32 summation order.
+// ---------------------------------------------------------------------------------------------
+__host__ __device__ __forceinline__ int align16i(int n) { return (n + 15) & ~15; }
+
+template <int W, int DEPTH, bool NTH>
+__global__ void __launch_bounds__(W * kWave) w8a16_stream_kernel(const GemmArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  constexpr int RING = DEPTH + 1;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int v = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int g = lane >> 4;
+  const int r = lane & 15;
+  const int ntiles = a.n_pad / kTileN;
+  const int t0 = (int)(((int64_t)blockIdx.x * ntiles) / gridDim.x);
+  const int t1 = (int)(((int64_t)(blockIdx.x + 1) * ntiles) / gridDim.x);
+  const int nt = t1 - t0;
+  if (nt <= 0) return;  // uniform over the workgroup: more workgroups than tiles
+  const int ksteps = a.ksteps;
+  const int S = (ksteps - v + W - 1) / W;  // k-steps of this wavefront in each tile, >= 1 (ksteps >= W)
+  const int total = nt * S;                // steps of this wavefront over the run
+  const int pitch = x_pitch(ksteps);
+  f32x4_t* part = reinterpret_cast<f32x4_t*>(smem + align16i(a.M * pitch));  // [nt][W][64 lanes]
+
+  // Prefetch cursor: the weight fragment of step pi (tile pi / S, k-step v + (pi % S) W) for this lane.
+  // Past the last step the cursor stays on it (an in-bounds re-read), so every load is unconditional.
+  const int8_t* pf = a.w + (((int64_t)t0 * ksteps + v) * kWave + lane) * 16;
+  const int64_t step_b = (int64_t)W * kTileN * kStepK;
+  const int64_t wrap_b = (int64_t)(ksteps - (S - 1) * W) * kTileN * kStepK;
+  int pi = 0, pj = 0;
+  auto advance = [&]() {
+    if (pi < total - 1) {
+      ++pi;
+      if (++pj < S) {
+        pf += step_b;
+      } else {
+        pj = 0;
+        pf += wrap_b;
+      }
+    }
+  };
+
+  u32x4_t buf[RING];
+  XStage<W * kWave> xst(a, 0, ksteps);
+  auto prologue = [&]() {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      buf[d] = load16<NTH>(pf);
+      advance();
+    }
+  };
+  if (xst.single_batch()) {  // uniform
+    xst.load_batch(a, 0);
+    __builtin_amdgcn_sched_barrier(0);  // the x requests go out before the weight requests
+    prologue();
+    __builtin_amdgcn_sched_barrier(0);
+    xst.store_batch(smem, 0);
+  } else {
+    xst.copy_all(a, smem);
+    prologue();
+  }
+  lds_barrier();  // the weight requests issued above stay in flight across it
+
+  // Lane (g, r) reads x[min(r, M - 1)][k + 16 g .. + 15] of each step (token rows r >= M are never stored).
+  const uint8_t* xrow = smem + min(r, a.M - 1) * pitch + 32 * g;
+  const uint32_t x0 = (uint32_t)v * (kStepK * 2);
+  uint32_t xoff = x0;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  int cj = 0, tl = 0;
+  for (int base = 0; base < total; base += RING) {
+#pragma unroll
+    for (int d = 0; d < RING; ++d) {
+      buf[(d + DEPTH) % RING] = load16<NTH>(pf);
+      advance();
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch issue ahead of this step's math
+      if (base + d < total) {             // uniform
+        const u32x4_t* xp = reinterpret_cast<const u32x4_t*>(xrow + xoff);
+        const bf16x8_t xb0 = __builtin_bit_cast(bf16x8_t, xp[0]);
+        const bf16x8_t xb1 = __builtin_bit_cast(bf16x8_t, xp[1]);
+        bf16x8_t w0, w1;
+        dequant16(buf[d], w0, w1);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, xb0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, xb1, acc, 0, 0, 0);
+        if (++cj < S) {
+          xoff += W * kStepK * 2;
+        } else {  // this wavefront's share of the tile is done: park its partial
+          part[(tl * W + v) * kWave + lane] = acc;
+          acc = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+          ++tl;
+          cj = 0;
+          xoff = x0;
+        }
+      }
+    }
+  }
+  lds_barrier();
+  // Lane (g, r) holds C[n = tile * 16 + 4 g + i][m = r], i = 0..3, in each partial.
+  for (int t = v; t < nt; t += W) {
+    f32x4_t sum = part[(t * W) * kWave + lane];
+#pragma unroll
+    for (int u = 1; u < W; ++u) sum += part[(t * W + u) * kWave + lane];
+    const int n = (t0 + t) * kTileN + 4 * g;
+    if (r < a.M && n < a.N)
+      store_out4(a.y, a.ldy, a.out_f32, a.vec_out, r, n, min(4, a.N - n), sum * load_scale4(a.scale, a.N, n));
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Wide-M MFMA kernel, TILED layout: M > 16 (prefill chunks, long verification batches).
 //
 // A workgroup owns WN * NT 16-row weight tiles over the whole K range (one wavefront per NT tiles,
@@ -2137,6 +2259,54 @@ KernelFn select_mfma(int layout, int nt, int waves, int k_waves, int depth, int 
 
 inline bool is_mfma(int kernel) { return kernel == QF_KERNEL_MFMA || kernel == QF_KERNEL_MFMA_XRING; }
 
+// Stream-kernel instantiations (TILED weights, non-temporal loads): 8 wavefronts at depth 2, 3, 4, 5, 6, 8, 12
+// or 16; 16 wavefronts at depth 2, 4 or 8.  Both keep the accumulator in VGPRs.  (A 4-wavefront build, one
+// wavefront per SIMD, was 20% slower on gate_up and gave wrong sums: its compiled loop moves the
+// conditionally cleared accumulator between AGPRs and VGPRs; it is not instantiated.)
+KernelFn select_stream(int waves, int depth, int hint) {
+  if (!hint) return nullptr;
+  if (waves == 8) {
+    if (depth == 2) return &w8a16_stream_kernel<8, 2, true>;
+    if (depth == 3) return &w8a16_stream_kernel<8, 3, true>;
+    if (depth == 4) return &w8a16_stream_kernel<8, 4, true>;
+    if (depth == 5) return &w8a16_stream_kernel<8, 5, true>;
+    if (depth == 6) return &w8a16_stream_kernel<8, 6, true>;
+    if (depth == 8) return &w8a16_stream_kernel<8, 8, true>;
+    if (depth == 12) return &w8a16_stream_kernel<8, 12, true>;
+    if (depth == 16) return &w8a16_stream_kernel<8, 16, true>;
+  }
+  if (waves == 16) {
+    if (depth == 2) return &w8a16_stream_kernel<16, 2, true>;
+    if (depth == 4) return &w8a16_stream_kernel<16, 4, true>;
+    if (depth == 8) return &w8a16_stream_kernel<16, 8, true>;
+  }
+  return nullptr;
+}
+
+// Compute units of the current device (the stream kernel's grid), cached per device; 256 (an MI355X)
+// when no device is visible, so that host-only configuration queries still answer.
+constexpr int kMaxCuDevices = 64;
+std::mutex g_cu_mutex;
+int g_cu_count[kMaxCuDevices];
+
+int device_cus() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxCuDevices) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  std::lock_guard<std::mutex> lock(g_cu_mutex);
+  if (g_cu_count[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) {
+      (void)hipGetLastError();
+      return 256;
+    }
+    g_cu_count[dev] = n;
+  }
+  return g_cu_count[dev];
+}
+
 // Wide-M instantiations: NT {1, 2} x MT {1..4} x WN {4, 8} x DEPTH {4, 8}, and NT 4 x MT {1..4} with 4
 // wavefronts and DEPTH 2 (non-temporal weight loads).
 template <int NT, int MT>
@@ -2214,8 +2384,11 @@ inline int round_up16(int n) { return (n + 15) / 16 * 16; }
 
 // LDS bytes of one workgroup: the largest split's x slice, or, for MFMA with k_waves > 1, the
 // slice-reduction buffer if that is larger.
-size_t lds_bytes(const qf_w8a16_config& c, int M, int ksteps) {
+size_t lds_bytes(const qf_w8a16_config& c, int M, int ksteps, int N) {
   const int steps = ceil_div(ksteps, c.split_k);
+  if (c.kernel == QF_KERNEL_MFMA_STREAM)  // the x slice, then a 1 KiB partial per (tile of the run, wavefront)
+    return (size_t)align16i(M * x_pitch(ksteps)) +
+           (size_t)ceil_div(round_up16(N) / kTileN, device_cus()) * c.waves * kWave * sizeof(f32x4_t);
   if (c.kernel == QF_KERNEL_GEMV) return (size_t)M * steps * kStepK * 2;
   if (c.kernel == QF_KERNEL_MFMA_WIDE) {
     int groups, rows;
@@ -2231,6 +2404,7 @@ size_t lds_bytes(const qf_w8a16_config& c, int M, int ksteps) {
 
 int workgroups(const qf_w8a16_config& c, int N) {
   if (c.kernel == QF_KERNEL_GEMV) return ceil_div(N, c.waves * c.tiles_per_wave);
+  if (c.kernel == QF_KERNEL_MFMA_STREAM) return device_cus();
   const int wn = c.waves / c.k_waves;
   return ceil_div(round_up16(N) / kTileN, wn * c.tiles_per_wave);
 }
@@ -2248,9 +2422,18 @@ size_t workspace_for(const qf_w8a16_config& c, int M, int N) {
 // Checks a complete configuration against the instantiated kernels and the LDS budget.
 int validate_config(int M, int N, int K, int layout, const qf_w8a16_config& c) {
   const int ksteps = K / kStepK;
-  if (c.kernel != QF_KERNEL_GEMV && !is_mfma(c.kernel) && c.kernel != QF_KERNEL_MFMA_WIDE) return QF_ERR_INVALID_ARG;
+  if (c.kernel != QF_KERNEL_GEMV && !is_mfma(c.kernel) && c.kernel != QF_KERNEL_MFMA_WIDE &&
+      c.kernel != QF_KERNEL_MFMA_STREAM)
+    return QF_ERR_INVALID_ARG;
   if (c.split_k < 1 || c.split_k > ksteps || c.waves < 1 || c.k_waves < 1 || c.tiles_per_wave < 1)
     return QF_ERR_INVALID_ARG;
+  if (c.kernel == QF_KERNEL_MFMA_STREAM) {
+    // TILED weights, M <= 16, one workgroup per CU over the whole K range, every wavefront splitting K.
+    if (layout != QF_LAYOUT_TILED || M > QF_W8A16_MAX_M) return QF_ERR_UNSUPPORTED;
+    if (c.split_k != 1 || c.k_waves != c.waves || c.tiles_per_wave != 1 || ksteps < c.waves) return QF_ERR_UNSUPPORTED;
+    if (select_stream(c.waves, c.depth, c.load_hint) == nullptr) return QF_ERR_UNSUPPORTED;
+    return lds_bytes(c, M, ksteps, N) > kMaxLds ? QF_ERR_UNSUPPORTED : QF_OK;
+  }
   if (c.kernel == QF_KERNEL_MFMA_WIDE) {
     // TILED weights, any M, the whole K range per workgroup.
     if (layout != QF_LAYOUT_TILED || c.k_waves != 1) return QF_ERR_UNSUPPORTED;
@@ -2258,7 +2441,7 @@ int validate_config(int M, int N, int K, int layout, const qf_w8a16_config& c) {
     wide_groups(M, groups, rows);
     if ((int64_t)workgroups(c, N) * groups * c.split_k > 0x7fffffff) return QF_ERR_UNSUPPORTED;
     if (select_wide(c.tiles_per_wave, rows / 16, c.waves, c.depth) == nullptr) return QF_ERR_UNSUPPORTED;
-    return lds_bytes(c, M, ksteps) > kMaxLds ? QF_ERR_UNSUPPORTED : QF_OK;
+    return lds_bytes(c, M, ksteps, N) > kMaxLds ? QF_ERR_UNSUPPORTED : QF_OK;
   }
   if (M > QF_W8A16_MAX_M) return QF_ERR_UNSUPPORTED;
   if (c.kernel == QF_KERNEL_GEMV && (M > 4 || layout != QF_LAYOUT_ROWMAJOR || c.k_waves != 1))
@@ -2268,7 +2451,7 @@ int validate_config(int M, int N, int K, int layout, const qf_w8a16_config& c) {
   if (is_mfma(c.kernel) && c.split_k > 1 && c.reduce == 0 &&
       (size_t)workgroups(c, N) * 4 > QF_W8A16_COUNTER_BYTES)
     return QF_ERR_UNSUPPORTED;  // one arrival counter per workgroup column
-  if (lds_bytes(c, M, ksteps) > kMaxLds) return QF_ERR_UNSUPPORTED;
+  if (lds_bytes(c, M, ksteps, N) > kMaxLds) return QF_ERR_UNSUPPORTED;
   if (is_mfma(c.kernel) && select_mfma(layout, c.tiles_per_wave, c.waves, c.k_waves, c.depth, c.load_hint,
                                        c.kernel == QF_KERNEL_MFMA_XRING) == nullptr)
     return QF_ERR_UNSUPPORTED;
@@ -2292,9 +2475,32 @@ constexpr TunedShape kTuned[] = {
     {5120, 17408, 8, 2},  // dense 27B-class down, split 3 (19.0 us against 19.4 us)
 };
 
-bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
+bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c, bool stream_ok = true) {
   if (M < 1 || N < 1 || K < QF_W8A16_K_ALIGN || K % QF_W8A16_K_ALIGN) return false;
   if (layout != QF_LAYOUT_ROWMAJOR && layout != QF_LAYOUT_TILED) return false;
+  if (stream_ok && layout == QF_LAYOUT_TILED && M >= 2 && M <= QF_W8A16_MAX_M &&
+      round_up16(N) / kTileN >= 4 * device_cus()) {
+    // Wide N (4 or more 16-row tiles per CU) at 2 or more tokens: the stream kernel, one workgroup per CU of
+    // 8 wavefronts with 4 steps in flight each, where the x slice and the partial tiles fit in LDS (K = 5120:
+    // up to 8 tokens).  Interleaved A/B on gate_up 34816 x 5120, weights rotated past the last-level cache:
+    // M = 2 / 3 / 4 / 5 / 6 / 7 / 8 29.6 / 29.7 / 29.7 / 29.7 / 30.8 / 30.7 / 30.7 us against 30.1 / 31.9 /
+    // 32.0 / 32.2 / 36.0 / 36.3 / 34.2 us for the shapes below; depth 3 and 5 are level with 4, depth 2, 6, 8,
+    // 12 and 16 slower (30.3, 30.3, 30.9, 32.3, 33.3 us at M = 5), 4-wavefront workgroups slower (35.5 us).
+    // At M = 1 the 4-wavefront shape below stays ahead (29.0 against 29.5 us).  Fewer tiles per CU leave the
+    // workgroups' whole-tile shares too uneven (qkv 10240 x 5120, 2.5 tiles a CU: 12.1 against 11.8 us).
+    qf_w8a16_config sc = qf_w8a16_config{};
+    sc.kernel = QF_KERNEL_MFMA_STREAM;
+    sc.split_k = 1;
+    sc.tiles_per_wave = 1;
+    sc.waves = 8;
+    sc.k_waves = 8;
+    sc.depth = 4;
+    sc.load_hint = 1;
+    if (validate_config(M, N, K, layout, sc) == QF_OK) {
+      *c = sc;
+      return true;
+    }
+  }
   if (M > QF_W8A16_MAX_M) {
     // Beyond the decode widths only TILED weights are served, by the wide-M kernel (64-row token
     // groups; measured on the dense 27B-class layer at M = 17 .. 2048 against 32-, 16- and 128-row
@@ -2359,7 +2565,7 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
     c->load_hint = 1;
     c->split_k = 1;
     c->reduce = 1;
-    while (lds_bytes(*c, M, ksteps) > kMaxLds && c->split_k < ksteps) ++c->split_k;
+    while (lds_bytes(*c, M, ksteps, N) > kMaxLds && c->split_k < ksteps) ++c->split_k;
     return validate_config(M, N, K, layout, *c) == QF_OK;
   }
   // wide N only (>= 128 workgroups of 256 rows), and only on the TILED layout, whose 1 KiB fragments
@@ -2404,7 +2610,7 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
       if (c->split_k > ksteps) c->split_k = ksteps;
       if (ksteps / c->split_k < c->k_waves) c->k_waves = 1;
       if (!wide_n && ksteps / c->split_k >= 64) c->depth = 8;  // down: 21.2 us against 21.8 at M = 2
-      while (lds_bytes(*c, M, ksteps) > kMaxLds && c->split_k < ksteps) ++c->split_k;
+      while (lds_bytes(*c, M, ksteps, N) > kMaxLds && c->split_k < ksteps) ++c->split_k;
       if (c->split_k > 1 && (size_t)workgroups(*c, N) * 4 > QF_W8A16_COUNTER_BYTES) c->reduce = 1;
       return validate_config(M, N, K, layout, *c) == QF_OK;
     }
@@ -2437,7 +2643,7 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
       }
     }
     c->reduce = 1;
-    while (lds_bytes(*c, M, ksteps) > kMaxLds && c->split_k < ksteps) ++c->split_k;
+    while (lds_bytes(*c, M, ksteps, N) > kMaxLds && c->split_k < ksteps) ++c->split_k;
     return validate_config(M, N, K, layout, *c) == QF_OK;
   }
   // Narrow M at 1..2 tokens: 4-wavefront workgroups (gate_up M = 1: 30.4 us against 35.1 us).
@@ -2446,7 +2652,7 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
   for (;;) {
     const int per_split = ksteps / c->split_k;
     c->k_waves = per_split >= 64 ? 4 : (per_split >= 16 ? 2 : 1);
-    if (lds_bytes(*c, M, ksteps) <= kMaxLds || c->split_k >= ksteps) break;
+    if (lds_bytes(*c, M, ksteps, N) <= kMaxLds || c->split_k >= ksteps) break;
     ++c->split_k;
   }
   for (const TunedShape& t : kTuned) {
@@ -2473,12 +2679,14 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c) {
 }
 
 // Validate / complete a caller configuration.
-int resolve_config(int M, int N, int K, int layout, const qf_w8a16_config* in, qf_w8a16_config* out) {
-  if (!auto_config(M, N, K, layout, out)) return QF_ERR_UNSUPPORTED;
+// stream_ok = false for the fused argmax, whose epilogue only the MFMA kernels have.
+int resolve_config(int M, int N, int K, int layout, const qf_w8a16_config* in, qf_w8a16_config* out,
+                   bool stream_ok = true) {
+  if (!auto_config(M, N, K, layout, out, stream_ok)) return QF_ERR_UNSUPPORTED;
   if (in == nullptr || in->kernel == QF_KERNEL_AUTO) return QF_OK;
   qf_w8a16_config c = *in;
-  if (c.waves == 0) c.waves = 4;
-  if (c.k_waves == 0) c.k_waves = 1;
+  if (c.waves == 0) c.waves = c.kernel == QF_KERNEL_MFMA_STREAM ? 8 : 4;
+  if (c.k_waves == 0) c.k_waves = c.kernel == QF_KERNEL_MFMA_STREAM ? c.waves : 1;
   if (c.tiles_per_wave == 0) c.tiles_per_wave = (c.kernel == QF_KERNEL_GEMV) ? 4 : 1;
   if (c.depth == 0) c.depth = 8;
   if (c.split_k == 0) c.split_k = c.kernel == QF_KERNEL_MFMA_WIDE ? 1 : out->split_k;
@@ -2540,7 +2748,7 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
   if (ldx % 8 || (layout == QF_LAYOUT_ROWMAJOR && ldw % 16)) return QF_ERR_UNSUPPORTED;
 
   qf_w8a16_config c;
-  const int rc = resolve_config(M, N, K, layout, cfg, &c);
+  const int rc = resolve_config(M, N, K, layout, cfg, &c, am == nullptr);
   if (rc != QF_OK) return rc;
   if (am != nullptr && (!is_mfma(c.kernel) || c.split_k != 1)) return QF_ERR_UNSUPPORTED;
   const size_t need = am != nullptr ? argmax_workspace_for(c, M, N) : workspace_for(c, M, N);
@@ -2584,9 +2792,11 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
   const dim3 grid = c.kernel == QF_KERNEL_MFMA_WIDE ? dim3(workgroups(c, N) * a.groups * c.split_k)
                                                     : dim3(workgroups(c, N), c.split_k);
   const dim3 block(c.waves * kWave);
-  const size_t smem = lds_bytes(c, M, a.ksteps);
+  const size_t smem = lds_bytes(c, M, a.ksteps, N);
   KernelFn fn = (c.kernel == QF_KERNEL_GEMV)
                     ? select_gemv(M, c.tiles_per_wave, c.waves, c.load_hint)
+                : (c.kernel == QF_KERNEL_MFMA_STREAM)
+                    ? select_stream(c.waves, c.depth, c.load_hint)
                 : (c.kernel == QF_KERNEL_MFMA_WIDE)
                     ? select_wide(c.tiles_per_wave, a.group_rows / 16, c.waves, c.depth)
                     : select_mfma(layout, c.tiles_per_wave, c.waves, c.k_waves, c.depth, c.load_hint,
@@ -3115,7 +3325,7 @@ int qf_w8a16_gemm_noalloc(const uint16_t* x, int64_t ldx, const int8_t* w, int64
 
 size_t qf_w8a16_argmax_workspace_bytes(int M, int N, int K, int layout, const qf_w8a16_config* cfg) {
   qf_w8a16_config c;
-  if (resolve_config(M, N, K, layout, cfg, &c) != QF_OK) return 0;
+  if (resolve_config(M, N, K, layout, cfg, &c, false) != QF_OK) return 0;
   if (!is_mfma(c.kernel) || c.split_k != 1) return 0;
   return argmax_workspace_for(c, M, N);
 }

@@ -31,6 +31,7 @@ KERNEL_MFMA_XRING = 3
 KERNEL_MFMA_WIDE = 4
 KERNEL_MFMA_W8A8 = 5
 KERNEL_MFMA_W8A8_TILE = 6
+KERNEL_MFMA_STREAM = 7
 
 MAX_M = 16
 K_ALIGN = 64

@@ -72,7 +72,41 @@ def test_pick_config_covers_every_supported_shape():
                 for layout in (0, 1):
                     c = L.pick_config(M, N, K, layout)
                     assert c is not None, (M, N, K, layout)
+                    if c.kernel == L.KERNEL_MFMA_STREAM:  # every wavefront splits K; TILED weights only
+                        assert layout == 1 and c.k_waves == c.waves == 8 and c.split_k == 1, (M, N, K, c.to_tuple())
+                        assert K // 64 >= c.waves and M >= 2, (M, N, K)
+                        continue
                     assert c.k_waves in (1, 2, 4) and c.waves % c.k_waves == 0
+
+
+def test_stream_kernel_rule_host_only():
+    """The stream kernel (one workgroup per CU) for TILED weights at M >= 2 with 4 or more 16-row tiles per CU
+    (256 CUs without a visible device) where its x slice and partial tiles fit in LDS; never row-major, M = 1,
+    narrow N, or the fused argmax (qf_w8a16_argmax_workspace_bytes resolves without it)."""
+    lib = L.load()
+    for M in range(2, 9):
+        c = L.pick_config(M, 34816, 5120, 1)
+        assert c.to_tuple() == (L.KERNEL_MFMA_STREAM, 1, 1, 8, 4, 1, 8, 0), (M, c.to_tuple())
+        assert L.workspace_bytes(M, 34816, 5120, 1, None) == 0
+        assert L.pick_config(M, 34816, 5120, 0).kernel != L.KERNEL_MFMA_STREAM
+    for M in range(9, 17):  # the x slice no longer fits beside the partial tiles
+        assert L.pick_config(M, 34816, 5120, 1).kernel != L.KERNEL_MFMA_STREAM, M
+    assert L.pick_config(1, 34816, 5120, 1).kernel != L.KERNEL_MFMA_STREAM
+    assert L.pick_config(5, 10240, 5120, 1).kernel != L.KERNEL_MFMA_STREAM          # 2.5 tiles per CU
+    assert L.pick_config(5, 16384, 5120, 1).kernel == L.KERNEL_MFMA_STREAM          # 4 tiles per CU
+    assert L.pick_config(5, 151936, 5120, 1).kernel != L.KERNEL_MFMA_STREAM         # partial tiles exceed LDS
+    assert L.pick_config(5, 5120, 17408, 1).kernel != L.KERNEL_MFMA_STREAM
+    # the fused argmax keeps an MFMA kernel: a non-zero candidate table for a shape the stream kernel takes
+    assert lib.qf_w8a16_argmax_workspace_bytes(4, 34816, 5120, 1, None) > 0
+    # explicit stream configurations: TILED only, k_waves == waves, one split, instantiated depths
+    ok = L.Config.from_seq((L.KERNEL_MFMA_STREAM, 1, 1, 8, 6, 1, 8, 0))
+    assert L.workspace_bytes(5, 34816, 5120, 1, ok) == 0
+    for bad in ((L.KERNEL_MFMA_STREAM, 2, 1, 8, 4, 1, 8, 0), (L.KERNEL_MFMA_STREAM, 1, 1, 8, 4, 1, 4, 0),
+                (L.KERNEL_MFMA_STREAM, 1, 1, 8, 7, 1, 8, 0), (L.KERNEL_MFMA_STREAM, 1, 1, 8, 4, 0, 8, 0),
+                (L.KERNEL_MFMA_STREAM, 1, 1, 4, 4, 1, 4, 0)):
+        fake = 1 << 20
+        assert _gemm(x=fake, w=fake, s=fake, y=fake, layout=1, K=5120, ldx=5120, ldw=5120, N=34816, ldy=34816,
+                     cfg=L.Config.from_seq(bad)) == L.ERR_UNSUPPORTED, bad
 
 
 def test_workspace_for_explicit_config():
