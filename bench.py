@@ -85,6 +85,15 @@ class Layer:
         return qf.w8a16_mm(self.x[name], self.w[name], self.s[name], cfg, torch.bfloat16, self.layout)
 
 
+def release_cache(torch):
+    """Return the caching allocator's free blocks to the driver.  Measured on MI355X: with large freed blocks
+    held in torch's cache (set-up temporaries, earlier weight sets), the streaming GEMMs run 4-5% slower
+    (gate_up M = 5: 31.5 against 29.8 us, whether the blocks were freed before or after the weights were
+    allocated; the same bytes kept allocated cost nothing), so every timed section starts with none."""
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
 def capture(torch, fn):
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -293,6 +302,7 @@ def main():
     R = max(1, args.layers)
     log(f"bench: allocating {R} layers ({R * sum(N * K for N, K in GEMMS.values()) / 1e9:.2f} GB of int8 weights)")
     layers = [Layer(torch, qf, dev, 1000 + i, M, layout) for i in range(R)]
+    release_cache(torch)
     bytes_per_step = sum(algo_bytes(M, N, K) for (N, K) in GEMMS.values())
 
     # Steps are captured GRAPH_STEPS at a time (step i runs layer i % R), as a decode forward pass
@@ -326,14 +336,26 @@ def main():
     log(f"bench: {args.steps} steps in {elapsed * 1e3:.1f} ms: {ms_per_step * 1e3:.2f} us/layer, {value:.0f} GB/s "
         f"({100 * value / PEAK_GBS:.1f}% of 8 TB/s)")
 
-    # per-GEMM times: a graph of 8 x R launches of one GEMM, weights rotating; HIP events on the
-    # current stream around each replay
+    # per-GEMM times: a graph of launches of one GEMM, weights rotating over the layers' copies plus extra
+    # seeded copies until they pass 768 MB (qkv's and o_proj's four layer copies alone, 210 and 168 MB, would
+    # fit the 256 MB MALL and be re-read from it); HIP events on the current stream around each replay
     per_gemm = {}
     dominant_us = None
     for name, (N, K) in GEMMS.items():
-        reps = 8
-        g, _ = capture(torch, lambda n=name: [L_.gemm(qf, torch, n) for _ in range(reps) for L_ in layers])
-        launches = reps * R
+        sets = [(L_.w[name], L_.s[name], L_.x[name]) for L_ in layers]
+        gx = torch.Generator(device=dev)
+        gx.manual_seed(5000 + N + K)
+        while len(sets) * N * K < (768 << 20):
+            w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=gx).t()
+            sets.append((qf.to_tiled(w) if layout == qf.TILED else w,
+                         (torch.randn(N, device=dev, generator=gx).abs() * 0.002 + 1e-4).float(),
+                         torch.randn(M, K, device=dev, generator=gx).to(torch.bfloat16)))
+            del w
+        release_cache(torch)
+        reps = max(1, 32 // len(sets))
+        g, _ = capture(torch, lambda: [qf.w8a16_mm(x_, w_, s_, None, torch.bfloat16, layout)
+                                       for _ in range(reps) for (w_, s_, x_) in sets])
+        launches = reps * len(sets)
         g.replay()
         torch.cuda.synchronize()
         times = []
@@ -349,13 +371,15 @@ def main():
         b = algo_bytes(M, N, K)
         cfg = qf.resolve_config(M, N, K, layout)
         per_gemm[name] = {"N": N, "K": K, "us": round(us, 2), "best_us": round(min(times), 2),
+                          "weight_sets_rotated": len(sets), "rotated_MB": round(len(sets) * N * K / 1e6, 1),
                           "GB_s": round(b / us / 1e3, 1), "weight_GB_s": round(N * K / us / 1e3, 1),
                           "pct_peak": round(100 * b / us / 1e3 / PEAK_GBS, 1), "config": list(cfg)}
         log(f"  {name:8s} N={N:6d} K={K:6d}: {us:7.2f} us  {b / us / 1e3:7.0f} GB/s  "
             f"{100 * b / us / 1e3 / PEAK_GBS:5.1f}%  cfg={tuple(cfg)}")
         if name == DOMINANT:
             dominant_us = us
-        del g
+        del g, sets
+        release_cache(torch)
 
     # The reference's single-linear case at one token: N = K = 5120, M = 1 (reported beside the step).
     single = {}
@@ -368,6 +392,7 @@ def main():
         sets1.append((qf.to_tiled(w1) if layout == qf.TILED else w1,
                       (torch.randn(N1, device=dev, generator=g1).abs() * 0.002 + 1e-4).float(),
                       torch.randn(1, K1, device=dev, generator=g1).to(torch.bfloat16)))
+    release_cache(torch)
     best1 = []
     us1 = time_graph(torch, lambda: [qf.w8a16_mm(x1, w1, s1, None, torch.bfloat16, layout)
                                      for _ in range(8) for (w1, s1, x1) in sets1], 8 * len(sets1), best=best1)
@@ -377,6 +402,7 @@ def main():
               "pct_peak": round(100 * b1 / us1 / 1e3 / PEAK_GBS, 1), "config": list(qf.resolve_config(1, N1, K1, layout))}
     log(f"  single linear M=1 N=K=5120: {us1:7.2f} us  {b1 / us1 / 1e3:7.0f} GB/s  {100 * b1 / us1 / 1e3 / PEAK_GBS:5.1f}%")
     del sets1
+    release_cache(torch)
 
     dom_bytes = algo_bytes(M, *GEMMS[DOMINANT])
     achieved = dom_bytes / dominant_us / 1e3
@@ -385,30 +411,42 @@ def main():
                 "kernel": f"{DOMINANT} M={M} N={GEMMS[DOMINANT][0]} K={GEMMS[DOMINANT][1]}",
                 "algorithmic_bytes_per_launch": dom_bytes, "mean_launch_us": round(dominant_us, 2)}
 
-    # the practical ceiling at each GEMM's size: the library's read probe over the same bytes (no math)
+    # the practical ceiling at each GEMM's size: the fastest of the library's read probes over the same bytes
+    # (no math), each probe's time kept beside it
     for name, (N, K) in GEMMS.items():
         b = algo_bytes(M, N, K)
-        gbs = read_ceiling(torch, qf, dev, b)
+        detail = {}
+        gbs = read_ceiling(torch, qf, dev, b, detail)
         per_gemm[name]["read_probe_us"] = round(b / gbs / 1e3, 2)
+        per_gemm[name]["read_probes_us"] = detail
         per_gemm[name]["pct_of_read_probe"] = round(100 * per_gemm[name]["read_probe_us"] / per_gemm[name]["us"], 1)
-        log(f"  read probe {name:8s} ({b / 1e6:6.1f} MB): {b / gbs / 1e3:7.2f} us  {gbs:6.0f} GB/s")
+        log(f"  read probe {name:8s} ({b / 1e6:6.1f} MB): {b / gbs / 1e3:7.2f} us  {gbs:6.0f} GB/s  {detail}")
         if name == DOMINANT:
             roofline["read_probe_GB_s"] = round(gbs, 1)
     b1 = algo_bytes(1, N1, K1)
-    gbs1 = read_ceiling(torch, qf, dev, b1)
+    detail1 = {}
+    gbs1 = read_ceiling(torch, qf, dev, b1, detail1)
     single["read_probe_us"] = round(b1 / gbs1 / 1e3, 2)
+    single["read_probes_us"] = detail1
+    single["pct_of_read_probe"] = round(100 * single["read_probe_us"] / single["us"], 1)
 
-    # the launch floor: the period of back-to-back graph launches of a kernel that reads 16 KiB -- what
-    # every GEMM launch pays before it moves its bytes; a GEMM of B bytes cannot take less than
-    # floor + B / 8 TB/s in this timing
+    # the launch floor: the period of back-to-back graph launches of a one-workgroup kernel that touches no
+    # memory -- what every GEMM launch pays before it moves its bytes; a GEMM of B bytes cannot take less than
+    # floor + B / 8 TB/s in this timing.  The same with a 16 KiB read adds one HBM round trip.
     floor = launch_floor(torch, qf, dev)
-    log(f"  launch floor (graph of trivial kernels): {floor:.2f} us per launch")
+    floor_read = launch_floor(torch, qf, dev, 16384)
+    log(f"  launch floor (graph of empty kernels): {floor:.2f} us per launch; with a 16 KiB read {floor_read:.2f} us")
     for name, (N, K) in list(GEMMS.items()) + [("single_linear_m1", (N1, K1))]:
         d = per_gemm[name] if name in per_gemm else single
         b = algo_bytes(1 if name == "single_linear_m1" else M, N, K)
         d["us_at_peak_with_floor"] = round(floor + b / PEAK_GBS / 1e3, 2)
         d["pct_peak_after_floor"] = round(100 * b / max(d["us"] - floor, 1e-3) / 1e3 / PEAK_GBS, 1)
 
+    del layers
+    torch.cuda.empty_cache()
+    msweep = msweep_rows(torch, qf, dev, layout)
+    lm_head = lm_head_rows(torch, qf, dev)
+    vendor = vendor_decode(torch, qf, dev)
     stack = stack64(torch, qf, dev, layout, steps=10, warmup=2)
 
     cpu = None if args.no_cpu else cpu_baseline(M)
@@ -435,6 +473,10 @@ def main():
         "per_gemm": per_gemm,
         "single_linear_m1": single,
         "launch_floor_us": round(floor, 2),
+        "launch_floor_read16k_us": round(floor_read, 2),
+        "msweep": msweep,
+        "lm_head": lm_head,
+        "vendor_decode": vendor,
         "stack64": stack,
         "roofline": roofline,
         "cpu_baseline": cpu,
@@ -442,55 +484,58 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def read_ceiling(torch, qf, dev, window: int) -> float:
-    """GB/s of the library's read probe over rotating windows of `window` bytes (at least 768 MB in all, past
-    the 256 MB MALL), timed like the GEMMs; the best of two grid sizes: the practical HBM read ceiling at
-    that size, a launch included."""
+def read_ceiling(torch, qf, dev, window: int, detail=None) -> float:
+    """GB/s of the fastest read of `window` bytes this library has: its read probes over rotating windows of
+    that size (at least 768 MB in all, past the 256 MB MALL), timed like the GEMMs.  Probes: the stream-shaped
+    probe (one workgroup per CU over a contiguous share, 8 wavefronts at depth 4 or 8, 16 at depth 4) and the
+    grid-stride probe (512 and 2048 workgroups); the best is the practical HBM read ceiling at that size, a
+    launch included.  With a dict as `detail`, each probe's µs per window is recorded in it."""
     from qwen_fastpath import _lib as L
     window = window // 4096 * 4096
     nwin = max(8, -(-(768 << 20) // window))
     buf = torch.empty(nwin * window, dtype=torch.uint8, device=dev)
     buf.fill_(1)
     lib = L.load()
+    sink = torch.empty(max(2048, int(lib.qf_device_cus())), dtype=torch.int32, device=dev)
+    probes = [("grid_stride_%d" % b, lambda i, st, b=b: lib.qf_read_probe(buf.data_ptr() + i * window, window,
+                                                                          sink.data_ptr(), b, st))
+              for b in (512, 2048)]
+    probes += [("stream_w%d_d%d" % (w, d), lambda i, st, w=w, d=d: lib.qf_read_probe_stream(
+                   buf.data_ptr() + i * window, window, sink.data_ptr(), w, d, st)) for (w, d) in ((8, 4), (8, 8), (16, 4))]
     best = 0.0
-    for blocks in (512, 2048):
-        sink = torch.empty(blocks, dtype=torch.int32, device=dev)
-
-        def fn():
+    for name, call in probes:
+        def fn(call=call):
             st = torch.cuda.current_stream().cuda_stream
             for i in range(nwin):
-                L.check(lib.qf_read_probe(buf.data_ptr() + i * window, window, sink.data_ptr(), blocks, st), "probe")
+                L.check(call(i, st), "probe")
 
-        g, _ = capture(torch, fn)
-        g.replay()
-        times = []
-        for _ in range(10):
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            e0.record()
-            g.replay()
-            e1.record()
-            e1.synchronize()
-            times.append(e0.elapsed_time(e1) * 1e3 / nwin)
-        us = sorted(times)[len(times) // 2]
+        us = time_graph(torch, fn, nwin)
+        if detail is not None:
+            detail[name] = round(us, 2)
         best = max(best, window / us / 1e3)
-        del g
     del buf
     return best
 
 
-def launch_floor(torch, qf, dev) -> float:
-    """µs per launch of a graph of 64 back-to-back launches of the library's read probe over 16 KiB (one
-    workgroup): the fixed cost of a dependent kernel launch on this device."""
+def launch_floor(torch, qf, dev, read_bytes: int = 0) -> float:
+    """µs per launch of a graph of 64 back-to-back launches of one workgroup: a kernel that touches no memory
+    (read_bytes = 0: the dispatch cost of a dependent launch on this device), or the library's read probe
+    over read_bytes (dispatch plus one HBM round trip)."""
     from qwen_fastpath import _lib as L
-    buf = torch.ones(16384, dtype=torch.uint8, device=dev)
-    sink = torch.empty(1, dtype=torch.int32, device=dev)
     lib = L.load()
+    if read_bytes:
+        buf = torch.ones(read_bytes, dtype=torch.uint8, device=dev)
+        sink = torch.empty(1, dtype=torch.int32, device=dev)
 
-    def fn():
-        st = torch.cuda.current_stream().cuda_stream
-        for _ in range(64):
-            L.check(lib.qf_read_probe(buf.data_ptr(), buf.numel(), sink.data_ptr(), 1, st), "probe")
+        def fn():
+            st = torch.cuda.current_stream().cuda_stream
+            for _ in range(64):
+                L.check(lib.qf_read_probe(buf.data_ptr(), buf.numel(), sink.data_ptr(), 1, st), "probe")
+    else:
+        def fn():
+            st = torch.cuda.current_stream().cuda_stream
+            for _ in range(64):
+                L.check(lib.qf_empty_kernel(st), "empty kernel")
 
     return time_graph(torch, fn, 64)
 
@@ -516,11 +561,11 @@ def time_graph(torch, fn, launches, reps=10, best=None):
     return sorted(times)[len(times) // 2]
 
 
-def run_msweep(torch, qf, dev, args):
-    """gate_up (N=34816, K=5120) at M = 1, 2, 3, 5, 8, 12, 16 over 4 rotating weight sets."""
-    layout = qf.TILED if args.layout == "tiled" else qf.ROWMAJOR
+def msweep_rows(torch, qf, dev, layout) -> dict:
+    """gate_up (N=34816, K=5120) at M = 1, 2, 3, 5, 8, 12, 16 over 5 rotating weight sets (891 MB, past the
+    256 MB MALL), each M a graph of 40 launches timed with HIP events: {M: µs, GB/s, % of 8 TB/s, config}."""
     N, K = GEMMS["gate_up"]
-    R = 4
+    R = 5
     g = torch.Generator(device=dev)
     g.manual_seed(7)
     sets = []
@@ -528,6 +573,8 @@ def run_msweep(torch, qf, dev, args):
         w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g).t()
         sets.append((qf.to_tiled(w) if layout == qf.TILED else w,
                      (torch.randn(N, device=dev, generator=g).abs() * 0.002 + 1e-4).float()))
+        del w
+    release_cache(torch)
     rows = {}
     for M in (1, 2, 3, 5, 8, 12, 16):
         xs = [torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16) for _ in range(R)]
@@ -538,6 +585,15 @@ def run_msweep(torch, qf, dev, args):
         rows[M] = {"us": round(us, 2), "GB_s": round(b / us / 1e3, 1), "pct_peak": round(100 * b / us / 1e3 / PEAK_GBS, 1),
                    "config": list(qf.resolve_config(M, N, K, layout))}
         log(f"  gate_up M={M:2d}: {us:7.2f} us  {b / us / 1e3:7.0f} GB/s  {100 * b / us / 1e3 / PEAK_GBS:5.1f}%")
+    del sets
+    torch.cuda.empty_cache()
+    return rows
+
+
+def run_msweep(torch, qf, dev, args):
+    """gate_up (N=34816, K=5120) at M = 1, 2, 3, 5, 8, 12, 16 (msweep_rows) as its own line."""
+    layout = qf.TILED if args.layout == "tiled" else qf.ROWMAJOR
+    rows = msweep_rows(torch, qf, dev, layout)
     worst = min(r["GB_s"] for r in rows.values())
     line = {"metric": METRIC, "value": worst, "unit": "GB/s", "n_gpus": 1, "steps": 10, "warmup": 2,
             "ms_per_step": round(rows[5]["us"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
@@ -545,6 +601,47 @@ def run_msweep(torch, qf, dev, args):
             "config": {"workload": "gate_up 34816x5120 M sweep (value = the slowest M's GB/s)", "weight_layout": args.layout},
             "per_m": rows}
     print(json.dumps(line), flush=True)
+
+
+def vendor_decode(torch, qf, dev, M: int = 5) -> dict:
+    """The platform's own GEMMs at the decode width, beside the kernel (context, as the reference times CUTLASS
+    next to its kernel, data/measurements.json:371-378): per layer GEMM, (a) F.linear on bf16 weights widened
+    ahead of time (hipBLASLt; twice the weight bytes), (b) torch._int_mm on int8 activations padded to 32 rows
+    and the row-major int8 weights (int32 out; the W8A8 arithmetic without its quantiser and epilogue).  Weights
+    rotate over sets past the MALL; µs per call from HIP events around a graph, and each route's GB/s of the
+    layer GEMM's algorithmic W8A16 bytes (what the kernel moves) for comparison."""
+    import torch.nn.functional as F
+    out = {}
+    g = torch.Generator(device=dev)
+    g.manual_seed(23)
+    for name, (N, K) in GEMMS.items():
+        row = {}
+        b = algo_bytes(M, N, K)
+        nset = max(3, -(-(768 << 20) // (2 * N * K)))
+        try:
+            ws = [(torch.randint(-127, 128, (N, K), device=dev, generator=g, dtype=torch.int8).to(torch.bfloat16)
+                   * 0.01) for _ in range(nset)]
+            x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+            us = time_graph(torch, lambda: [F.linear(x, w) for _ in range(4) for w in ws], 4 * nset)
+            row["bf16_linear_us"] = round(us, 2)
+            row["bf16_linear_pct_of_w8a16_bytes"] = round(100 * b / us / 1e3 / PEAK_GBS, 1)
+            del ws
+        except Exception as e:  # noqa: BLE001 - context figure only
+            row["bf16_linear_error"] = str(e)[:120]
+        try:
+            nset8 = max(3, -(-(768 << 20) // (N * K)))
+            ws8 = [torch.randint(-127, 128, (N, K), device=dev, generator=g, dtype=torch.int8) for _ in range(nset8)]
+            xq = torch.randint(-127, 128, (32, K), device=dev, generator=g, dtype=torch.int8)
+            us = time_graph(torch, lambda: [torch._int_mm(xq, w.t()) for _ in range(4) for w in ws8], 4 * nset8)
+            row["int8_int_mm_m32_us"] = round(us, 2)
+            row["int8_int_mm_pct_of_w8a16_bytes"] = round(100 * b / us / 1e3 / PEAK_GBS, 1)
+            del ws8
+        except Exception as e:  # noqa: BLE001 - context figure only
+            row["int8_int_mm_error"] = str(e)[:120]
+        torch.cuda.empty_cache()
+        out[name] = row
+        log(f"  vendor {name:8s} M={M}: {row}")
+    return out
 
 
 def w8a8_gate_up_gemm(torch, qf, dev, g, M, sets, name="gate_up"):
@@ -789,17 +886,22 @@ def lm_head_cpu_baseline(M: int = 1, rows: int = 16384, H: int = 5120):
                       f"bf16 rounding + pad mask + argmax, best of 3 over {cores} threads: {best * 1e3:.1f} ms"}
 
 
-def run_lm_head(torch, qf, dev, args):
-    """Int8 MTP draft head: V=151936, H=5120, at M = 1 and 4.  One step = W8A16 logits for M hidden rows
-    plus the pad-masked argmax (64 pad columns, vocab offset 0); weights rotate over 2 copies (1.56 GB)."""
+def lm_head_rows(torch, qf, dev) -> dict:
+    """Int8 MTP draft head: V=151936, H=5120, at M = 1 and 4, with the draft-head configuration's inputs: int8
+    weights uniform in [-127, 127] and per-row scales |N(0,1)| * 0.002 + 1e-4 (the head's TILED copy), bf16
+    N(0,1) hidden rows.  One step = W8A16 logits for M hidden rows plus the pad-masked argmax (64 pad columns,
+    vocab offset 0), fused into the GEMM epilogue (the default) and as logits then argmax; weights rotate over
+    2 copies (1.56 GB)."""
     V, H, num_pad = 151936, 5120, 64
     g = torch.Generator(device=dev)
     g.manual_seed(11)
     heads = []
     for i in range(2):
-        w = (torch.randn(V, H, device=dev, generator=g) * 0.02).to(torch.bfloat16)
-        heads.append(qf.make_int8_head(w, num_pad))
+        w = torch.randint(-127, 128, (V, H), dtype=torch.int8, device=dev, generator=g)
+        sc = (torch.randn(V, device=dev, generator=g).abs() * 0.002 + 1e-4).float()
+        heads.append(qf.Int8Head(qf.to_tiled(w.t()), sc, num_pad, qf.pick_config(V, H, qf.TILED), qf.TILED))
         del w
+    release_cache(torch)
     rows = {}
     for M in (1, 4):
         hs = [torch.randn(M, H, device=dev, generator=g).to(torch.bfloat16) for _ in heads]
@@ -809,23 +911,39 @@ def run_lm_head(torch, qf, dev, args):
 
         def step_fused(i):  # argmax folded into the GEMM epilogue (logits neither written nor re-read)
             return qf.int8_top_tokens(heads[i], hs[i], 0, fused=True)
+
+        def logits(i):  # the GEMM alone
+            return qf.int8_logits(heads[i], hs[i])
         reps = 8
         launches = reps * len(heads)
-        us, us2 = float("inf"), float("inf")
+        us, us2, us3 = float("inf"), float("inf"), float("inf")
         for _ in range(3):  # interleaved, the best of three each: the first graph timed after set-up runs slower
             us = min(us, time_graph(torch, lambda: [step(i) for _ in range(reps) for i in range(len(heads))], launches))
             us2 = min(us2, time_graph(torch, lambda: [step_fused(i) for _ in range(reps) for i in range(len(heads))],
                                       launches))
+            us3 = min(us3, time_graph(torch, lambda: [logits(i) for _ in range(reps) for i in range(len(heads))],
+                                      launches))
         b = algo_bytes(M, V, H) - 2 * M * V + 8 * M  # compulsory: weights, scales and x read, M ids written
+        bg = algo_bytes(M, V, H)
         best = us2  # int8_top_tokens' default: the fused epilogue
         rows[M] = {"us_per_draft_step": round(best, 2), "GB_s": round(b / best / 1e3, 1),
                    "pct_peak": round(100 * b / best / 1e3 / PEAK_GBS, 1), "algorithmic_bytes": b,
-                   "us_logits_then_argmax": round(us, 2), "us_fused_epilogue": round(us2, 2)}
-        log(f"  lm_head M={M}: logits + argmax {us:7.2f} us, argmax fused into the epilogue {us2:7.2f} us;"
-            f"  fused {b / best / 1e3:6.0f} GB/s  {100 * b / best / 1e3 / PEAK_GBS:5.1f}%")
+                   "us_logits_then_argmax": round(us, 2), "us_fused_epilogue": round(us2, 2),
+                   "us_gemm_alone": round(us3, 2), "gemm_alone_pct_peak": round(100 * bg / us3 / 1e3 / PEAK_GBS, 1)}
+        log(f"  lm_head M={M}: logits + argmax {us:7.2f} us, argmax fused into the epilogue {us2:7.2f} us, GEMM alone "
+            f"{us3:7.2f} us;  fused {b / best / 1e3:6.0f} GB/s  {100 * b / best / 1e3 / PEAK_GBS:5.1f}%")
+    del heads
+    torch.cuda.empty_cache()
+    return rows
+
+
+def run_lm_head(torch, qf, dev, args):
+    """The int8 draft head (lm_head_rows) as its own line, with its CPU baseline."""
+    rows = lm_head_rows(torch, qf, dev)
     line = {"metric": METRIC, "value": rows[1]["GB_s"], "unit": "GB/s", "n_gpus": 1, "steps": 10, "warmup": 2,
             "ms_per_step": round(rows[1]["us_per_draft_step"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": None, "dtype": "bf16", "data": "synthetic (bf16 N(0,0.02) head quantised per row to int8)",
+            "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (int8 uniform [-127, 127] weights, per-row fp32 scales |N(0,1)|*0.002+1e-4)",
             "config": {"workload": "int8 draft lm_head 151936x5120 plus the pad-masked argmax, ids out "
                                    "(value = M=1 GB/s of compulsory bytes)",
                        "weight_layout": "tiled"},
@@ -975,6 +1093,7 @@ def stack64(torch, qf, dev, layout: int, steps: int, warmup: int) -> dict:
     nl = 64
     log(f"stack64: allocating {nl} layers ({nl * sum(N * K for N, K in GEMMS.values()) / 1e9:.1f} GB)")
     layers = [StackLayer(torch, qf, dev, 5000 + i, layout) for i in range(nl)]
+    release_cache(torch)
     x0 = torch.randn(M, 5120, device=dev).to(torch.bfloat16)
 
     def step():

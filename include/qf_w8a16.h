@@ -95,9 +95,15 @@ typedef enum qf_kernel {
                                launch; reduce 3 (split_k 1): one launch of 256-channel x 128-token
                                workgroups */
   QF_KERNEL_MFMA_STREAM = 7 /* TILED layout, M <= 16: one workgroup per CU, each over a contiguous run of
-                               16-row tiles and the whole K range; its waves (8, or 16 at depth 8) all split
-                               K (k_waves == waves) with a depth-step prefetch ring (8, 12 or 16) that runs
-                               across tile boundaries; split_k 1, tiles_per_wave 1, load_hint 1 */
+                               16-row tiles and the whole K range; all its waves split K (k_waves == waves)
+                               with a depth-step prefetch ring that runs across tile boundaries; split_k 1,
+                               load_hint 1.  reduce bit 0 clear: x staged in LDS (8 waves at depth 2, 3, 4, 5,
+                               6, 8, 12 or 16; 16 waves at depth 2, 4 or 8); set: each wave's x fragments held
+                               in registers (8 waves: K = 5120 at depth 4 or 9, K = 8192 at depth 3 or 7, K =
+                               4096 at depth 3; 16 waves: K = 5120 at depth 4).  reduce bit 1: workgroup b owns
+                               tiles b, b + G, ... instead of a contiguous run.  reduce bit 2: G = ceil(tiles /
+                               tiles_per_wave) workgroups of tiles_per_wave tiles each (several may share a CU)
+                               instead of one per CU (tiles_per_wave 1) */
 } qf_kernel;
 
 /* Launch configuration.  A zero field means "choose automatically". */
@@ -318,6 +324,20 @@ int qf_stream_capture_info(void* stream, int* capturing, unsigned long long* id)
  * HBM read ceiling the GEMM is compared with; the analogue of the reference's device-copy probe
  * (bench/kernels/linear_kernels.py:87-89).  bytes % 16 == 0, buf 16-byte aligned. */
 int qf_read_probe(const void* buf, size_t bytes, uint32_t* sink, int blocks, void* stream);
+
+/* Diagnostic: read [buf, buf + bytes) once in the stream kernel's pattern: one workgroup per CU (sink holds
+ * qf_device_cus() words), workgroup b reading the contiguous b-th share of the buffer's KiB, its `waves`
+ * wavefronts interleaved at 1 KiB with `depth` KiB in flight each (waves 8 at depth 4 or 8, waves 16 at depth
+ * 4).  The fastest read of a GEMM's bytes measured on this device; the ceiling the GEMMs are compared with.
+ * bytes a positive multiple of 1024, buf 16-byte aligned. */
+int qf_read_probe_stream(const void* buf, size_t bytes, uint32_t* sink, int waves, int depth, void* stream);
+
+/* Diagnostic: launch one workgroup of a kernel that touches no memory (the dispatch cost of a launch in a
+ * graph of back-to-back launches). */
+int qf_empty_kernel(void* stream);
+
+/* Compute units of the current device (256 when no device is visible): the stream kernel's grid. */
+int qf_device_cus(void);
 
 #ifdef __cplusplus
 }

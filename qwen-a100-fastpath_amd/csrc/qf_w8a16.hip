@@ -81,6 +81,8 @@ struct GemmArgs {
   // (b, s) of tokens 16 b .. 16 b + 15 and k 64 s .. 64 s + 63 at byte (b * ksteps + s) * 1024, lane
   // (g, r) = token 16 b + r, k 64 s + 16 g .. + 15 at byte 16 (16 g + r) of the block).
   int x_tiled;
+  // Stream kernel: 1 = workgroup b owns tiles b, b + G, b + 2 G, ... (G = grid) instead of a contiguous run.
+  int tiles_strided;
 };
 
 // ---------------------------------------------------------------------------------------------
@@ -713,9 +715,11 @@ __global__ void __launch_bounds__(W * kWave) w8a16_stream_kernel(const GemmArgs 
   const int g = lane >> 4;
   const int r = lane & 15;
   const int ntiles = a.n_pad / kTileN;
-  const int t0 = (int)(((int64_t)blockIdx.x * ntiles) / gridDim.x);
-  const int t1 = (int)(((int64_t)(blockIdx.x + 1) * ntiles) / gridDim.x);
-  const int nt = t1 - t0;
+  // The workgroup's tiles: t0, t0 + tstep, ..., nt of them (a contiguous run, or every G-th tile).
+  const int tstep = a.tiles_strided ? (int)gridDim.x : 1;
+  const int t0 = a.tiles_strided ? (int)blockIdx.x : (int)(((int64_t)blockIdx.x * ntiles) / gridDim.x);
+  const int nt = a.tiles_strided ? (ntiles - (int)blockIdx.x + tstep - 1) / tstep
+                                 : (int)(((int64_t)(blockIdx.x + 1) * ntiles) / gridDim.x) - t0;
   if (nt <= 0) return;  // uniform over the workgroup: more workgroups than tiles
   const int ksteps = a.ksteps;
   const int S = (ksteps - v + W - 1) / W;  // k-steps of this wavefront in each tile, >= 1 (ksteps >= W)
@@ -727,7 +731,7 @@ __global__ void __launch_bounds__(W * kWave) w8a16_stream_kernel(const GemmArgs 
   // Past the last step the cursor stays on it (an in-bounds re-read), so every load is unconditional.
   const int8_t* pf = a.w + (((int64_t)t0 * ksteps + v) * kWave + lane) * 16;
   const int64_t step_b = (int64_t)W * kTileN * kStepK;
-  const int64_t wrap_b = (int64_t)(ksteps - (S - 1) * W) * kTileN * kStepK;
+  const int64_t wrap_b = ((int64_t)(tstep - 1) * ksteps + ksteps - (S - 1) * W) * kTileN * kStepK;
   int pi = 0, pj = 0;
   auto advance = [&]() {
     if (pi < total - 1) {
@@ -800,7 +804,91 @@ __global__ void __launch_bounds__(W * kWave) w8a16_stream_kernel(const GemmArgs 
     f32x4_t sum = part[(t * W) * kWave + lane];
 #pragma unroll
     for (int u = 1; u < W; ++u) sum += part[(t * W + u) * kWave + lane];
-    const int n = (t0 + t) * kTileN + 4 * g;
+    const int n = (t0 + t * tstep) * kTileN + 4 * g;
+    if (r < a.M && n < a.N)
+      store_out4(a.y, a.ldy, a.out_f32, a.vec_out, r, n, min(4, a.N - n), sum * load_scale4(a.scale, a.N, n));
+  }
+}
+
+// The stream kernel with each wavefront's x fragments in registers instead of a staged LDS slice
+// (QF_KERNEL_MFMA_STREAM, reduce = 1): wavefront v uses the x fragments of its k-steps v, v + W, ..., the same
+// S = K / (64 W) steps in every tile, so it loads those 2 S fragments (16 bytes per lane each) once, before
+// its first weight requests, and no barrier precedes the first step.  S is a multiple of the ring size, so
+// both the ring slot and the x register of every step are compile-time.  Sums and results are those of
+// w8a16_stream_kernel<W, DEPTH> bit for bit (the same steps in the same order, the same partial slots).
+template <int W, int S, int DEPTH>
+__global__ void __launch_bounds__(W * kWave) w8a16_stream_xreg_kernel(const GemmArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  constexpr int RING = DEPTH + 1;
+  static_assert(S % RING == 0, "a tile's steps fill whole ring turns");
+  const int lane = threadIdx.x & (kWave - 1);
+  const int v = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int g = lane >> 4;
+  const int r = lane & 15;
+  const int ntiles = a.n_pad / kTileN;
+  // The workgroup's tiles: t0, t0 + tstep, ..., nt of them (a contiguous run, or every G-th tile).
+  const int tstep = a.tiles_strided ? (int)gridDim.x : 1;
+  const int t0 = a.tiles_strided ? (int)blockIdx.x : (int)(((int64_t)blockIdx.x * ntiles) / gridDim.x);
+  const int nt = a.tiles_strided ? (ntiles - (int)blockIdx.x + tstep - 1) / tstep
+                                 : (int)(((int64_t)(blockIdx.x + 1) * ntiles) / gridDim.x) - t0;
+  if (nt <= 0) return;  // uniform over the workgroup: more workgroups than tiles
+  constexpr int ksteps = W * S;  // the host launches this kernel only for K = 64 W S
+  const int total = nt * S;
+  f32x4_t* part = reinterpret_cast<f32x4_t*>(smem);  // [nt][W][64 lanes]
+
+  // x fragments: lane (g, r) holds x[min(r, M - 1)][64 (v + j W) + 16 g .. + 15] for j < S.
+  const uint16_t* xp = a.x + (int64_t)min(r, a.M - 1) * a.ldx + (int64_t)v * kStepK + 16 * g;
+  u32x4_t xf[S][2];
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    const u32x4_t* q = reinterpret_cast<const u32x4_t*>(xp + (int64_t)j * W * kStepK);
+    xf[j][0] = q[0];
+    xf[j][1] = q[1];
+  }
+  __builtin_amdgcn_sched_barrier(0);  // the x requests go out before the weight requests
+
+  const int8_t* pf = a.w + (((int64_t)t0 * ksteps + v) * kWave + lane) * 16;
+  constexpr int64_t step_b = (int64_t)W * kTileN * kStepK;
+  const int64_t wrap_b = ((int64_t)(tstep - 1) * ksteps + ksteps - (S - 1) * W) * kTileN * kStepK;
+  int pi = 0, pj = 0;
+  auto advance = [&]() {
+    if (pi < total - 1) {  // past the last step the cursor stays on it (an in-bounds re-read)
+      ++pi;
+      if (++pj < S) {
+        pf += step_b;
+      } else {
+        pj = 0;
+        pf += wrap_b;
+      }
+    }
+  };
+  u32x4_t buf[RING];
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) {
+    buf[d] = load16<true>(pf);
+    advance();
+  }
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < nt; ++t) {
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+      buf[(j + DEPTH) % RING] = load16<true>(pf);
+      advance();
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch issue ahead of this step's math
+      bf16x8_t w0, w1;
+      dequant16(buf[j % RING], w0, w1);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, __builtin_bit_cast(bf16x8_t, xf[j][0]), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, __builtin_bit_cast(bf16x8_t, xf[j][1]), acc, 0, 0, 0);
+    }
+    part[(t * W + v) * kWave + lane] = acc;
+    acc = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+  }
+  lds_barrier();
+  for (int t = v; t < nt; t += W) {
+    f32x4_t sum = part[(t * W) * kWave + lane];
+#pragma unroll
+    for (int u = 1; u < W; ++u) sum += part[(t * W + u) * kWave + lane];
+    const int n = (t0 + t * tstep) * kTileN + 4 * g;
     if (r < a.M && n < a.N)
       store_out4(a.y, a.ldy, a.out_f32, a.vec_out, r, n, min(4, a.N - n), sum * load_scale4(a.scale, a.N, n));
   }
@@ -2213,6 +2301,56 @@ __global__ void __launch_bounds__(256) read_probe_kernel(const u32x4_t* buf, int
   if (threadIdx.x == 0) sink[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
 }
 
+// Read probe in the stream kernel's shape: one workgroup per CU, workgroup b reading the contiguous KiB
+// range [b U / G, (b + 1) U / G) of the U KiB of the buffer, its W wavefronts interleaved at 1 KiB (wavefront
+// v reads KiB v, v + W, ... of the range) with DEPTH KiB in flight each (non-temporal 16-byte loads).  No
+// math: the fastest way this device reads a GEMM's bytes in that pattern.  One xor per workgroup goes to sink.
+template <int W, int DEPTH>
+__global__ void __launch_bounds__(W * kWave) read_probe_stream_kernel(const int8_t* buf, int64_t units,
+                                                                      uint32_t* sink) {
+  __shared__ uint32_t red[W];
+  constexpr int RING = DEPTH + 1;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int v = threadIdx.x / kWave;
+  const int64_t u0 = ((int64_t)blockIdx.x * units) / gridDim.x;
+  const int64_t u1 = ((int64_t)(blockIdx.x + 1) * units) / gridDim.x;
+  const int total = (int)((u1 - u0 - v + W - 1) / W);  // KiB read by this wavefront (may be 0)
+  uint32_t acc = 0;
+  if (total > 0) {  // uniform per wavefront
+    // The GEMM's ring: the load for step i + DEPTH goes into the slot step i - 1 freed, and indices past the
+    // last step are clamped to it (an in-bounds re-read), so every load is unconditional and DEPTH stay in
+    // flight.
+    const int8_t* p = buf + (u0 + v) * 1024 + lane * 16;
+    const int64_t stride = (int64_t)W * 1024;
+    u32x4_t ring[RING];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) ring[d] = load16<true>(p + (int64_t)min(d, total - 1) * stride);
+    for (int base = 0; base < total; base += RING) {
+#pragma unroll
+      for (int d = 0; d < RING; ++d) {
+        ring[(d + DEPTH) % RING] = load16<true>(p + (int64_t)min(base + d + DEPTH, total - 1) * stride);
+        __builtin_amdgcn_sched_barrier(0);
+        if (base + d < total) {
+          const u32x4_t x = ring[d];
+          acc ^= x.x ^ x.y ^ x.z ^ x.w;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) acc ^= __shfl_xor(acc, off, kWave);
+  if (lane == 0) red[v] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t t = 0;
+    for (int i = 0; i < W; ++i) t ^= red[i];
+    sink[blockIdx.x] = t;
+  }
+}
+
+// A kernel that touches no memory: the dispatch cost of one launch in a graph of back-to-back launches.
+__global__ void __launch_bounds__(64) empty_kernel() {}
+
 // ---------------------------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------------------------
@@ -2280,6 +2418,20 @@ KernelFn select_stream(int waves, int depth, int hint) {
     if (depth == 4) return &w8a16_stream_kernel<16, 4, true>;
     if (depth == 8) return &w8a16_stream_kernel<16, 8, true>;
   }
+  return nullptr;
+}
+
+// The register-x stream kernel for K = 64 W S: 8 wavefronts with S = 10 (K = 5120) at depth 4 or 9, S = 16
+// (K = 8192) at depth 3 or 7, S = 8 (K = 4096) at depth 3; 16 wavefronts with S = 5 (K = 5120) at depth 4.
+KernelFn select_stream_xreg(int waves, int depth, int ksteps) {
+  if (waves == 8) {
+    if (ksteps == 80 && depth == 4) return &w8a16_stream_xreg_kernel<8, 10, 4>;
+    if (ksteps == 80 && depth == 9) return &w8a16_stream_xreg_kernel<8, 10, 9>;
+    if (ksteps == 128 && depth == 3) return &w8a16_stream_xreg_kernel<8, 16, 3>;
+    if (ksteps == 128 && depth == 7) return &w8a16_stream_xreg_kernel<8, 16, 7>;
+    if (ksteps == 64 && depth == 3) return &w8a16_stream_xreg_kernel<8, 8, 3>;
+  }
+  if (waves == 16 && ksteps == 80 && depth == 4) return &w8a16_stream_xreg_kernel<16, 5, 4>;
   return nullptr;
 }
 
@@ -2384,11 +2536,13 @@ inline int round_up16(int n) { return (n + 15) / 16 * 16; }
 
 // LDS bytes of one workgroup: the largest split's x slice, or, for MFMA with k_waves > 1, the
 // slice-reduction buffer if that is larger.
+int workgroups(const qf_w8a16_config& c, int N);
+
 size_t lds_bytes(const qf_w8a16_config& c, int M, int ksteps, int N) {
   const int steps = ceil_div(ksteps, c.split_k);
-  if (c.kernel == QF_KERNEL_MFMA_STREAM)  // the x slice, then a 1 KiB partial per (tile of the run, wavefront)
-    return (size_t)align16i(M * x_pitch(ksteps)) +
-           (size_t)ceil_div(round_up16(N) / kTileN, device_cus()) * c.waves * kWave * sizeof(f32x4_t);
+  if (c.kernel == QF_KERNEL_MFMA_STREAM)  // the x slice (reduce 0), then a 1 KiB partial per (tile, wavefront)
+    return ((c.reduce & 1) ? 0 : (size_t)align16i(M * x_pitch(ksteps))) +
+           (size_t)ceil_div(round_up16(N) / kTileN, workgroups(c, N)) * c.waves * kWave * sizeof(f32x4_t);
   if (c.kernel == QF_KERNEL_GEMV) return (size_t)M * steps * kStepK * 2;
   if (c.kernel == QF_KERNEL_MFMA_WIDE) {
     int groups, rows;
@@ -2404,7 +2558,8 @@ size_t lds_bytes(const qf_w8a16_config& c, int M, int ksteps, int N) {
 
 int workgroups(const qf_w8a16_config& c, int N) {
   if (c.kernel == QF_KERNEL_GEMV) return ceil_div(N, c.waves * c.tiles_per_wave);
-  if (c.kernel == QF_KERNEL_MFMA_STREAM) return device_cus();
+  if (c.kernel == QF_KERNEL_MFMA_STREAM)  // one per CU, or (reduce bit 2) runs of tiles_per_wave tiles
+    return (c.reduce & 4) ? ceil_div(round_up16(N) / kTileN, c.tiles_per_wave) : device_cus();
   const int wn = c.waves / c.k_waves;
   return ceil_div(round_up16(N) / kTileN, wn * c.tiles_per_wave);
 }
@@ -2430,8 +2585,11 @@ int validate_config(int M, int N, int K, int layout, const qf_w8a16_config& c) {
   if (c.kernel == QF_KERNEL_MFMA_STREAM) {
     // TILED weights, M <= 16, one workgroup per CU over the whole K range, every wavefront splitting K.
     if (layout != QF_LAYOUT_TILED || M > QF_W8A16_MAX_M) return QF_ERR_UNSUPPORTED;
-    if (c.split_k != 1 || c.k_waves != c.waves || c.tiles_per_wave != 1 || ksteps < c.waves) return QF_ERR_UNSUPPORTED;
-    if (select_stream(c.waves, c.depth, c.load_hint) == nullptr) return QF_ERR_UNSUPPORTED;
+    if (c.split_k != 1 || c.k_waves != c.waves || ksteps < c.waves) return QF_ERR_UNSUPPORTED;
+    if (c.reduce < 0 || c.reduce > 7 || ((c.reduce & 4) == 0 && c.tiles_per_wave != 1)) return QF_ERR_INVALID_ARG;
+    if ((c.reduce & 1) == 0 && select_stream(c.waves, c.depth, c.load_hint) == nullptr) return QF_ERR_UNSUPPORTED;
+    if ((c.reduce & 1) != 0 && (!c.load_hint || select_stream_xreg(c.waves, c.depth, ksteps) == nullptr))
+      return QF_ERR_UNSUPPORTED;
     return lds_bytes(c, M, ksteps, N) > kMaxLds ? QF_ERR_UNSUPPORTED : QF_OK;
   }
   if (c.kernel == QF_KERNEL_MFMA_WIDE) {
@@ -2488,6 +2646,9 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c, bool strea
     // 12 and 16 slower (30.3, 30.3, 30.9, 32.3, 33.3 us at M = 5), 4-wavefront workgroups slower (35.5 us).
     // At M = 1 the 4-wavefront shape below stays ahead (29.0 against 29.5 us).  Fewer tiles per CU leave the
     // workgroups' whole-tile shares too uneven (qkv 10240 x 5120, 2.5 tiles a CU: 12.1 against 11.8 us).
+    // Where the x slice does not fit (K = 5120: M >= 9), each wavefront holds its x fragments in registers
+    // (reduce 1; the same sums bit for bit): gate_up M = 12 31.8 us and M = 16 32.1 us (16 wavefronts; 32.6 with
+    // 8) against 34.9 and 35.4 us for the two-slot x ring below.
     qf_w8a16_config sc = qf_w8a16_config{};
     sc.kernel = QF_KERNEL_MFMA_STREAM;
     sc.split_k = 1;
@@ -2496,6 +2657,21 @@ bool auto_config(int M, int N, int K, int layout, qf_w8a16_config* c, bool strea
     sc.k_waves = 8;
     sc.depth = 4;
     sc.load_hint = 1;
+    if (validate_config(M, N, K, layout, sc) == QF_OK) {
+      *c = sc;
+      return true;
+    }
+    const int ks = K / kStepK;
+    sc.reduce = 1;
+    if (M >= 13) {
+      sc.waves = sc.k_waves = 16;
+    }
+    sc.depth = ks == 128 ? 3 : 4;
+    if (validate_config(M, N, K, layout, sc) == QF_OK) {
+      *c = sc;
+      return true;
+    }
+    sc.waves = sc.k_waves = 8;
     if (validate_config(M, N, K, layout, sc) == QF_OK) {
       *c = sc;
       return true;
@@ -2775,6 +2951,7 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
   a.out_f32 = out_dtype == QF_DTYPE_F32;
   a.vec_out = (ldy % 4) == 0;
   a.fused_reduce = is_mfma(c.kernel) && c.reduce == 0;
+  a.tiles_strided = c.kernel == QF_KERNEL_MFMA_STREAM && (c.reduce & 2) != 0;
   a.argmax = am != nullptr;
   a.n_valid = am != nullptr ? am->n_valid : 0;
   a.index_offset = am != nullptr ? am->index_offset : 0;
@@ -2796,7 +2973,8 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
   KernelFn fn = (c.kernel == QF_KERNEL_GEMV)
                     ? select_gemv(M, c.tiles_per_wave, c.waves, c.load_hint)
                 : (c.kernel == QF_KERNEL_MFMA_STREAM)
-                    ? select_stream(c.waves, c.depth, c.load_hint)
+                    ? ((c.reduce & 1) ? select_stream_xreg(c.waves, c.depth, a.ksteps)
+                                     : select_stream(c.waves, c.depth, c.load_hint))
                 : (c.kernel == QF_KERNEL_MFMA_WIDE)
                     ? select_wide(c.tiles_per_wave, a.group_rows / 16, c.waves, c.depth)
                     : select_mfma(layout, c.tiles_per_wave, c.waves, c.k_waves, c.depth, c.load_hint,
@@ -3513,6 +3691,26 @@ int qf_read_probe(const void* buf, size_t bytes, uint32_t* sink, int blocks, voi
                      reinterpret_cast<const u32x4_t*>(buf), (int64_t)(bytes / 16), sink);
   return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
 }
+
+int qf_read_probe_stream(const void* buf, size_t bytes, uint32_t* sink, int waves, int depth, void* stream) {
+  if (buf == nullptr || sink == nullptr || bytes % 1024 || bytes == 0 || !aligned16(buf)) return QF_ERR_INVALID_ARG;
+  using ProbeFn = void (*)(const int8_t*, int64_t, uint32_t*);
+  ProbeFn fn = nullptr;
+  if (waves == 8 && depth == 4) fn = &read_probe_stream_kernel<8, 4>;
+  if (waves == 8 && depth == 8) fn = &read_probe_stream_kernel<8, 8>;
+  if (waves == 16 && depth == 4) fn = &read_probe_stream_kernel<16, 4>;
+  if (fn == nullptr) return QF_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(fn, dim3(device_cus()), dim3(waves * kWave), 0, reinterpret_cast<hipStream_t>(stream),
+                     reinterpret_cast<const int8_t*>(buf), (int64_t)(bytes / 1024), sink);
+  return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
+}
+
+int qf_empty_kernel(void* stream) {
+  hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream));
+  return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
+}
+
+int qf_device_cus(void) { return device_cus(); }
 
 size_t qf_argmax_rows_workspace_bytes(void) { return QF_W8A16_COUNTER_BYTES + qf::kArgmaxTableBytes; }
 

@@ -68,6 +68,9 @@ EXPORTS = (
     "qf_w8a8_pick_config",
     "qf_w8a8_workspace_bytes",
     "qf_w8a8_launch_plan",
+    "qf_read_probe_stream",
+    "qf_empty_kernel",
+    "qf_device_cus",
 )
 
 
@@ -179,6 +182,12 @@ def load() -> ctypes.CDLL:
     L.qf_w8a8_launch_plan.restype = i32
     L.qf_read_probe.argtypes = [p, sz, p, i32, p]
     L.qf_read_probe.restype = i32
+    L.qf_read_probe_stream.argtypes = [p, sz, p, i32, i32, p]
+    L.qf_read_probe_stream.restype = i32
+    L.qf_empty_kernel.argtypes = [p]
+    L.qf_empty_kernel.restype = i32
+    L.qf_device_cus.argtypes = []
+    L.qf_device_cus.restype = i32
     v = L.qf_abi_version()
     if v != ABI_VERSION:
         raise ImportError(f"{LIB_PATH}: ABI version {v}, expected {ABI_VERSION}")

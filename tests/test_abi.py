@@ -73,7 +73,7 @@ def test_pick_config_covers_every_supported_shape():
                     c = L.pick_config(M, N, K, layout)
                     assert c is not None, (M, N, K, layout)
                     if c.kernel == L.KERNEL_MFMA_STREAM:  # every wavefront splits K; TILED weights only
-                        assert layout == 1 and c.k_waves == c.waves == 8 and c.split_k == 1, (M, N, K, c.to_tuple())
+                        assert layout == 1 and c.k_waves == c.waves in (8, 16) and c.split_k == 1, (M, N, K, c.to_tuple())
                         assert K // 64 >= c.waves and M >= 2, (M, N, K)
                         continue
                     assert c.k_waves in (1, 2, 4) and c.waves % c.k_waves == 0
@@ -89,8 +89,11 @@ def test_stream_kernel_rule_host_only():
         assert c.to_tuple() == (L.KERNEL_MFMA_STREAM, 1, 1, 8, 4, 1, 8, 0), (M, c.to_tuple())
         assert L.workspace_bytes(M, 34816, 5120, 1, None) == 0
         assert L.pick_config(M, 34816, 5120, 0).kernel != L.KERNEL_MFMA_STREAM
-    for M in range(9, 17):  # the x slice no longer fits beside the partial tiles
-        assert L.pick_config(M, 34816, 5120, 1).kernel != L.KERNEL_MFMA_STREAM, M
+    for M in range(9, 17):  # the x slice no longer fits beside the partial tiles: x fragments in registers
+        want = (L.KERNEL_MFMA_STREAM, 1, 1, 16 if M >= 13 else 8, 4, 1, 16 if M >= 13 else 8, 1)
+        assert L.pick_config(M, 34816, 5120, 1).to_tuple() == want, M
+    assert L.pick_config(12, 16384, 8192, 1).to_tuple() == (L.KERNEL_MFMA_STREAM, 1, 1, 8, 3, 1, 8, 1)
+    assert L.pick_config(12, 16384, 8256, 1).kernel != L.KERNEL_MFMA_STREAM  # no register-x build for this K
     assert L.pick_config(1, 34816, 5120, 1).kernel != L.KERNEL_MFMA_STREAM
     assert L.pick_config(5, 10240, 5120, 1).kernel != L.KERNEL_MFMA_STREAM          # 2.5 tiles per CU
     assert L.pick_config(5, 16384, 5120, 1).kernel == L.KERNEL_MFMA_STREAM          # 4 tiles per CU

@@ -280,3 +280,41 @@ def test_load_time_tiled_repack(oracle, monkeypatch):
     torch.cuda.synchronize()
     assert torch.equal(y20.view(torch.int16), ref.view(torch.int16))
     assert not qf.repack_layer_weight(_Layer(torch.zeros(4, 4, dtype=torch.float32, device=DEV), None))
+
+
+def test_draft_head_baseline_inputs_full_size(oracle):
+    """The draft-head configuration's own inputs at full size: V = 151936, H = 5120, int8 weights uniform in
+    [-127, 127] and per-row fp32 scales |N(0,1)| * 0.002 + 1e-4 (the oracle's generator, seed 0), bf16 N(0,1)
+    hidden rows, M = 1 and 4, the head in its TILED copy.  The logits pass oracle.check_w8a16 against the exact
+    product; the ids of the fused epilogue (qf_w8a16_gemm_argmax) and of logits-then-argmax equal the argmax of
+    the kernel's own logits, and equal the exact product's argmax on every row whose top-2 exact logits are 2
+    bf16 ulp or more apart (a row under that gap is reported, not compared)."""
+    V, H, num_pad, start = 151936, 5120, 64, 0
+    for M in (1, 4):
+        inp = oracle.gen_inputs(M, V, H, seed=0)
+        w_dev = torch.from_numpy(inp.w).to(DEV)
+        head = qf.Int8Head(qf.to_tiled(w_dev.t()), torch.from_numpy(inp.s).to(DEV), num_pad,
+                           qf.pick_config(V, H, qf.TILED), qf.TILED)
+        del w_dev
+        hb = to_dev_bf16(inp.x, DEV)
+        print(f"draft head baseline inputs M={M}", flush=True)
+        logits = qf.int8_logits(head, hb)
+        fused = qf.int8_top_tokens(head, hb, start, fused=True)
+        two = qf.int8_top_tokens(head, hb, start, fused=False)
+        torch.cuda.synchronize()
+        lb = bf16_bits(logits)
+        ex_bits, ex64 = oracle.w8a16_exact(inp.x, inp.w, inp.s)
+        rep = oracle.check_w8a16(lb, inp.x, inp.w, inp.s, exact=(ex_bits, ex64))
+        print(f"  logits: {rep}", flush=True)
+        assert rep.ok, rep
+        own = oracle.argmax_rows(lb, V - num_pad, start)
+        assert np.array_equal(fused.cpu().numpy(), own) and np.array_equal(two.cpu().numpy(), own), M
+        ex_ids = oracle.argmax_rows(ex_bits, V - num_pad, start)
+        for m in range(M):
+            row = ex64[m, : V - num_pad]
+            top2 = np.sort(row)[-2:]
+            gap_ulp = (top2[1] - top2[0]) / oracle.bf16_ulp(np.array([top2[1]]))[0]
+            print(f"  row {m}: exact argmax {ex_ids[m]}, kernel {own[m]}, top-2 gap {gap_ulp:.2f} ulp", flush=True)
+            if gap_ulp >= 2:
+                assert own[m] == ex_ids[m], (M, m, gap_ulp)
+        del head

@@ -96,3 +96,33 @@ def test_stream_auto_gate_up_graph_replay(oracle):
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.int16), eager.view(torch.int16)), rep
     assert oracle.check_w8a16(bf16_bits(eager), inp.x, inp.w, inp.s).ok
+
+
+@pytest.mark.parametrize("M,N,K", [(5, 1000, 5120), (16, 4100, 5120), (1, 16, 5120), (9, 34816, 5120),
+                                   (12, 3000, 8192), (3, 300, 4096), (16, 24592, 4096)])
+@pytest.mark.parametrize("waves,depth", [(8, 4), (8, 9), (8, 3), (8, 7), (16, 4)])
+def test_stream_xreg_against_oracle(oracle, M, N, K, waves, depth):
+    """x fragments held in registers (reduce 1, K = 64 W S for the instantiated S): passes the oracle at every M
+    up to 16, and equals the LDS-staged stream kernel at the same wavefront count bit for bit wherever the
+    latter's x slice fits in LDS (the same steps summed in the same order)."""
+    xreg = qf.W8A16Config(STREAM, 1, 1, waves, depth, 1, waves, 1)
+    inp = oracle.gen_inputs(M, N, K, seed=M + 7 * N + K)
+    x, w, s = dev_inputs(inp, DEV)
+    img = qf.to_tiled(w)
+    print(f"stream xreg M={M} N={N} K={K} cfg={tuple(xreg)}", flush=True)
+    try:
+        y = run(x, img, s, xreg)
+    except L.QFError as e:  # refused before any launch: no instantiation for this (K, waves, depth)
+        assert e.status == L.ERR_UNSUPPORTED, e
+        pytest.skip("not instantiated for this K")
+    torch.cuda.synchronize()
+    rep = oracle.check_w8a16(bf16_bits(y), inp.x, inp.w, inp.s)
+    assert rep.ok, (M, N, K, waves, depth, rep)
+    for lds_depth in ((2, 4, 8) if waves == 16 else (4,)):
+        lds = qf.W8A16Config(STREAM, 1, 1, waves, lds_depth, 1, waves, 0)
+        try:
+            y_lds = run(x, img, s, lds)
+        except L.QFError:
+            continue  # the x slice does not fit beside the partial tiles
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), y_lds.view(torch.int16)), (M, N, K, waves, lds_depth)
