@@ -191,7 +191,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", choices=["layer", "stack64", "msweep", "lm_head", "prefill", "spec_attn", "tp8"],
                     default="layer")
-    ap.add_argument("--layers", type=int, default=4, help="distinct layers rotated through (layer workload)")
+    ap.add_argument("--layers", type=int, default=20,
+                    help="distinct layers allocated at start and rotated through (layer workload; 20 x 363 MB)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--profile-gemm", choices=list(GEMMS) + ["single"], default=None,
                     help="only that GEMM at M=5 (single: the 5120x5120 linear at M=1), --iters launches, weights "
@@ -336,23 +337,14 @@ def main():
     log(f"bench: {args.steps} steps in {elapsed * 1e3:.1f} ms: {ms_per_step * 1e3:.2f} us/layer, {value:.0f} GB/s "
         f"({100 * value / PEAK_GBS:.1f}% of 8 TB/s)")
 
-    # per-GEMM times: a graph of launches of one GEMM, weights rotating over the layers' copies plus extra
-    # seeded copies until they pass 768 MB (qkv's and o_proj's four layer copies alone, 210 and 168 MB, would
-    # fit the 256 MB MALL and be re-read from it); HIP events on the current stream around each replay
+    # per-GEMM times: a graph of launches of one GEMM, its weights rotating over every layer's copy (all
+    # allocated at start, as a model's weights are; 20 layers put even o_proj's copies past 768 MB, three times
+    # the 256 MB MALL); HIP events on the current stream around each replay
     per_gemm = {}
     dominant_us = None
     for name, (N, K) in GEMMS.items():
         sets = [(L_.w[name], L_.s[name], L_.x[name]) for L_ in layers]
-        gx = torch.Generator(device=dev)
-        gx.manual_seed(5000 + N + K)
-        while len(sets) * N * K < (768 << 20):
-            w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=gx).t()
-            sets.append((qf.to_tiled(w) if layout == qf.TILED else w,
-                         (torch.randn(N, device=dev, generator=gx).abs() * 0.002 + 1e-4).float(),
-                         torch.randn(M, K, device=dev, generator=gx).to(torch.bfloat16)))
-            del w
-        release_cache(torch)
-        reps = max(1, 32 // len(sets))
+        reps = max(1, 40 // len(sets))
         g, _ = capture(torch, lambda: [qf.w8a16_mm(x_, w_, s_, None, torch.bfloat16, layout)
                                        for _ in range(reps) for (w_, s_, x_) in sets])
         launches = reps * len(sets)
@@ -379,7 +371,6 @@ def main():
         if name == DOMINANT:
             dominant_us = us
         del g, sets
-        release_cache(torch)
 
     # The reference's single-linear case at one token: N = K = 5120, M = 1 (reported beside the step).
     single = {}
@@ -442,9 +433,9 @@ def main():
         d["us_at_peak_with_floor"] = round(floor + b / PEAK_GBS / 1e3, 2)
         d["pct_peak_after_floor"] = round(100 * b / max(d["us"] - floor, 1e-3) / 1e3 / PEAK_GBS, 1)
 
+    msweep = msweep_rows(torch, qf, dev, layout, layers)
     del layers
-    torch.cuda.empty_cache()
-    msweep = msweep_rows(torch, qf, dev, layout)
+    release_cache(torch)
     lm_head = lm_head_rows(torch, qf, dev)
     vendor = vendor_decode(torch, qf, dev)
     stack = stack64(torch, qf, dev, layout, steps=10, warmup=2)
@@ -467,7 +458,7 @@ def main():
         "config": {"workload": "dense GQA 27B-class layer GEMMs at M=5: qkv 10240x5120, o_proj 5120x8192, "
                                "gate_up 34816x5120, down 5120x17408 (N x K int8)",
                    "M": M, "layers_rotated": R, "bytes_per_step": bytes_per_step, "weight_layout": args.layout,
-                   "timing": f"hipGraphs of {GRAPH_STEPS} steps replayed; step i runs layer i % {R}"},
+                   "timing": f"hipGraphs of {gsteps} steps replayed; step i runs layer i % {R}"},
         "us_per_layer": round(ms_per_step * 1e3, 2),
         "pct_of_peak": round(100 * value / PEAK_GBS, 2),
         "per_gemm": per_gemm,
@@ -561,24 +552,28 @@ def time_graph(torch, fn, launches, reps=10, best=None):
     return sorted(times)[len(times) // 2]
 
 
-def msweep_rows(torch, qf, dev, layout) -> dict:
-    """gate_up (N=34816, K=5120) at M = 1, 2, 3, 5, 8, 12, 16 over 5 rotating weight sets (891 MB, past the
-    256 MB MALL), each M a graph of 40 launches timed with HIP events: {M: µs, GB/s, % of 8 TB/s, config}."""
+def msweep_rows(torch, qf, dev, layout, layers=None) -> dict:
+    """gate_up (N=34816, K=5120) at M = 1, 2, 3, 5, 8, 12, 16 over rotating weight sets past the 256 MB MALL (the
+    given layers' gate_up weights, else 5 sets of its own, 891 MB), each M a graph of 40 launches timed with HIP
+    events: {M: µs, GB/s, % of 8 TB/s, config}."""
     N, K = GEMMS["gate_up"]
-    R = 5
     g = torch.Generator(device=dev)
     g.manual_seed(7)
-    sets = []
-    for i in range(R):
-        w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g).t()
-        sets.append((qf.to_tiled(w) if layout == qf.TILED else w,
-                     (torch.randn(N, device=dev, generator=g).abs() * 0.002 + 1e-4).float()))
-        del w
-    release_cache(torch)
+    if layers is not None:
+        sets = [(L_.w["gate_up"], L_.s["gate_up"]) for L_ in layers[:8]]
+    else:
+        sets = []
+        for i in range(5):
+            w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g).t()
+            sets.append((qf.to_tiled(w) if layout == qf.TILED else w,
+                         (torch.randn(N, device=dev, generator=g).abs() * 0.002 + 1e-4).float()))
+            del w
+        release_cache(torch)
+    R = len(sets)
     rows = {}
     for M in (1, 2, 3, 5, 8, 12, 16):
         xs = [torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16) for _ in range(R)]
-        reps = 8
+        reps = max(1, 40 // R)
         us = time_graph(torch, lambda: [qf.w8a16_mm(xs[i], w, s, None, torch.bfloat16, layout)
                                         for _ in range(reps) for i, (w, s) in enumerate(sets)], reps * R)
         b = algo_bytes(M, N, K)

@@ -126,3 +126,30 @@ def test_stream_xreg_against_oracle(oracle, M, N, K, waves, depth):
             continue  # the x slice does not fit beside the partial tiles
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.int16), y_lds.view(torch.int16)), (M, N, K, waves, lds_depth)
+
+
+@pytest.mark.parametrize("M,N,K", [(5, 4100, 5120), (3, 1000, 2048), (9, 20000, 5120), (2, 16, 512)])
+def test_stream_grid_variants_bitwise(M, N, K):
+    """Which workgroup sums a tile does not change how it is summed: the strided assignment (reduce bit 1) and
+    runs of a fixed tile count (reduce bit 2, tiles_per_wave 1..3: several workgroups a CU) give the bits of the
+    default grid (one contiguous run per CU), with x staged in LDS or held in registers."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(M + N + K)
+    x = torch.randn(M, K, device=DEV, generator=g).to(torch.bfloat16)
+    img = torch.randint(-127, 128, (qf.tiled_numel(N, K),), dtype=torch.int8, device=DEV, generator=g)
+    s = (torch.rand(N, device=DEV, generator=g) * 0.002 + 1e-4).float()
+    for xreg in (0, 1):
+        base = None
+        for bits in (0, 2, 4, 6):
+            for tpw in ((1, 2, 3) if bits & 4 else (1,)):
+                c = qf.W8A16Config(STREAM, 1, tpw, 8, 4, 1, 8, bits | xreg)
+                print(f"stream grid M={M} N={N} K={K} cfg={tuple(c)}", flush=True)
+                try:
+                    y = run(x, img, s, c)
+                except L.QFError as e:
+                    assert e.status == L.ERR_UNSUPPORTED, e
+                    continue  # no register-x build for this K, or LDS too small
+                torch.cuda.synchronize()
+                if base is None:
+                    base = y
+                assert torch.equal(y.view(torch.int16), base.view(torch.int16)), (M, N, K, tuple(c))
