@@ -223,12 +223,26 @@ int qf_scale_cast_bf16(const float* acc, int64_t lda, const float* scale, int M,
 
 /* y[m, :] = bf16_rne(x[m, :] * (1 / sqrt(mean_k(x[m, k]^2) + eps))) for m < M: each row of a bf16 [M, N] matrix
  * (row stride ldx) scaled to unit RMS, into y (row stride ldy; y may be x).  The sum of squares is formed in a
- * fixed order, so results are reproducible; against torch's fp32 rms_norm of the same rows they differ by at
- * most one bf16 ulp.  N % 8 == 0, N <= 8192, x and y 16-byte aligned, ldx % 8 == 0 and ldy % 8 == 0, else
- * QF_ERR_UNSUPPORTED.  No reference counterpart: the re-normalisation between the layers of the 64-layer
- * decode-step benchmark (each layer's output to unit RMS as the next layer's input), one launch per layer. */
+ * fixed order (the row as N / 8 pieces of 8 values; lane t of a wavefront sums pieces t, t + 64, ... with fused
+ * multiply-adds, then a butterfly over the 64 lanes), the same order qf_w8a16_gemm_rmsnorm uses, so results are
+ * reproducible; against torch's fp32 rms_norm of the same rows they differ by at most one bf16 ulp.  N % 8 == 0,
+ * x and y 16-byte aligned, ldx % 8 == 0 and ldy % 8 == 0, else QF_ERR_UNSUPPORTED.  No reference
+ * counterpart: the re-normalisation between the layers of the 64-layer decode-step benchmark (each layer's
+ * output to unit RMS as the next layer's input). */
 int qf_rms_norm_rows_bf16(const uint16_t* x, int64_t ldx, int M, int N, float eps, uint16_t* y, int64_t ldy,
                           void* stream);
+
+/* qf_w8a16_gemm of the rows of x scaled to unit RMS: y = qf_w8a16_gemm(qf_rms_norm_rows_bf16(x, eps)), bit for bit,
+ * in one launch.  Each workgroup stages the whole rows of x (K % 8 == 0) and normalises them in LDS in the same
+ * order as qf_rms_norm_rows_bf16 before its first multiply, so the normalisation costs no launch of its own.
+ * Served where the configuration (automatic, or cfg) stages whole rows without a K split on TILED weights: the
+ * MFMA kernel with one tile a wavefront at depth 4 and (waves / k_waves, k_waves) = (4, 2), (2, 4), (1, 4) or
+ * (8, 1), or the x-in-LDS stream kernel with 8 waves at depth 4; otherwise QF_ERR_UNSUPPORTED (the caller then
+ * makes the two calls).  No reference counterpart: the layer-to-layer glue of the 64-layer decode step (the
+ * normalised layer output as the next layer's qkv input). */
+int qf_w8a16_gemm_rmsnorm(const uint16_t* x, int64_t ldx, float eps, const int8_t* w, int64_t ldw, int layout,
+                          const float* scale, void* y, int64_t ldy, int out_dtype, int M, int N, int K,
+                          const qf_w8a16_config* cfg, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- W8A8 path for M > 16: the reference's fallback arithmetic (dynamic per-token int8 activations, int8
  * weights, exact integer sums, fp32 scales), plugin/qwen_fastpath/patches.py:99-100, on MI355X's int8

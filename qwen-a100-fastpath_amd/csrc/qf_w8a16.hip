@@ -83,6 +83,8 @@ struct GemmArgs {
   int x_tiled;
   // Stream kernel: 1 = workgroup b owns tiles b, b + G, b + 2 G, ... (G = grid) instead of a contiguous run.
   int tiles_strided;
+  // Kernels instantiated with NORM: the staged x rows are first scaled to unit RMS (qf_w8a16_gemm_rmsnorm).
+  float norm_eps;
 };
 
 // ---------------------------------------------------------------------------------------------
@@ -204,6 +206,65 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Row normalisation to unit RMS, in one canonical order shared by qf_rms_norm_rows_bf16 and the GEMMs that
+// normalise their staged x (qf_w8a16_gemm_rmsnorm), so that both give the same bits.  A row of N bf16 values is
+// read as N / 8 pieces of 16 bytes.  Lane t of one wavefront sums the squares of pieces t, t + 64, t + 128, ...
+// in that order (each piece's 8 values in order, one fused multiply-add each); the 64 lane sums then fold by a
+// butterfly of xor shuffles (32, 16, ..., 1), after which every lane holds the same total.
+template <typename Piece>
+__device__ __forceinline__ float row_sumsq(int npieces, int lane, Piece piece) {
+  float ss = 0.f;
+  for (int j = lane; j < npieces; j += kWave) {
+    const u32x4_t v = piece(j);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = __uint_as_float(v[e] << 16), hi = __uint_as_float(v[e] & 0xffff0000u);
+      ss = __builtin_fmaf(lo, lo, ss);
+      ss = __builtin_fmaf(hi, hi, ss);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+  return ss;
+}
+
+// 1 / sqrt(mean of squares + eps) (IEEE division; the same instructions wherever it is used).
+__device__ __forceinline__ float rms_inv(float total, int n, float eps) {
+  return 1.0f / __builtin_sqrtf(total / (float)n + eps);
+}
+
+// One 16-byte piece of 8 bf16 values scaled by inv, each product rounded to bf16 (nearest even).
+__device__ __forceinline__ u32x4_t scale_piece(const u32x4_t v, float inv) {
+  u32x4_t o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    o[e] = pack_bf16_rne(__uint_as_float(v[e] << 16) * inv, __uint_as_float(v[e] & 0xffff0000u) * inv);
+  return o;
+}
+
+// Normalise the M staged rows of x in LDS (row m at byte m * pitch, K values) in place: wavefront w computes the
+// rows w, w + WAVES, ... in the canonical order, then every thread rescales its share of the pieces.  Called by
+// the whole workgroup after the staging barrier; LDS-only barriers keep the weight prefetch in flight.
+template <int WAVES>
+__device__ __forceinline__ void normalise_staged_rows(uint8_t* smem, int pitch, int M, int K, float eps,
+                                                      float* inv_lds) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int npieces = K / 8;
+  for (int m = wave; m < M; m += WAVES) {
+    const uint8_t* row = smem + m * pitch;
+    const float total = row_sumsq(npieces, lane, [&](int j) { return *reinterpret_cast<const u32x4_t*>(row + j * 16); });
+    if (lane == 0) inv_lds[m] = rms_inv(total, K, eps);
+  }
+  lds_barrier();
+  for (int q = threadIdx.x; q < M * npieces; q += WAVES * kWave) {
+    const int m = q / npieces;
+    u32x4_t* pc = reinterpret_cast<u32x4_t*>(smem + m * pitch + (q - m * npieces) * 16);
+    *pc = scale_piece(*pc, inv_lds[m]);
+  }
+  lds_barrier();
 }
 
 // LDS row pitch (bytes) of a staged x slice of `steps` k-steps: the row bytes plus 32, so the rows
@@ -415,12 +476,13 @@ struct MfmaMinWaves {
   static constexpr int value = (NT == 1 && DEPTH == 4) ? 6 : (WAVES >= 8 ? 2 : 1);
 };
 
-template <int LAYOUT, int NT, int WN, int WK, int DEPTH, bool NTH, bool XRING>
+template <int LAYOUT, int NT, int WN, int WK, int DEPTH, bool NTH, bool XRING, bool NORM = false>
 __global__ void __launch_bounds__(WN * WK * kWave)
     __attribute__((amdgpu_waves_per_eu(MfmaMinWaves<NT, DEPTH, WN * WK>::value, 8)))
     w8a16_mfma_kernel(const GemmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ int last_arrival;
+  __shared__ float norm_inv[NORM ? QF_W8A16_MAX_M : 1];
   constexpr int WAVES = WN * WK;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // uniform: scalar registers
@@ -519,6 +581,7 @@ __global__ void __launch_bounds__(WN * WK * kWave)
       prologue();
     }
     lds_barrier();  // the weight requests issued above stay in flight across it
+    if constexpr (NORM) normalise_staged_rows<WAVES>(smem, pitch, a.M, a.K, a.norm_eps, norm_inv);
     const uint8_t* xs = smem + xr * pitch + (k_lo * kStepK + 16 * g) * 2;
     constexpr int xs_stride = kStepK * 2 * WK;
     for (int base = 0; base < nsteps; base += RING) {
@@ -706,9 +769,10 @@ __global__ void __launch_bounds__(WN * WK * kWave)
 // ---------------------------------------------------------------------------------------------
 __host__ __device__ __forceinline__ int align16i(int n) { return (n + 15) & ~15; }
 
-template <int W, int DEPTH, bool NTH>
+template <int W, int DEPTH, bool NTH, bool NORM = false>
 __global__ void __launch_bounds__(W * kWave) w8a16_stream_kernel(const GemmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ float norm_inv[NORM ? QF_W8A16_MAX_M : 1];
   constexpr int RING = DEPTH + 1;
   const int lane = threadIdx.x & (kWave - 1);
   const int v = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -765,6 +829,7 @@ __global__ void __launch_bounds__(W * kWave) w8a16_stream_kernel(const GemmArgs 
     prologue();
   }
   lds_barrier();  // the weight requests issued above stay in flight across it
+  if constexpr (NORM) normalise_staged_rows<W>(smem, pitch, a.M, a.K, a.norm_eps, norm_inv);
 
   // Lane (g, r) reads x[min(r, M - 1)][k + 16 g .. + 15] of each step (token rows r >= M are never stored).
   const uint8_t* xrow = smem + min(r, a.M - 1) * pitch + 32 * g;
@@ -2229,49 +2294,34 @@ __global__ void __launch_bounds__(kArgmaxSplitThreads) argmax_rows_split_kernel(
 // eps))).  One workgroup per row; each thread keeps its 16-byte pieces in registers between the two
 // passes.  The sum of squares is formed in a fixed order (per thread over its pieces, a fixed butterfly
 // per wavefront, then the wavefronts in order), so results are reproducible.
-constexpr int kNormThreads = 256;
-constexpr int kNormPieces = 4;  // 16-byte pieces per thread: rows of up to 8192 elements
+constexpr int kNormPieces = 16;  // 16-byte pieces per lane held in registers: 64 x 16 x 8 = 8192 values
 
-__global__ void __launch_bounds__(kNormThreads) rms_norm_rows_kernel(const uint16_t* x, int64_t ldx, int N, float eps,
-                                                                    uint16_t* y, int64_t ldy) {
-  __shared__ float part[kNormThreads / kWave];
+// One wavefront per row: the row's first pieces are loaded into registers (lane t: pieces t, t + 64, ..., up to
+// kNormPieces of them; longer rows read the rest from memory in both passes), summed in the canonical order of
+// row_sumsq, and written back scaled (y may be x: each piece is read and written by its own lane only).
+__global__ void __launch_bounds__(kWave) rms_norm_rows_kernel(const uint16_t* x, int64_t ldx, int N, float eps,
+                                                              uint16_t* y, int64_t ldy) {
   const uint16_t* xr = x + (int64_t)blockIdx.x * ldx;
   uint16_t* yr = y + (int64_t)blockIdx.x * ldy;
+  const int lane = threadIdx.x;
   const int npieces = N / 8;
   u32x4_t v[kNormPieces];
-  float ss = 0.f;
 #pragma unroll
   for (int p = 0; p < kNormPieces; ++p) {
-    const int idx = p * kNormThreads + (int)threadIdx.x;
-    if (idx < npieces) {
-      v[p] = *reinterpret_cast<const u32x4_t*>(xr + idx * 8);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float lo = __uint_as_float(v[p][e] << 16), hi = __uint_as_float(v[p][e] & 0xffff0000u);
-        ss += lo * lo;
-        ss += hi * hi;
-      }
-    }
+    const int j = p * kWave + lane;
+    v[p] = j < npieces ? *reinterpret_cast<const u32x4_t*>(xr + j * 8) : (u32x4_t){0, 0, 0, 0};
   }
+  auto piece = [&](int j) {
+    const int p = j / kWave;
+    if (p >= kNormPieces) return *reinterpret_cast<const u32x4_t*>(xr + (int64_t)j * 8);
+    u32x4_t r = v[0];
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, kWave);
-  if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = ss;
-  __syncthreads();
-  float total = part[0];
-#pragma unroll
-  for (int w = 1; w < kNormThreads / kWave; ++w) total += part[w];
-  const float inv = 1.0f / __builtin_sqrtf(total / (float)N + eps);
-#pragma unroll
-  for (int p = 0; p < kNormPieces; ++p) {
-    const int idx = p * kNormThreads + (int)threadIdx.x;
-    if (idx < npieces) {
-      u32x4_t o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        o[e] = pack_bf16_rne(__uint_as_float(v[p][e] << 16) * inv, __uint_as_float(v[p][e] & 0xffff0000u) * inv);
-      *reinterpret_cast<u32x4_t*>(yr + idx * 8) = o;
-    }
-  }
+    for (int q = 1; q < kNormPieces; ++q)
+      if (p == q) r = v[q];
+    return r;
+  };
+  const float inv = rms_inv(row_sumsq(npieces, lane, piece), N, eps);
+  for (int j = lane; j < npieces; j += kWave) *reinterpret_cast<u32x4_t*>(yr + (int64_t)j * 8) = scale_piece(piece(j), inv);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -2396,6 +2446,23 @@ KernelFn select_mfma(int layout, int nt, int waves, int k_waves, int depth, int 
 }
 
 inline bool is_mfma(int kernel) { return kernel == QF_KERNEL_MFMA || kernel == QF_KERNEL_MFMA_XRING; }
+
+// Instantiations that normalise their staged x rows first (qf_w8a16_gemm_rmsnorm): the MFMA kernel on TILED
+// weights, one tile a wavefront, depth 4, non-temporal loads, whole-slice x, as (WN, WK) = (4, 2), (2, 4),
+// (1, 4) or (8, 1); the LDS-staged stream kernel with 8 wavefronts at depth 4.
+KernelFn select_norm(const qf_w8a16_config& c, int layout) {
+  if (layout != QF_LAYOUT_TILED || c.depth != 4 || !c.load_hint || c.tiles_per_wave != 1) return nullptr;
+  if (c.kernel == QF_KERNEL_MFMA) {
+    const int wn = c.waves / c.k_waves, wk = c.k_waves;
+    if (wn == 4 && wk == 2) return &w8a16_mfma_kernel<QF_LAYOUT_TILED, 1, 4, 2, 4, true, false, true>;
+    if (wn == 2 && wk == 4) return &w8a16_mfma_kernel<QF_LAYOUT_TILED, 1, 2, 4, 4, true, false, true>;
+    if (wn == 1 && wk == 4) return &w8a16_mfma_kernel<QF_LAYOUT_TILED, 1, 1, 4, 4, true, false, true>;
+    if (wn == 8 && wk == 1) return &w8a16_mfma_kernel<QF_LAYOUT_TILED, 1, 8, 1, 4, true, false, true>;
+  }
+  if (c.kernel == QF_KERNEL_MFMA_STREAM && c.reduce == 0 && c.waves == 8)
+    return &w8a16_stream_kernel<8, 4, true, true>;
+  return nullptr;
+}
 
 // Stream-kernel instantiations (TILED weights, non-temporal loads): 8 wavefronts at depth 2, 3, 4, 5, 6, 8, 12
 // or 16; 16 wavefronts at depth 2, 4 or 8.  Both keep the accumulator in VGPRs.  (A 4-wavefront build, one
@@ -2911,9 +2978,10 @@ size_t argmax_workspace_for(const qf_w8a16_config& c, int M, int N) {
   return QF_W8A16_COUNTER_BYTES + argmax_stride(c, N) * (size_t)M * sizeof(uint64_t);
 }
 
+// norm_eps != nullptr: the x rows are scaled to unit RMS first (qf_w8a16_gemm_rmsnorm), by a NORM instantiation.
 int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int layout, const float* scale, void* y,
              int64_t ldy, int out_dtype, int M, int N, int K, const qf_w8a16_config* cfg, void* workspace,
-             size_t workspace_bytes, void* stream, const ArgmaxRequest* am) {
+             size_t workspace_bytes, void* stream, const ArgmaxRequest* am, const float* norm_eps = nullptr) {
   if (x == nullptr || w == nullptr || scale == nullptr) return QF_ERR_INVALID_ARG;
   if (M < 1 || N < 1 || K < 1) return QF_ERR_INVALID_ARG;
   if (layout != QF_LAYOUT_ROWMAJOR && layout != QF_LAYOUT_TILED) return QF_ERR_INVALID_ARG;
@@ -2927,6 +2995,8 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
   const int rc = resolve_config(M, N, K, layout, cfg, &c, am == nullptr);
   if (rc != QF_OK) return rc;
   if (am != nullptr && (!is_mfma(c.kernel) || c.split_k != 1)) return QF_ERR_UNSUPPORTED;
+  // The normalising GEMM needs whole rows staged: no K split, and an instantiation that normalises.
+  if (norm_eps != nullptr && (c.split_k != 1 || select_norm(c, layout) == nullptr)) return QF_ERR_UNSUPPORTED;
   const size_t need = am != nullptr ? argmax_workspace_for(c, M, N) : workspace_for(c, M, N);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))) return QF_ERR_WORKSPACE;
 
@@ -2952,6 +3022,7 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
   a.vec_out = (ldy % 4) == 0;
   a.fused_reduce = is_mfma(c.kernel) && c.reduce == 0;
   a.tiles_strided = c.kernel == QF_KERNEL_MFMA_STREAM && (c.reduce & 2) != 0;
+  a.norm_eps = norm_eps != nullptr ? *norm_eps : 0.f;
   a.argmax = am != nullptr;
   a.n_valid = am != nullptr ? am->n_valid : 0;
   a.index_offset = am != nullptr ? am->index_offset : 0;
@@ -2979,6 +3050,7 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
                     ? select_wide(c.tiles_per_wave, a.group_rows / 16, c.waves, c.depth)
                     : select_mfma(layout, c.tiles_per_wave, c.waves, c.k_waves, c.depth, c.load_hint,
                                   c.kernel == QF_KERNEL_MFMA_XRING);
+  if (norm_eps != nullptr) fn = select_norm(c, layout);
   if (fn == nullptr) return QF_ERR_UNSUPPORTED;
   int st = launch(fn, grid, block, smem, s, a);
   if (st != QF_OK) return st;
@@ -3487,6 +3559,14 @@ int qf_w8a16_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, 
                   nullptr);
 }
 
+int qf_w8a16_gemm_rmsnorm(const uint16_t* x, int64_t ldx, float eps, const int8_t* w, int64_t ldw, int layout,
+                          const float* scale, void* y, int64_t ldy, int out_dtype, int M, int N, int K,
+                          const qf_w8a16_config* cfg, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!(eps >= 0.f) || K % 8) return QF_ERR_INVALID_ARG;
+  return run_gemm(x, ldx, w, ldw, layout, scale, y, ldy, out_dtype, M, N, K, cfg, workspace, workspace_bytes, stream,
+                  nullptr, &eps);
+}
+
 int qf_w8a16_gemm_noalloc(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int layout, const float* scale,
                           void* y, int64_t ldy, int out_dtype, int M, int N, int K, const qf_w8a16_config* cfg,
                           void* stream) {
@@ -3578,9 +3658,8 @@ int qf_scale_cast_bf16(const float* acc, int64_t lda, const float* scale, int M,
 int qf_rms_norm_rows_bf16(const uint16_t* x, int64_t ldx, int M, int N, float eps, uint16_t* y, int64_t ldy,
                           void* stream) {
   if (x == nullptr || y == nullptr || M < 1 || N < 1 || ldx < N || ldy < N || !(eps >= 0.f)) return QF_ERR_INVALID_ARG;
-  if (N % 8 || N > kNormPieces * kNormThreads * 8 || !aligned16(x) || !aligned16(y) || ldx % 8 || ldy % 8)
-    return QF_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(rms_norm_rows_kernel, dim3((unsigned)M), dim3(kNormThreads), 0, reinterpret_cast<hipStream_t>(stream),
+  if (N % 8 || !aligned16(x) || !aligned16(y) || ldx % 8 || ldy % 8) return QF_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(rms_norm_rows_kernel, dim3((unsigned)M), dim3(kWave), 0, reinterpret_cast<hipStream_t>(stream),
                      x, ldx, N, eps, y, ldy);
   return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
 }

@@ -15,6 +15,7 @@ import os
 from .w8a16 import (  # noqa: F401
     AUTO, ROWMAJOR, SMALL_M, TILED, W8A16Config, dequant_bf16, from_tiled, pick_config, resolve_config, tiled_numel,
     quantize_tokens_int8, rms_norm_rows, scale_cast_bf16, to_tiled, w8a16_mm, w8a16_mm_argmax, w8a16_mm_prefill,
+    w8a16_mm_rmsnorm,
     w8a8_mm)
 from .spec_attn import gqa_packed_spec_attention  # noqa: F401
 from .patches import (  # noqa: F401

@@ -52,6 +52,7 @@ EXPORTS = (
     "qf_w8a16_dequant_bf16",
     "qf_scale_cast_bf16",
     "qf_rms_norm_rows_bf16",
+    "qf_w8a16_gemm_rmsnorm",
     "qf_quantize_rows_int8",
     "qf_argmax_rows_bf16",
     "qf_argmax_rows_workspace_bytes",
@@ -148,6 +149,9 @@ def load() -> ctypes.CDLL:
     L.qf_scale_cast_bf16.restype = i32
     L.qf_rms_norm_rows_bf16.argtypes = [p, i64, i32, i32, ctypes.c_float, p, i64, p]
     L.qf_rms_norm_rows_bf16.restype = i32
+    L.qf_w8a16_gemm_rmsnorm.argtypes = [p, i64, ctypes.c_float, p, i64, i32, p, p, i64, i32, i32, i32, i32,
+                                        ctypes.POINTER(Config), p, sz, p]
+    L.qf_w8a16_gemm_rmsnorm.restype = i32
     L.qf_quantize_rows_int8.argtypes = [p, i64, p, p, i32, i32, p]
     L.qf_quantize_rows_int8.restype = i32
     L.qf_argmax_rows_bf16.argtypes = [p, i64, i32, i32, i32, i64, p, p]

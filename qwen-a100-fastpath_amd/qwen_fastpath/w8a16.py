@@ -209,6 +209,39 @@ def w8a16_mm(x: torch.Tensor, w_t: torch.Tensor, w_scale: torch.Tensor, cfg, out
     return torch.ops.qwen_fastpath.w8a16_mm(x, w_t, w_scale, int(layout), out_dtype, [int(v) for v in cfg])
 
 
+def w8a16_mm_rmsnorm(x: torch.Tensor, w_t: torch.Tensor, w_scale: torch.Tensor, cfg, out_dtype: torch.dtype,
+                     layout: int = TILED, eps: float = 2.0 ** -23) -> torch.Tensor:
+    """w8a16_mm of the rows of x scaled to unit RMS, w8a16_mm(rms_norm_rows(x, eps), ...) bit for bit, in one
+    launch where the configuration stages whole rows (qf_w8a16_gemm_rmsnorm); where it does not (a K split,
+    row-major weights), the same two calls."""
+    _on_gpu(x, w_t, w_scale)
+    lib = L.load()
+    if x.dim() != 2 or x.dtype != torch.bfloat16 or w_scale.dtype != torch.float32:
+        raise TypeError("x must be 2-D bf16 and w_scale fp32")
+    M, K = x.shape
+    N = w_scale.numel()
+    ldw = _weight_geometry(w_t, N, K, layout)
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"out_dtype must be bf16 or fp32, got {out_dtype}")
+    if M == 0:
+        return x.new_empty((0, N), dtype=out_dtype)
+    if x.stride(1) != 1 or x.data_ptr() % 16 or (M > 1 and x.stride(0) % 8):
+        x = x.contiguous()
+    ldx = x.stride(0) if M > 1 else K
+    c = _config_struct(AUTO if cfg is None else cfg)
+    ws_bytes = int(lib.qf_w8a16_workspace_bytes(M, N, K, layout, ctypes.byref(c)))
+    y = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    ws = _workspace(x.device, ws_bytes) if ws_bytes else None
+    rc = lib.qf_w8a16_gemm_rmsnorm(x.data_ptr(), ldx, float(eps), w_t.data_ptr(), ldw, layout, w_scale.data_ptr(),
+                                   y.data_ptr(), N, L.DTYPE_BF16 if out_dtype == torch.bfloat16 else L.DTYPE_F32,
+                                   M, N, K, ctypes.byref(c), ws.data_ptr() if ws is not None else None,
+                                   ws.numel() if ws is not None else 0, torch.cuda.current_stream(x.device).cuda_stream)
+    if rc == L.ERR_UNSUPPORTED:
+        return w8a16_mm(rms_norm_rows(x, eps), w_t, w_scale, cfg, out_dtype, layout)
+    L.check(rc, f"qf_w8a16_gemm_rmsnorm(M={M}, N={N}, K={K}, layout={layout})")
+    return y
+
+
 def w8a16_mm_argmax(x: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, n_valid: int, index_offset: int = 0,
                     cfg=None, layout: int = ROWMAJOR, with_logits: bool = False):
     """The draft head's argmax fused into the GEMM (the logits of w8a16_mm, then
@@ -330,7 +363,7 @@ def rms_norm_rows(x: torch.Tensor, eps: float = 2.0 ** -23, out: torch.Tensor | 
     """Each row of a bf16 [M, N] tensor scaled to unit RMS in one launch (qf_rms_norm_rows_bf16):
     bf16(x * (1 / sqrt(mean(x^2) + eps))), within one bf16 ulp of torch.nn.functional.rms_norm(x, (N,), eps=eps)
     (whose default eps for a bf16 input is float32's epsilon, 2^-23, the default here too).  The glue between
-    the layers of the 64-layer decode-step benchmark; N % 8 == 0 and N <= 8192."""
+    the layers of the 64-layer decode-step benchmark; N % 8 == 0."""
     _on_gpu(x, out)
     if x.dim() != 2 or x.dtype != torch.bfloat16:
         raise TypeError("x must be a 2-D bf16 tensor")

@@ -6,7 +6,8 @@
 * the gate_up M sweep (M = 1, 2, 3, 5, 8, 12, 16) on TILED weights;
 * the 64-layer decode-step stack at M = 5 (distinct seeded weights per layer, o_proj reading the first
   8192 qkv outputs, down the first 17408 gate_up outputs, each layer's output re-normalised to unit RMS
-  as the next input by qf_rms_norm_rows_bf16) captured as one graph: replays equal the eager step bit for bit, and for sampled
+  as the next input inside the next qkv GEMM's staging, qf_w8a16_gemm_rmsnorm, the same bits as
+  qf_rms_norm_rows_bf16 and then the GEMM) captured as one graph: replays equal the eager step bit for bit, and for sampled
   layers every GEMM is checked against the oracle on the input it actually received.
 
 Each check applies oracle.check_w8a16 (every output within 1 bf16 ulp plus the fp32 floor of the exact
@@ -119,12 +120,20 @@ class _StackLayer:
             self.s[name] = torch.randn(N, device=DEV, generator=g).abs_().mul_(0.002).add_(1e-4)
 
 
-def _step(layers, x0, record=None):
+def _step(layers, x0, record=None, fused=True):
+    """One decode step.  fused: layers 1..63 take the previous layer's output through the normalising qkv GEMM
+    (qf_w8a16_gemm_rmsnorm); otherwise through qf_rms_norm_rows_bf16 and then the GEMM (the same bits)."""
     h = x0
+    d = None
     for i, L_ in enumerate(layers):
         mm = lambda a, n: qf.w8a16_mm(a, L_.w[n], L_.s[n], None, torch.bfloat16, qf.TILED)  # noqa: E731
+        if d is not None:
+            h = qf.rms_norm_rows(d) if (not fused or record is not None) else None
         ins = {"qkv": h}
-        qkv = mm(h, "qkv")
+        if d is not None and fused:
+            qkv = qf.w8a16_mm_rmsnorm(d, L_.w["qkv"], L_.s["qkv"], None, torch.bfloat16, qf.TILED)
+        else:
+            qkv = mm(h, "qkv")
         ins["o_proj"] = qkv[:, :8192]
         o = mm(ins["o_proj"], "o_proj")
         ins["gate_up"] = o
@@ -133,8 +142,7 @@ def _step(layers, x0, record=None):
         d = mm(ins["down"], "down")
         if record is not None and i in record:
             record[i] = ({n: t.clone() for n, t in ins.items()}, {"qkv": qkv, "o_proj": o, "gate_up": gu, "down": d})
-        h = qf.rms_norm_rows(d)  # unit RMS, torch's default eps for bf16 (2^-23), one launch
-    return h
+    return qf.rms_norm_rows(d)  # unit RMS, torch's default eps for bf16 (2^-23)
 
 
 def test_stack64_graph_replay_and_sampled_layers(oracle):
@@ -147,6 +155,8 @@ def test_stack64_graph_replay_and_sampled_layers(oracle):
     assert torch.isfinite(eager.float()).all()
     again = _step(layers, x0)
     assert torch.equal(eager, again), "eager step is not bitwise reproducible"
+    unfused = _step(layers, x0, fused=False)
+    assert torch.equal(eager, unfused), "the normalising qkv GEMM differs from the norm launch + GEMM"
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -175,7 +185,8 @@ def test_stack64_graph_replay_and_sampled_layers(oracle):
                    qf.resolve_config(M5, N, K, qf.TILED))
 
 
-@pytest.mark.parametrize("M,N", [(5, 5120), (1, 8), (7, 8192), (16, 4096), (3, 17408 // 8 * 8 // 4)])
+@pytest.mark.parametrize("M,N", [(5, 5120), (1, 8), (7, 8192), (16, 4096), (3, 17408 // 8 * 8 // 4), (5, 17408),
+                                 (2, 34816)])
 def test_rms_norm_rows(M, N):
     """The stack's glue (qf_rms_norm_rows_bf16) against torch's fp32 restatement and torch's rms_norm (eps 2^-23,
     torch's default for bf16 inputs), also with eps 2^-7: at most one bf16 ulp apart; reproducible; in place equal
@@ -199,3 +210,48 @@ def test_rms_norm_rows(M, N):
     assert (yi - tref.view(torch.int16).int()).abs().max().item() <= 1
     assert (y7.view(torch.int16).int() - ref7.view(torch.int16).int()).abs().max().item() <= 1
     assert torch.equal(y, again) and torch.equal(y, inplace)
+
+
+@pytest.mark.parametrize("M,N,K,cfg", [
+    (5, 10240, 5120, None),                       # qkv's automatic shape: MFMA kernel, 4 tile groups x 2 k-slices
+    (5, 34816, 5120, None),                       # gate_up's: the stream kernel, x staged in LDS
+    (3, 5120, 8192, None),                        # o_proj's: 2 x 4
+    (1, 5120, 5120, None),                        # the single linear at M = 1: 1 x 4, 4 wavefronts
+    (16, 4096, 2048, (2, 1, 1, 8, 4, 1, 1, 0)),   # 8 x 1
+    (7, 1000, 4096, (2, 1, 1, 8, 4, 1, 4, 0)),    # 2 x 4, ragged N
+    (5, 2000, 17408, None),                       # a K split: the two calls instead
+])
+def test_gemm_rmsnorm_bitwise(M, N, K, cfg):
+    """qf_w8a16_gemm_rmsnorm (the staged rows normalised inside the GEMM) equals qf_rms_norm_rows_bf16 followed by
+    the GEMM bit for bit, bf16 and fp32 outputs, rows at scales 2^-6 .. 2^6 and a zero row, eps 2^-23 and 2^-7;
+    a configuration that splits K is refused by the library (QF_ERR_UNSUPPORTED) and the package makes the two
+    calls."""
+    import ctypes
+    from qwen_fastpath import _lib as L
+    g = torch.Generator(device=DEV)
+    g.manual_seed(M * 7 + N + K)
+    scale = torch.exp2(torch.randint(-6, 7, (M, 1), device=DEV, generator=g).float())
+    x = (torch.randn(M, K, device=DEV, generator=g) * scale).to(torch.bfloat16)
+    if M > 2:
+        x[1].zero_()
+    img = torch.randint(-127, 128, (qf.tiled_numel(N, K),), dtype=torch.int8, device=DEV, generator=g)
+    s = (torch.randn(N, device=DEV, generator=g).abs() * 0.002 + 1e-4).float()
+    c = None if cfg is None else qf.W8A16Config(*cfg)
+    print(f"gemm_rmsnorm M={M} N={N} K={K} cfg={cfg}", flush=True)
+    for eps in (2.0 ** -23, 2.0 ** -7):
+        for dt in (torch.bfloat16, torch.float32):
+            want = qf.w8a16_mm(qf.rms_norm_rows(x, eps), img, s, c, dt, qf.TILED)
+            got = qf.w8a16_mm_rmsnorm(x, img, s, c, dt, qf.TILED, eps)
+            torch.cuda.synchronize()
+            bits = torch.int16 if dt == torch.bfloat16 else torch.int32
+            assert torch.equal(got.view(bits), want.view(bits)), (M, N, K, cfg, eps, dt)
+    lib = L.load()
+    rc_cfg = L.Config.from_seq(tuple(c) if c is not None else (0,) * 8)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    need = int(lib.qf_w8a16_workspace_bytes(M, N, K, qf.TILED, ctypes.byref(rc_cfg)))
+    ws = torch.zeros(max(need, 16), dtype=torch.uint8, device=DEV)
+    rc = lib.qf_w8a16_gemm_rmsnorm(x.data_ptr(), K, 2.0 ** -23, img.data_ptr(), K, qf.TILED, s.data_ptr(), y.data_ptr(),
+                                   N, L.DTYPE_BF16, M, N, K, ctypes.byref(rc_cfg), ws.data_ptr(), ws.numel(),
+                                   torch.cuda.current_stream().cuda_stream)
+    split = qf.resolve_config(M, N, K, qf.TILED).split_k > 1 if cfg is None else cfg[1] > 1
+    assert rc == (L.ERR_UNSUPPORTED if split else L.OK), rc
