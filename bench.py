@@ -493,14 +493,17 @@ def read_ceiling(torch, qf, dev, window: int, detail=None) -> float:
               for b in (512, 2048)]
     probes += [("stream_w%d_d%d" % (w, d), lambda i, st, w=w, d=d: lib.qf_read_probe_stream(
                    buf.data_ptr() + i * window, window, sink.data_ptr(), w, d, st)) for (w, d) in ((8, 4), (8, 8), (16, 4))]
+    # at least 40 launches a graph, as the GEMM timings have: a graph's own start is then a small share
+    reps = -(-40 // nwin)
     best = 0.0
     for name, call in probes:
         def fn(call=call):
             st = torch.cuda.current_stream().cuda_stream
-            for i in range(nwin):
-                L.check(call(i, st), "probe")
+            for _ in range(reps):
+                for i in range(nwin):
+                    L.check(call(i, st), "probe")
 
-        us = time_graph(torch, fn, nwin)
+        us = time_graph(torch, fn, nwin * reps)
         if detail is not None:
             detail[name] = round(us, 2)
         best = max(best, window / us / 1e3)
