@@ -1139,7 +1139,8 @@ def run_stack64(torch, qf, dev, args):
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded int8 weights, fp32 scales, bf16 activations)",
         "config": {"workload": "64-layer decode-step linear stack at M=5 (4 GEMMs/layer, distinct weights, "
-                               "one row normalisation per layer), one hipGraph per step", "M": st["M"], "layers": st["layers"],
+                               "each layer's input normalised to unit RMS inside its qkv GEMM), one hipGraph per step",
+                   "M": st["M"], "layers": st["layers"],
                    "bytes_per_step": st["bytes_per_step"]},
         "us_per_layer": st["us_per_layer"],
         "pct_of_peak": st["pct_peak"],

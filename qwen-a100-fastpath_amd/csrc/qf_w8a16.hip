@@ -213,22 +213,6 @@ __device__ __forceinline__ void lds_barrier() {
 // read as N / 8 pieces of 16 bytes.  Lane t of one wavefront sums the squares of pieces t, t + 64, t + 128, ...
 // in that order (each piece's 8 values in order, one fused multiply-add each); the 64 lane sums then fold by a
 // butterfly of xor shuffles (32, 16, ..., 1), after which every lane holds the same total.
-template <typename Piece>
-__device__ __forceinline__ float row_sumsq(int npieces, int lane, Piece piece) {
-  float ss = 0.f;
-  for (int j = lane; j < npieces; j += kWave) {
-    const u32x4_t v = piece(j);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float lo = __uint_as_float(v[e] << 16), hi = __uint_as_float(v[e] & 0xffff0000u);
-      ss = __builtin_fmaf(lo, lo, ss);
-      ss = __builtin_fmaf(hi, hi, ss);
-    }
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, kWave);
-  return ss;
-}
 
 // 1 / sqrt(mean of squares + eps) (IEEE division; the same instructions wherever it is used).
 __device__ __forceinline__ float rms_inv(float total, int n, float eps) {
@@ -244,25 +228,79 @@ __device__ __forceinline__ u32x4_t scale_piece(const u32x4_t v, float inv) {
   return o;
 }
 
-// Normalise the M staged rows of x in LDS (row m at byte m * pitch, K values) in place: wavefront w computes the
-// rows w, w + WAVES, ... in the canonical order, then every thread rescales its share of the pieces.  Called by
-// the whole workgroup after the staging barrier; LDS-only barriers keep the weight prefetch in flight.
+// One row of npieces pieces normalised by one wavefront in the canonical order, through load(j) and
+// store(j, piece).  The lane's pieces are read P at a time (the P loads issued before their multiply-adds); its
+// first P pieces stay in registers for the scaling pass, later ones are read again.  Each piece is read and
+// written by its own lane only, so y may be x.
+template <int P, typename Load, typename Store>
+__device__ __forceinline__ void normalise_row(int npieces, int n, float eps, int lane, Load load, Store store) {
+  float ss = 0.f;
+  auto add = [&](const u32x4_t x) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = __uint_as_float(x[e] << 16), hi = __uint_as_float(x[e] & 0xffff0000u);
+      ss = __builtin_fmaf(lo, lo, ss);
+      ss = __builtin_fmaf(hi, hi, ss);
+    }
+  };
+  u32x4_t v[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int j = p * kWave + lane;
+    v[p] = j < npieces ? load(j) : (u32x4_t){0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+    if (p * kWave + lane < npieces) add(v[p]);
+  for (int j0 = P * kWave + lane; j0 < npieces; j0 += P * kWave) {
+    u32x4_t t[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int j = j0 + p * kWave;
+      t[p] = j < npieces ? load(j) : (u32x4_t){0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+      if (j0 + p * kWave < npieces) add(t[p]);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+  const float inv = rms_inv(ss, n, eps);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int j = p * kWave + lane;
+    if (j < npieces) store(j, scale_piece(v[p], inv));
+  }
+  for (int j0 = P * kWave + lane; j0 < npieces; j0 += P * kWave) {
+    u32x4_t t[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int j = j0 + p * kWave;
+      t[p] = j < npieces ? load(j) : (u32x4_t){0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int j = j0 + p * kWave;
+      if (j < npieces) store(j, scale_piece(t[p], inv));
+    }
+  }
+}
+
+// Normalise the M staged rows of x in LDS (row m at byte m * pitch, K values) in place: wavefront w normalises
+// the rows w, w + WAVES, ... (normalise_row, 3 pieces a lane at a time: the one-tile MFMA kernels that call this
+// run within 80 VGPRs beside their weight prefetch ring, and 4 would spill), then one LDS-only barrier, so the
+// prefetch stays in flight.
+// Called by the whole workgroup after the staging barrier.
+constexpr int kStagedNormPieces = 3;
 template <int WAVES>
-__device__ __forceinline__ void normalise_staged_rows(uint8_t* smem, int pitch, int M, int K, float eps,
-                                                      float* inv_lds) {
+__device__ __forceinline__ void normalise_staged_rows(uint8_t* smem, int pitch, int M, int K, float eps) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int npieces = K / 8;
   for (int m = wave; m < M; m += WAVES) {
-    const uint8_t* row = smem + m * pitch;
-    const float total = row_sumsq(npieces, lane, [&](int j) { return *reinterpret_cast<const u32x4_t*>(row + j * 16); });
-    if (lane == 0) inv_lds[m] = rms_inv(total, K, eps);
-  }
-  lds_barrier();
-  for (int q = threadIdx.x; q < M * npieces; q += WAVES * kWave) {
-    const int m = q / npieces;
-    u32x4_t* pc = reinterpret_cast<u32x4_t*>(smem + m * pitch + (q - m * npieces) * 16);
-    *pc = scale_piece(*pc, inv_lds[m]);
+    uint8_t* row = smem + m * pitch;
+    normalise_row<kStagedNormPieces>(
+        K / 8, K, eps, lane, [&](int j) { return *reinterpret_cast<const u32x4_t*>(row + j * 16); },
+        [&](int j, const u32x4_t o) { *reinterpret_cast<u32x4_t*>(row + j * 16) = o; });
   }
   lds_barrier();
 }
@@ -482,7 +520,6 @@ __global__ void __launch_bounds__(WN * WK * kWave)
     w8a16_mfma_kernel(const GemmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ int last_arrival;
-  __shared__ float norm_inv[NORM ? QF_W8A16_MAX_M : 1];
   constexpr int WAVES = WN * WK;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // uniform: scalar registers
@@ -581,7 +618,7 @@ __global__ void __launch_bounds__(WN * WK * kWave)
       prologue();
     }
     lds_barrier();  // the weight requests issued above stay in flight across it
-    if constexpr (NORM) normalise_staged_rows<WAVES>(smem, pitch, a.M, a.K, a.norm_eps, norm_inv);
+    if constexpr (NORM) normalise_staged_rows<WAVES>(smem, pitch, a.M, a.K, a.norm_eps);
     const uint8_t* xs = smem + xr * pitch + (k_lo * kStepK + 16 * g) * 2;
     constexpr int xs_stride = kStepK * 2 * WK;
     for (int base = 0; base < nsteps; base += RING) {
@@ -772,7 +809,6 @@ __host__ __device__ __forceinline__ int align16i(int n) { return (n + 15) & ~15;
 template <int W, int DEPTH, bool NTH, bool NORM = false>
 __global__ void __launch_bounds__(W * kWave) w8a16_stream_kernel(const GemmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
-  __shared__ float norm_inv[NORM ? QF_W8A16_MAX_M : 1];
   constexpr int RING = DEPTH + 1;
   const int lane = threadIdx.x & (kWave - 1);
   const int v = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -829,7 +865,7 @@ __global__ void __launch_bounds__(W * kWave) w8a16_stream_kernel(const GemmArgs 
     prologue();
   }
   lds_barrier();  // the weight requests issued above stay in flight across it
-  if constexpr (NORM) normalise_staged_rows<W>(smem, pitch, a.M, a.K, a.norm_eps, norm_inv);
+  if constexpr (NORM) normalise_staged_rows<W>(smem, pitch, a.M, a.K, a.norm_eps);
 
   // Lane (g, r) reads x[min(r, M - 1)][k + 16 g .. + 15] of each step (token rows r >= M are never stored).
   const uint8_t* xrow = smem + min(r, a.M - 1) * pitch + 32 * g;
@@ -2291,37 +2327,15 @@ __global__ void __launch_bounds__(kArgmaxSplitThreads) argmax_rows_split_kernel(
 }
 
 // Row normalisation to unit RMS, bf16 in and out: y[m, :] = bf16_rne(x[m, :] * (1 / sqrt(mean(x[m, :]^2) +
-// eps))).  One workgroup per row; each thread keeps its 16-byte pieces in registers between the two
-// passes.  The sum of squares is formed in a fixed order (per thread over its pieces, a fixed butterfly
-// per wavefront, then the wavefronts in order), so results are reproducible.
+// eps))).  One wavefront per row (normalise_row); rows up to 64 x kNormPieces pieces are read from memory once.
 constexpr int kNormPieces = 16;  // 16-byte pieces per lane held in registers: 64 x 16 x 8 = 8192 values
-
-// One wavefront per row: the row's first pieces are loaded into registers (lane t: pieces t, t + 64, ..., up to
-// kNormPieces of them; longer rows read the rest from memory in both passes), summed in the canonical order of
-// row_sumsq, and written back scaled (y may be x: each piece is read and written by its own lane only).
 __global__ void __launch_bounds__(kWave) rms_norm_rows_kernel(const uint16_t* x, int64_t ldx, int N, float eps,
                                                               uint16_t* y, int64_t ldy) {
   const uint16_t* xr = x + (int64_t)blockIdx.x * ldx;
   uint16_t* yr = y + (int64_t)blockIdx.x * ldy;
-  const int lane = threadIdx.x;
-  const int npieces = N / 8;
-  u32x4_t v[kNormPieces];
-#pragma unroll
-  for (int p = 0; p < kNormPieces; ++p) {
-    const int j = p * kWave + lane;
-    v[p] = j < npieces ? *reinterpret_cast<const u32x4_t*>(xr + j * 8) : (u32x4_t){0, 0, 0, 0};
-  }
-  auto piece = [&](int j) {
-    const int p = j / kWave;
-    if (p >= kNormPieces) return *reinterpret_cast<const u32x4_t*>(xr + (int64_t)j * 8);
-    u32x4_t r = v[0];
-#pragma unroll
-    for (int q = 1; q < kNormPieces; ++q)
-      if (p == q) r = v[q];
-    return r;
-  };
-  const float inv = rms_inv(row_sumsq(npieces, lane, piece), N, eps);
-  for (int j = lane; j < npieces; j += kWave) *reinterpret_cast<u32x4_t*>(yr + (int64_t)j * 8) = scale_piece(piece(j), inv);
+  normalise_row<kNormPieces>(
+      N / 8, N, eps, (int)threadIdx.x, [&](int j) { return *reinterpret_cast<const u32x4_t*>(xr + (int64_t)j * 8); },
+      [&](int j, const u32x4_t o) { *reinterpret_cast<u32x4_t*>(yr + (int64_t)j * 8) = o; });
 }
 
 // ---------------------------------------------------------------------------------------------
