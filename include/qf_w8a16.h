@@ -175,11 +175,16 @@ int qf_w8a16_gemm_noalloc(const uint16_t* x, int64_t ldx,
  * with NaN counting as the maximum and ties going to the lowest index: the result of
  * qf_argmax_rows_bf16 on the stored logits, without writing and re-reading them.  y may be NULL (no
  * logits are stored); otherwise it is written as by qf_w8a16_gemm.  Each wavefront column of the GEMM
- * leaves one candidate per token in the workspace and a second small launch folds them.  Served when
- * the configuration is the MFMA kernel without a K split (else QF_ERR_UNSUPPORTED: call qf_w8a16_gemm
- * and qf_argmax_rows_bf16).  Workspace: qf_w8a16_argmax_workspace_bytes() bytes, needing no clearing
- * (the same buffer as a split-K workspace may serve: its counter prefix is not touched); calls that may
- * run at the same time need distinct workspaces.  1 <= n_valid <= N.
+ * folds its candidate per token into one of 64 slots of the token in the workspace (a 64-bit atomic
+ * maximum of a key that orders candidates as above; the slots spread over the counter prefix so that no
+ * address or memory channel takes many of the atomics), and a second launch of one wavefront per token
+ * folds the slots into the ids and clears them.
+ * Served when the configuration is the MFMA kernel without a K split (else QF_ERR_UNSUPPORTED: call
+ * qf_w8a16_gemm and qf_argmax_rows_bf16).  Workspace: qf_w8a16_argmax_workspace_bytes() bytes with the
+ * split-K workspace contract: its first QF_W8A16_COUNTER_BYTES bytes (the slots) must be zero when a
+ * call starts and are zero again when it ends, so a workspace zeroed once serves any number of calls
+ * issued in order on one stream (a split-K workspace may serve); calls that may run at the same time
+ * need distinct workspaces.  1 <= n_valid <= N.
  * Reference: the W8A16 logits and the pad-masked argmax of get_top_tokens,
  * plugin/qwen_fastpath/patches.py:160-166,178-185, in one launch. */
 int qf_w8a16_gemm_argmax(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int layout,

@@ -62,14 +62,13 @@ struct GemmArgs {
   int fused_reduce;  // MFMA, split_k > 1: the last workgroup of an n-block reduces (else a second kernel)
   // Fused argmax (MFMA, split_k == 1): ids[m] = index_offset + argmax over n < n_valid of the bf16
   // outputs y[m, n] (NaN highest, then value, then the lowest index); y may be null.  Each wavefront
-  // column writes its candidate per token as one (value bits | index << 32) record to
-  // am_cand[m * am_stride + column], columns = grid.x * WN; argmax_fold_kernel folds them.
+  // column folds its candidate per token into one of the token's kArgmaxSlots slots (a 64-bit atomic
+  // maximum of argmax_key); argmax_slots_kernel folds the slots into ids and clears them.
   int argmax;
   int n_valid;
-  int am_stride;  // records per token row: the column count rounded up to even (16-byte pairs)
   int64_t index_offset;
   int64_t* ids;
-  uint64_t* am_cand;
+  uint64_t* am_slots;
   // Wide-M kernel: token groups per n-block and rows per group (a multiple of 16; the last group
   // takes the rest, at least one row).
   int groups;
@@ -194,6 +193,26 @@ __device__ __forceinline__ void argmax_fold(float v, int i, float& bv, int& bi) 
     bv = v;
     bi = i;
   }
+}
+
+// Slots of the fused argmax per token, spread over the workspace's counter prefix: wavefront column c of the GEMM
+// folds into slot c % kArgmaxSlots of its token, slot (m, s) at 64-bit word (s * M + m) * stride, the stride the
+// largest power of two that fits (64 bytes at M = 16), so the atomics on any one address and any one memory
+// channel stay few (one slot per token serialised 9496 of them on the draft head: 155 against 122 us a step).
+constexpr int kArgmaxSlots = 64;
+__host__ __device__ __forceinline__ int argmax_slot_stride(int M) {
+  int st = QF_W8A16_COUNTER_BYTES / 8 / (kArgmaxSlots * M);
+  while (st & (st - 1)) st &= st - 1;
+  return st;
+}
+static_assert(QF_W8A16_COUNTER_BYTES / 8 / (kArgmaxSlots * QF_W8A16_MAX_M) >= 8, "slots on separate 64-byte lines");
+
+// A 64-bit key that orders candidates as argmax_better does: the larger key is the better candidate (NaN
+// highest, then the larger value, -0 ranking with +0, then the lower index), and 0 is below every key.
+__device__ __forceinline__ uint64_t argmax_key(float v, int i) {
+  const uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);
+  const uint32_t k = v != v ? 0xffffffffu : ((u >> 31) ? ~u : (u | 0x80000000u));
+  return ((uint64_t)k << 32) | (uint64_t)(~(uint32_t)i);
 }
 
 // s_waitcnt immediate (gfx9 encoding) that waits for vmcnt == 0 and leaves expcnt / lgkmcnt free.
@@ -401,8 +420,9 @@ __device__ __forceinline__ float bf16_value(float v) { return __uint_as_float((u
 
 // Fused argmax epilogue of the MFMA kernel (split_k == 1).  Each lane ranks its scaled outputs (bf16
 // values, columns < n_valid) per token, the lanes of a token fold by shuffles, and each wavefront
-// column stores one candidate record per token; argmax_fold_kernel then folds the candidates.  Plain
-// stores, no barrier and no arrival counting: the workgroup leaves at once.
+// column folds its candidate into the token's slot with one 64-bit atomic maximum of argmax_key (the
+// maximum of keys is the argmax whatever the order of arrival).  The atomics return nothing: no wait,
+// no barrier, the workgroup leaves at once; argmax_slots_kernel reads the slots after the kernel.
 template <int NT, int WN>
 __device__ __forceinline__ void argmax_epilogue(const GemmArgs& a, const f32x4_t (&acc)[NT], bool holder, int tile0,
                                                 int ntiles, int g, int wk, int wn, int lane) {
@@ -438,70 +458,27 @@ __device__ __forceinline__ void argmax_epilogue(const GemmArgs& a, const f32x4_t
     const int oi = __shfl_xor(bi, off);
     argmax_fold(ov, oi, bv, bi);
   }
-  // every wavefront column stores its own candidate: no barrier, the workgroup leaves at once
-  if (wk == 0 && lane < a.M)
-    a.am_cand[(int64_t)lane * a.am_stride + (int64_t)blockIdx.x * WN + wn] =
-        (uint64_t)__float_as_uint(bv) | ((uint64_t)(uint32_t)bi << 32);
+  if (wk == 0 && lane < a.M) {
+    const int slot = (int)((blockIdx.x * WN + wn) % kArgmaxSlots);
+    (void)__hip_atomic_fetch_max(a.am_slots + ((int64_t)slot * a.M + lane) * argmax_slot_stride(a.M),
+                                 argmax_key(bv, bi), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
-// Second pass of the fused argmax: one 1024-thread workgroup per token folds the token's ncand
-// candidate records (contiguous, 16-byte aligned row).  Each thread issues all its 16-byte pair loads
-// of a pass before it folds any (kFoldBatch pairs, 16384 records per pass), then a fixed butterfly and
-// an LDS tree.  argmax_better is a total order, so the result is that of a sequential scan.
-constexpr int kFoldThreads = 1024;
-constexpr int kFoldBatch = 8;
-
-__global__ void __launch_bounds__(kFoldThreads) argmax_fold_kernel(const uint64_t* cand, int ncand, int stride,
-                                                                   int64_t index_offset, int64_t* ids) {
-  __shared__ float sv[kFoldThreads / kWave];
-  __shared__ int si[kFoldThreads / kWave];
-  const int r = blockIdx.x;
-  const uint64_t* row = cand + (int64_t)r * stride;
-  float bv = -__builtin_inff();
-  int bi = 0x7fffffff;
-  const int npairs = ncand / 2;  // whole pairs; an odd last record is folded below
-  for (int base = threadIdx.x; base < npairs; base += kFoldThreads * kFoldBatch) {
-    u32x4_t p[kFoldBatch];  // (value, index) of two records
-#pragma unroll
-    for (int u = 0; u < kFoldBatch; ++u) {
-      const int e = base + u * kFoldThreads;
-      if (e < npairs) p[u] = *reinterpret_cast<const u32x4_t*>(row + 2 * e);
-    }
-#pragma unroll
-    for (int u = 0; u < kFoldBatch; ++u) {
-      if (base + u * kFoldThreads < npairs) {
-        argmax_fold(__uint_as_float(p[u][0]), (int)p[u][1], bv, bi);
-        argmax_fold(__uint_as_float(p[u][2]), (int)p[u][3], bv, bi);
-      }
-    }
-  }
-  if ((ncand & 1) && threadIdx.x == 0) {
-    const uint64_t rec = row[ncand - 1];
-    argmax_fold(__uint_as_float((uint32_t)rec), (int)(uint32_t)(rec >> 32), bv, bi);
-  }
+// Second pass of the fused argmax: one wavefront per token; lane s reads slot s (every atomic maximum of the
+// GEMM is complete at the kernel boundary) and clears it for the next call (the workspace's counter prefix is
+// zero on entry and on exit of every call); the maximum key over the lanes holds the token's index.
+__global__ void __launch_bounds__(kWave) argmax_slots_kernel(uint64_t* slots, int64_t index_offset, int64_t* ids) {
+  static_assert(kArgmaxSlots == kWave, "one slot per lane");
+  uint64_t* p = slots + ((int64_t)threadIdx.x * gridDim.x + blockIdx.x) * argmax_slot_stride(gridDim.x);
+  uint64_t key = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(p, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
-    const float ov = __shfl_xor(bv, off);
-    const int oi = __shfl_xor(bi, off);
-    argmax_fold(ov, oi, bv, bi);
+    const uint64_t o = __shfl_xor(key, off, kWave);
+    key = o > key ? o : key;
   }
-  if ((threadIdx.x & (kWave - 1)) == 0) {
-    sv[threadIdx.x / kWave] = bv;
-    si[threadIdx.x / kWave] = bi;
-  }
-  __syncthreads();
-  if (threadIdx.x < kWave) {
-    const int w = threadIdx.x;
-    bv = w < kFoldThreads / kWave ? sv[w] : -__builtin_inff();
-    bi = w < kFoldThreads / kWave ? si[w] : 0x7fffffff;
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bv, off);
-      const int oi = __shfl_xor(bi, off);
-      argmax_fold(ov, oi, bv, bi);
-    }
-    if (threadIdx.x == 0) ids[r] = (int64_t)bi + index_offset;
-  }
+  if (threadIdx.x == 0) ids[blockIdx.x] = (int64_t)(uint32_t)~(uint32_t)key + index_offset;
 }
 
 // Occupancy floor of the MFMA kernel.  One-tile, DEPTH-4 wavefronts fit in 80 VGPRs (the compiler's
@@ -2979,18 +2956,8 @@ struct ArgmaxRequest {
   int64_t* ids;
 };
 
-// Candidates of the fused argmax: one per (workgroup, wavefront column).
-size_t argmax_candidates(const qf_w8a16_config& c, int N) {
-  return (size_t)workgroups(c, N) * (size_t)(c.waves / c.k_waves);
-}
-
-// Records per token row of the fused argmax's candidate table (even: rows stay 16-byte aligned).
-size_t argmax_stride(const qf_w8a16_config& c, int N) { return (argmax_candidates(c, N) + 1) & ~(size_t)1; }
-
-// Workspace of the fused argmax: the counter prefix (unused here), then the [M][stride] records.
-size_t argmax_workspace_for(const qf_w8a16_config& c, int M, int N) {
-  return QF_W8A16_COUNTER_BYTES + argmax_stride(c, N) * (size_t)M * sizeof(uint64_t);
-}
+// Workspace of the fused argmax: the counter prefix, which holds the per-token slots.
+size_t argmax_workspace_for(const qf_w8a16_config&, int, int) { return QF_W8A16_COUNTER_BYTES; }
 
 // norm_eps != nullptr: the x rows are scaled to unit RMS first (qf_w8a16_gemm_rmsnorm), by a NORM instantiation.
 int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int layout, const float* scale, void* y,
@@ -3041,11 +3008,7 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
   a.n_valid = am != nullptr ? am->n_valid : 0;
   a.index_offset = am != nullptr ? am->index_offset : 0;
   a.ids = am != nullptr ? am->ids : nullptr;
-  const size_t ncand = argmax_candidates(c, N);
-  a.am_stride = (int)argmax_stride(c, N);
-  a.am_cand = am != nullptr
-                  ? reinterpret_cast<uint64_t*>(reinterpret_cast<uint8_t*>(workspace) + QF_W8A16_COUNTER_BYTES)
-                  : nullptr;
+  a.am_slots = am != nullptr ? reinterpret_cast<uint64_t*>(workspace) : nullptr;
   a.groups = 1;
   a.group_rows = M;
   if (c.kernel == QF_KERNEL_MFMA_WIDE) wide_groups(M, a.groups, a.group_rows);
@@ -3069,8 +3032,7 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
   int st = launch(fn, grid, block, smem, s, a);
   if (st != QF_OK) return st;
   if (am != nullptr) {
-    hipLaunchKernelGGL(argmax_fold_kernel, dim3(M), dim3(kFoldThreads), 0, s, a.am_cand, (int)ncand, a.am_stride,
-                       a.index_offset, a.ids);
+    hipLaunchKernelGGL(argmax_slots_kernel, dim3(M), dim3(kWave), 0, s, a.am_slots, a.index_offset, a.ids);
     return hipGetLastError() == hipSuccess ? QF_OK : QF_ERR_HIP;
   }
   if (c.split_k > 1 && !a.fused_reduce) {

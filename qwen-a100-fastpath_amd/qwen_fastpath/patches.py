@@ -604,8 +604,8 @@ def int8_top_tokens(head: Optional[Int8Head], hidden_states: torch.Tensor, vocab
     """Draft token ids of the int8 head (patches.py:178-185); None when the guard of int8_logits fails.
     Two ways, same ids: the W8A16 logits, then the pad-masked argmax over them (two launches); or the
     argmax folded into the GEMM's epilogue (qf_w8a16_gemm_argmax: the logits are neither written nor
-    re-read, at the cost of a small candidate-fold launch; the default).  Measured on MI355X for the
-    151936 x 5120 head: 117.2 us fused vs 120.2 us two-launch at M = 1, 125.1 vs 127.0 us at M = 4.
+    re-read; a one-wavefront launch per token reads the folded slots; the default).  Measured on MI355X for
+    the 151936 x 5120 head: 117.2 us fused vs 121.2 us two-launch at M = 1, 124.4 vs 128.0 us at M = 4.
     Shapes the fused path does not serve take the two-launch path."""
     if (head is None or hidden_states.dim() != 2 or hidden_states.shape[0] > SMALL_M
             or hidden_states.dtype != torch.bfloat16 or logits_as_input or soft_cap is not None

@@ -94,7 +94,7 @@ def _weight_geometry(w: torch.Tensor, N: int, K: int, layout: int) -> int:
     raise ValueError(f"unknown layout {layout}")
 
 
-# Workspaces (split-K partials and arrival counters, the fused argmax's candidate table, the row-split
+# Workspaces (split-K partials and arrival counters, the fused argmax's per-token slots, the row-split
 # argmax table), one per (device, stream): calls issued in order on one stream share it, and calls on
 # different streams never do, so they may overlap.  The library's arrival counters at the front of a
 # workspace must be zero when a call starts and every call leaves them zero, so:

@@ -1,8 +1,9 @@
 """The draft head's argmax fused into the W8A16 kernel (qf_w8a16_gemm_argmax): the ids must equal the
 pad-masked argmax of the bf16 logits the plain kernel writes (plugin/qwen_fastpath/patches.py:178-185),
-and the oracle's argmax of those logits, bit for bit -- with planted ties (first index wins), a NaN
-row (NaN is the maximum), a winner planted in the pad columns (ignored), workgroup counts below and
-above one group of 64 with a ragged last group, repeated calls and graph replay."""
+and the oracle's argmax of those logits, bit for bit -- with planted ties (first index wins, -0.0 and
++0.0 tie), a NaN row (NaN is the maximum), rows of negative logits, a winner planted in the pad columns
+(ignored), several grid sizes, repeated calls (the per-token slots are cleared for the next call) and
+graph replay."""
 import numpy as np
 import pytest
 import torch
@@ -50,7 +51,7 @@ def test_fused_ids_equal_unfused(oracle, layout, M, N, K):
     ref = qf.top_tokens(y, num_pad, offset).cpu().numpy()
     y_bits = y.view(torch.int16).cpu().numpy().view(np.uint16)
     assert np.array_equal(ref, _ref_ids(y_bits, N - num_pad, offset, oracle))
-    for rep in range(2):  # the arrival counters are back at zero for the next call
+    for rep in range(2):  # the per-token slots are back at zero for the next call
         res = qf.w8a16_mm_argmax(x, wl, s, N - num_pad, offset, None, layout, with_logits=True)
         if res is None:  # configurations without the fused epilogue (GEMV, split K)
             assert qf.w8a16_mm_argmax(x, wl, s, N - num_pad, offset, None, layout) is None
@@ -114,3 +115,41 @@ def test_int8_top_tokens_matches_two_step(oracle):
         two = P.top_tokens(P.int8_logits(head, hs), 64, 100)
         torch.cuda.synchronize()
         assert torch.equal(ids, two) and torch.equal(dflt, two)
+
+
+@pytest.mark.parametrize("layout", [qf.TILED, qf.ROWMAJOR])
+def test_signed_zero_tie_and_negative_logits(oracle, layout):
+    """-0.0 and +0.0 are equal maxima (the first index wins, as in torch.argmax), and a row whose logits are
+    all negative picks the least negative one."""
+    N, K, M = 3000, 512, 2
+    g = torch.Generator(device=DEV)
+    g.manual_seed(17)
+    w = torch.full((N, K), 127, dtype=torch.int8, device=DEV)
+    w[5] = 0
+    w[9] = 0
+    s = torch.full((N,), -0.01, dtype=torch.float32, device=DEV)
+    s[9] = 0.01                       # column 9: +0.0; column 5: -0.0 (a zero sum times a negative scale)
+    wl = qf.to_tiled(w.t()) if layout == qf.TILED else w.t()
+    x = (torch.rand(M, K, device=DEV, generator=g) + 0.1).to(torch.bfloat16)
+    y = qf.w8a16_mm(x, wl, s, None, torch.bfloat16, layout)
+    torch.cuda.synchronize()
+    yb = y.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert (yb[:, 5] == 0x8000).all() and (yb[:, 9] == 0).all()
+    ref = qf.top_tokens(y, 0, 0)
+    assert ref.cpu().tolist() == [5] * M
+    ids = qf.w8a16_mm_argmax(x, wl, s, N, 0, None, layout)
+    if ids is None:
+        pytest.skip("no fused epilogue for this configuration")
+    assert torch.equal(ids, ref)
+    # all logits negative: random positive weights, negative scales
+    w2 = torch.randint(1, 128, (N, K), dtype=torch.int8, device=DEV, generator=g)
+    s2 = -(torch.rand(N, device=DEV, generator=g) * 0.002 + 1e-4).float()
+    wl2 = qf.to_tiled(w2.t()) if layout == qf.TILED else w2.t()
+    y2 = qf.w8a16_mm(x, wl2, s2, None, torch.bfloat16, layout)
+    torch.cuda.synchronize()
+    assert (y2.float() < 0).all()
+    ref2 = qf.top_tokens(y2, 0, 3)
+    y2b = y2.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(ref2.cpu().numpy(), _ref_ids(y2b, N, 3, oracle))
+    ids2 = qf.w8a16_mm_argmax(x, wl2, s2, N, 3, None, layout)
+    assert torch.equal(ids2, ref2)
