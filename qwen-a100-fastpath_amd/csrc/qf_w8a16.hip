@@ -49,7 +49,8 @@ struct GemmArgs {
   const float* scale;
   void* y;
   float* partial;      // [split_k][M][n_pad] fp32 when split_k > 1
-  unsigned* counters;  // [grid.x] arrival counters (MFMA, split_k > 1): zero on entry and on exit
+  unsigned* counters;  // arrival counters (split_k > 1), counter_stride words apart: zero on entry and on exit
+  int counter_stride;
   int64_t ldx;
   int64_t ldw;
   int64_t ldy;
@@ -734,7 +735,7 @@ __global__ void __launch_bounds__(WN * WK * kWave)
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(a.counters + blockIdx.x, 1u, __ATOMIC_RELAXED,
+    const unsigned prev = __hip_atomic_fetch_add(a.counters + blockIdx.x * a.counter_stride, 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
     last_arrival = prev == (unsigned)(a.split_k - 1);
   }
@@ -760,7 +761,8 @@ __global__ void __launch_bounds__(WN * WK * kWave)
       }
     }
   }
-  if (threadIdx.x == 0) __hip_atomic_store(a.counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0)
+    __hip_atomic_store(a.counters + blockIdx.x * a.counter_stride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1682,7 +1684,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
     if (threadIdx.x == 0) {
-      const unsigned prev = __hip_atomic_fetch_add(a.counters + l, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const unsigned prev =
+          __hip_atomic_fetch_add(a.counters + l * a.counter_stride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       last_arrival = prev == (unsigned)(a.split_k - 1);
     }
     __syncthreads();
@@ -1701,7 +1704,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
                                  (int)(uint32_t)(hi >> 32)};
         }
     }
-    if (threadIdx.x == 0) __hip_atomic_store(a.counters + l, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0)
+      __hip_atomic_store(a.counters + l * a.counter_stride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   // Lane (g, r) holds C[n = 16 (tile0 + FA wn + i) + 4 g + e][m = m0 + 16 FB wm + 16 j + r], e = 0..3.
@@ -2950,6 +2954,16 @@ int launch(KernelFn fn, dim3 grid, dim3 block, size_t smem, hipStream_t stream, 
   return QF_OK;
 }
 
+// Words between the arrival counters of n workgroup groups: spread over the counter prefix (up to 1 KiB apart),
+// since atomics on nearby addresses share a memory channel (measured on the fused argmax: 64 slots 64 bytes apart
+// cost 11 us on 9496 workgroups, 1 KiB apart about 3).
+int counter_stride_for(int n) {
+  int st = QF_W8A16_COUNTER_BYTES / 4 / (n > 0 ? n : 1);
+  st = st < 256 ? st : 256;
+  while (st & (st - 1)) st &= st - 1;
+  return st > 0 ? st : 1;
+}
+
 struct ArgmaxRequest {
   int n_valid;
   int64_t index_offset;
@@ -2987,6 +3001,7 @@ int run_gemm(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, int l
   a.scale = scale;
   a.y = y;
   a.counters = reinterpret_cast<unsigned*>(workspace);
+  a.counter_stride = counter_stride_for(workgroups(c, N));
   a.partial = need > 0 && am == nullptr
                   ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + QF_W8A16_COUNTER_BYTES)
                   : nullptr;
@@ -3392,6 +3407,7 @@ int run_w8a8(const int8_t* xq, int64_t ldq, int x_tiled, const float* s_a, const
   a.partial = need > 0 ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + QF_W8A16_COUNTER_BYTES)
                        : nullptr;
   a.counters = need > 0 ? reinterpret_cast<unsigned*>(workspace) : nullptr;
+  a.counter_stride = 1;
   a.ldx = ldq;
   a.ldw = ldw;
   a.ldy = ldy;
@@ -3419,6 +3435,8 @@ int run_w8a8(const int8_t* xq, int64_t ldq, int x_tiled, const float* s_a, const
       al.scale = a.scale + p.n0;
       al.y = reinterpret_cast<uint8_t*>(a.y) + (size_t)p.n0 * (a.out_f32 ? 4 : 2);
     }
+    if (p.kind == kW8a8Tile || p.kind == kW8a8TileHalf || p.kind == kW8a8TileSmall)
+      al.counter_stride = counter_stride_for((int)(p.grid / (a.split_k > 0 ? a.split_k : 1)));
     int st = QF_ERR_UNSUPPORTED;
     switch (p.kind) {
       case kW8a8Tile:
