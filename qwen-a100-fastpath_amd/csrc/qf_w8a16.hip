@@ -336,9 +336,9 @@ __host__ __device__ __forceinline__ int x_pitch(int steps) { return steps * kSte
 // issued first).  Larger slices are copied by copy_all() before the weight requests.
 // Pieces are indexed (row << shift) | column, the column space padded to a power of two, so row and
 // column come from a shift and a mask.
-template <int THREADS>
+template <int THREADS, int BATCH = 10>
 struct XStage {
-  static constexpr int kBatch = 10;  // pieces per thread requested before the first LDS write
+  static constexpr int kBatch = BATCH;  // pieces per thread requested before the first LDS write
   u32x4_t v[kBatch];
   const uint16_t* src0;
   int row_pieces, shift, mask, span, pitch;
@@ -825,7 +825,8 @@ __global__ void __launch_bounds__(W * kWave) w8a16_stream_kernel(const GemmArgs 
   };
 
   u32x4_t buf[RING];
-  XStage<W * kWave> xst(a, 0, ksteps);
+  // 16 pieces a thread at 8 wavefronts (10 at 16): one batch stages M = 8 rows of K = 5120 or 8192
+  XStage<W * kWave, W >= 16 ? 10 : 16> xst(a, 0, ksteps);
   auto prologue = [&]() {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
@@ -839,9 +840,10 @@ __global__ void __launch_bounds__(W * kWave) w8a16_stream_kernel(const GemmArgs 
     prologue();
     __builtin_amdgcn_sched_barrier(0);
     xst.store_batch(smem, 0);
-  } else {
-    xst.copy_all(a, smem);
+  } else {  // larger slices: the weight requests first, so they are in flight while x is staged
     prologue();
+    __builtin_amdgcn_sched_barrier(0);
+    xst.copy_all(a, smem);
   }
   lds_barrier();  // the weight requests issued above stay in flight across it
   if constexpr (NORM) normalise_staged_rows<W>(smem, pitch, a.M, a.K, a.norm_eps);
