@@ -678,9 +678,11 @@ __global__ void __launch_bounds__(WN * WK * kWave)
   // Lane (g, r) of slice 0 holds C[n = tile*16 + 4g + i][m = r], i = 0..3.
   const bool holder = wk == 0 && tile0 < ntiles && r < a.M;
   if (a.split_k == 1) {
-    if (a.argmax) {
-      argmax_epilogue<NT, WN>(a, acc, holder, tile0, ntiles, g, wk, wn, lane);
-      return;
+    if constexpr (!NORM) {  // the normalising builds serve qf_w8a16_gemm_rmsnorm only, never the fused argmax
+      if (a.argmax) {
+        argmax_epilogue<NT, WN>(a, acc, holder, tile0, ntiles, g, wk, wn, lane);
+        return;
+      }
     }
     if (holder) {
 #pragma unroll
