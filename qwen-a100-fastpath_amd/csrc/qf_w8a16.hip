@@ -40,6 +40,16 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 constexpr int kWave = 64;
 constexpr int kTileN = 16;     // output channels per MFMA tile
 constexpr int kStepK = 64;     // k covered by one 16-byte-per-lane weight fragment of a tile
+constexpr int kXcds = 8;       // accelerator complexes (XCDs) of an MI355X
+
+// The hardware hands workgroup i of a launch to XCD i % kXcds.  xcd_major(i, total) renumbers the
+// workgroups XCD by XCD: the workgroups of one XCD (i, i + kXcds, i + 2 kXcds, ...) get consecutive
+// indices, XCD 0's first.  A bijection of [0, total) for any total.
+__device__ __forceinline__ int xcd_major(int i, int total) {
+  const int xcd = i % kXcds, j = i / kXcds;
+  const int per = total / kXcds, rem = total % kXcds;
+  return xcd < rem ? xcd * (per + 1) + j : rem * (per + 1) + (xcd - rem) * per + j;
+}
 constexpr size_t kMaxLds = 160 * 1024 - 256;  // gfx950 LDS per workgroup; static __shared__ uses the rest
 constexpr size_t kDefaultLds = 64 * 1024;      // above this a kernel needs the dynamic-LDS attribute raised
 
@@ -994,8 +1004,6 @@ __global__ void __launch_bounds__(W * kWave) w8a16_stream_xreg_kernel(const Gemm
 // consecutive workgroups of one XCD, so they run together and all but the first find the block's
 // weights in that XCD's L2.
 // ---------------------------------------------------------------------------------------------
-constexpr int kXcds = 8;  // accelerator complexes of an MI355X
-
 template <int NT, int MT, int WN, int DEPTH>
 __global__ void __launch_bounds__(WN * kWave) w8a16_wide_kernel(const GemmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
@@ -1023,10 +1031,7 @@ __global__ void __launch_bounds__(WN * kWave) w8a16_wide_kernel(const GemmArgs a
   const int nblocks = (ntiles + WN * NT - 1) / (WN * NT);
   int l = blockIdx.x;
   if (a.groups > 1) {
-    const int total = gridDim.x;
-    const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
-    const int per = total / kXcds, rem = total % kXcds;
-    l = xcd < rem ? xcd * (per + 1) + j : rem * (per + 1) + (xcd - rem) * per + j;
+    l = xcd_major(blockIdx.x, gridDim.x);
   }
   const int grp = l % a.groups;
   const int nb = (l / a.groups) % nblocks;
@@ -1226,12 +1231,7 @@ __global__ void __launch_bounds__(256) quantize_tokens_kernel(const uint16_t* x,
                                                               int64_t ldq, float* s_a, int M, int tiled) {
   __shared__ float red[256 / kWave];
   int64_t m = blockIdx.x;
-  if (tiled) {  // consecutive rows on one XCD
-    const int total = gridDim.x;
-    const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
-    const int per = total / kXcds, rem = total % kXcds;
-    m = xcd < rem ? xcd * (per + 1) + j : rem * (per + 1) + (xcd - rem) * per + j;
-  }
+  if (tiled) m = xcd_major(blockIdx.x, gridDim.x);  // consecutive rows on one XCD
   const int pieces = K / 8;
   if (m >= M) {  // tiled only: a padding row of the last token block
     for (int c = threadIdx.x; c < pieces; c += 256)
@@ -1304,10 +1304,7 @@ __global__ void __launch_bounds__(WN * kWave) w8a8_wide_kernel(const GemmArgs a)
   const int nblocks = (ntiles + WN * NT - 1) / (WN * NT);
   int l = blockIdx.x;
   if (a.groups > 1) {  // the groups of one (split, n-block) on consecutive workgroups of one XCD
-    const int total = gridDim.x;
-    const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
-    const int per = total / kXcds, rem = total % kXcds;
-    l = xcd < rem ? xcd * (per + 1) + j : rem * (per + 1) + (xcd - rem) * per + j;
+    l = xcd_major(blockIdx.x, gridDim.x);
   }
   const int grp = l % a.groups;
   const int nb = (l / a.groups) % nblocks;
@@ -1540,13 +1537,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int mblocks = (a.M + T::rows - 1) / T::rows;
   // The hardware hands workgroup i to XCD i % kXcds; consecutive logical blocks share an XCD, so the
   // token blocks of one channel block run together and share its weights in that XCD's L2.
-  int l;
-  {
-    const int total = gridDim.x;
-    const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
-    const int per = total / kXcds, rem = total % kXcds;
-    l = xcd < rem ? xcd * (per + 1) + j : rem * (per + 1) + (xcd - rem) * per + j;
-  }
+  int l = xcd_major(blockIdx.x, gridDim.x);
   // split_k > 1: the grid is split_k copies of the tile grid, copy `split` computing k-steps
   // [s_begin, s_end) of every tile.
   const int tiles_grid = gridDim.x / a.split_k;
