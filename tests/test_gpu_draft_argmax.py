@@ -35,7 +35,7 @@ def _ref_ids(y_bits, n_valid, offset, oracle):
 
 
 @pytest.mark.parametrize("layout", [qf.TILED, qf.ROWMAJOR])
-@pytest.mark.parametrize("M", [1, 2, 4, 7, 8, 12])
+@pytest.mark.parametrize("M", [1, 2, 4, 7, 8, 12, 16])
 @pytest.mark.parametrize("N,K", [(151936, 5120), (5000, 1024), (1000, 256)])
 def test_fused_ids_equal_unfused(oracle, layout, M, N, K):
     w, s = _head(N, K, seed=N + M)
