@@ -228,9 +228,11 @@ int qf_scale_cast_bf16(const float* acc, int64_t lda, const float* scale, int M,
 
 /* y[m, :] = bf16_rne(x[m, :] * (1 / sqrt(mean_k(x[m, k]^2) + eps))) for m < M: each row of a bf16 [M, N] matrix
  * (row stride ldx) scaled to unit RMS, into y (row stride ldy; y may be x).  The sum of squares is formed in a
- * fixed order (the row as N / 8 pieces of 8 values; lane t of a wavefront sums pieces t, t + 64, ... with fused
- * multiply-adds, then a butterfly over the 64 lanes), the same order qf_w8a16_gemm_rmsnorm uses, so results are
- * reproducible; against torch's fp32 rms_norm of the same rows they differ by at most one bf16 ulp.  N % 8 == 0,
+ * fixed order (the row as N / 8 pieces of 8 values; lane t of a wavefront takes pieces t, t + 64, ... and keeps
+ * one fp32 sum per value position, each over its pieces in order with fused multiply-adds; the eight sums add as a
+ * balanced tree, and the 64 lane sums fold within 16-lane rows, then across the four rows), the same order
+ * qf_w8a16_gemm_rmsnorm uses, so results are reproducible; against torch's fp32 rms_norm of the same rows they
+ * differ by at most one bf16 ulp.  N % 8 == 0,
  * x and y 16-byte aligned, ldx % 8 == 0 and ldy % 8 == 0, else QF_ERR_UNSUPPORTED.  No reference
  * counterpart: the re-normalisation between the layers of the 64-layer decode-step benchmark (each layer's
  * output to unit RMS as the next layer's input). */

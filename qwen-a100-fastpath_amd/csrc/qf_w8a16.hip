@@ -50,8 +50,9 @@ __device__ __forceinline__ int xcd_major(int i, int total) {
   const int per = total / kXcds, rem = total % kXcds;
   return xcd < rem ? xcd * (per + 1) + j : rem * (per + 1) + (xcd - rem) * per + j;
 }
-constexpr size_t kMaxLds = 160 * 1024 - 256;  // gfx950 LDS per workgroup; static __shared__ uses the rest
-constexpr size_t kDefaultLds = 64 * 1024;      // above this a kernel needs the dynamic-LDS attribute raised
+constexpr size_t kLdsPerWorkgroup = 160 * 1024;     // gfx950 LDS per workgroup
+constexpr size_t kMaxLds = kLdsPerWorkgroup - 256;  // the dynamic budget; static __shared__ uses the rest
+constexpr size_t kDefaultLds = 64 * 1024;           // above this a kernel needs the dynamic-LDS attribute raised
 
 struct GemmArgs {
   const uint16_t* x;
@@ -240,9 +241,12 @@ __device__ __forceinline__ void lds_barrier() {
 
 // Row normalisation to unit RMS, in one canonical order shared by qf_rms_norm_rows_bf16 and the GEMMs that
 // normalise their staged x (qf_w8a16_gemm_rmsnorm), so that both give the same bits.  A row of N bf16 values is
-// read as N / 8 pieces of 16 bytes.  Lane t of one wavefront sums the squares of pieces t, t + 64, t + 128, ...
-// in that order (each piece's 8 values in order, one fused multiply-add each); the 64 lane sums then fold by a
-// butterfly of xor shuffles (32, 16, ..., 1), after which every lane holds the same total.
+// read as N / 8 pieces of 16 bytes, and lane t of one wavefront takes pieces t, t + 64, t + 128, ...  The lane
+// keeps eight sums, one per value position in a piece, each adding the squares of its values over the lane's
+// pieces in increasing order with fused multiply-adds (eight independent chains, N / 512 long); the lane's sum is
+// ((a0 + a1) + (a2 + a3)) + ((a4 + a5) + (a6 + a7)).  The 64 lane sums fold within each 16-lane row by DPP adds
+// (the neighbour, the other pair of the quad, the other quad of the 8 lanes, the other 8 lanes), and the four row
+// sums r0..r3 (lanes 0, 16, 32, 48) add as (r0 + r1) + (r2 + r3).  Every step is an IEEE fp32 operation.
 
 // 1 / sqrt(mean of squares + eps) (IEEE division; the same instructions wherever it is used).
 __device__ __forceinline__ float rms_inv(float total, int n, float eps) {
@@ -258,21 +262,59 @@ __device__ __forceinline__ u32x4_t scale_piece(const u32x4_t v, float inv) {
   return o;
 }
 
+// Adds the squares of one piece's 8 values to the lane's eight sums (value e of the piece into sum e).
+__device__ __forceinline__ void add_squares(float (&acc)[8], const u32x4_t x) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float lo = __uint_as_float(x[e] << 16), hi = __uint_as_float(x[e] & 0xffff0000u);
+    acc[2 * e] = __builtin_fmaf(lo, lo, acc[2 * e]);
+    acc[2 * e + 1] = __builtin_fmaf(hi, hi, acc[2 * e + 1]);
+  }
+}
+
+// Continues the lane's sums over the pieces base + 64 p + lane, for base = base0, base0 + 64 P, ... below npieces,
+// read P at a time (the P loads issued before their multiply-adds).  base0 is the same for every lane, so the
+// loop is uniform; a lane past the row's end adds zeros, which leaves its sums unchanged.
+template <int P, typename Load>
+__device__ __forceinline__ void add_row_squares(float (&acc)[8], int base0, int npieces, int lane, Load load) {
+  for (int base = base0; base < npieces; base += P * kWave) {
+    u32x4_t t[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int j = base + p * kWave + lane;
+      t[p] = j < npieces ? load(j) : (u32x4_t){0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+      if (base + p * kWave < npieces) add_squares(acc, t[p]);
+  }
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_fold(float v) {
+  return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+
+// The row's sum of squares from the lanes' eight sums (every lane of the wavefront active); every lane returns it.
+__device__ __forceinline__ float wave_square_total(const float (&a)[8]) {
+  float s = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+  s = dpp_fold<0xb1>(s);   // quad_perm [1, 0, 3, 2]: the neighbour
+  s = dpp_fold<0x4e>(s);   // quad_perm [2, 3, 0, 1]: the other pair of the quad
+  s = dpp_fold<0x141>(s);  // row_half_mirror: the other quad of each 8 lanes
+  s = dpp_fold<0x140>(s);  // row_mirror: the other 8 lanes of each 16-lane row
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 // One row of npieces pieces normalised by one wavefront in the canonical order, through load(j) and
-// store(j, piece).  The lane's pieces are read P at a time (the P loads issued before their multiply-adds); its
-// first P pieces stay in registers for the scaling pass, later ones are read again.  Each piece is read and
-// written by its own lane only, so y may be x.
+// store(j, piece).  The lane's first P pieces stay in registers for the scaling pass, later ones are read again.
+// Each piece is read and written by its own lane only, so y may be x.
 template <int P, typename Load, typename Store>
 __device__ __forceinline__ void normalise_row(int npieces, int n, float eps, int lane, Load load, Store store) {
-  float ss = 0.f;
-  auto add = [&](const u32x4_t x) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float lo = __uint_as_float(x[e] << 16), hi = __uint_as_float(x[e] & 0xffff0000u);
-      ss = __builtin_fmaf(lo, lo, ss);
-      ss = __builtin_fmaf(hi, hi, ss);
-    }
-  };
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   u32x4_t v[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
@@ -281,21 +323,9 @@ __device__ __forceinline__ void normalise_row(int npieces, int n, float eps, int
   }
 #pragma unroll
   for (int p = 0; p < P; ++p)
-    if (p * kWave + lane < npieces) add(v[p]);
-  for (int j0 = P * kWave + lane; j0 < npieces; j0 += P * kWave) {
-    u32x4_t t[P];
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int j = j0 + p * kWave;
-      t[p] = j < npieces ? load(j) : (u32x4_t){0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int p = 0; p < P; ++p)
-      if (j0 + p * kWave < npieces) add(t[p]);
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, kWave);
-  const float inv = rms_inv(ss, n, eps);
+    if (p * kWave < npieces) add_squares(acc, v[p]);
+  add_row_squares<P>(acc, P * kWave, npieces, lane, load);
+  const float inv = rms_inv(wave_square_total(acc), n, eps);
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int j = p * kWave + lane;
@@ -316,21 +346,58 @@ __device__ __forceinline__ void normalise_row(int npieces, int n, float eps, int
   }
 }
 
-// Normalise the M staged rows of x in LDS (row m at byte m * pitch, K values) in place: wavefront w normalises
-// the rows w, w + WAVES, ... (normalise_row, 3 pieces a lane at a time: the one-tile MFMA kernels that call this
-// run within 80 VGPRs beside their weight prefetch ring, and 4 would spill), then one LDS-only barrier, so the
-// prefetch stays in flight.
-// Called by the whole workgroup after the staging barrier.
-constexpr int kStagedNormPieces = 3;
+// Normalise the M staged rows of x in LDS (row m at byte m * pitch, K values) in place, in two passes between
+// LDS-only barriers (the weight prefetch stays in flight across them):
+// * the sums: wavefront w takes the rows w, w + WAVES, ..., each in the canonical order (the lane's pieces read
+//   kStagedSumPieces at a time), and writes the row's scale factor to LDS;
+// * the scaling, which has no order: piece q of the rows' M x K / 8 pieces (row-major) goes to thread
+//   q mod (WAVES x 64), so every wavefront scales the same share whatever M is; each thread reads
+//   kStagedScalePieces pieces before it scales and writes them (a read past the last piece is clamped to the last
+//   row's first piece and not written back).
+// Called by the whole workgroup after the staging barrier.  Both passes are bound by one wavefront's
+// instruction issue (about one VALU instruction per 5.5 cycles on its own), not by the SIMD's throughput: the
+// batches put all of a lane's loads for K = 5120 ahead of its arithmetic.
+constexpr int kStagedSumPieces = 10;
+constexpr int kStagedScalePieces = 8;
 template <int WAVES>
 __device__ __forceinline__ void normalise_staged_rows(uint8_t* smem, int pitch, int M, int K, float eps) {
+  __shared__ float row_inv[QF_W8A16_MAX_M];
+  constexpr int THREADS = WAVES * kWave;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  for (int m = wave; m < M; m += WAVES) {
-    uint8_t* row = smem + m * pitch;
-    normalise_row<kStagedNormPieces>(
-        K / 8, K, eps, lane, [&](int j) { return *reinterpret_cast<const u32x4_t*>(row + j * 16); },
-        [&](int j, const u32x4_t o) { *reinterpret_cast<u32x4_t*>(row + j * 16) = o; });
+  const int npieces = K / 8;
+  for (int m = wave; m < M; m += WAVES) {  // uniform over the wavefront
+    const uint8_t* row = smem + m * pitch;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    add_row_squares<kStagedSumPieces>(acc, 0, npieces, lane,
+                                      [&](int j) { return *reinterpret_cast<const u32x4_t*>(row + j * 16); });
+    const float inv = rms_inv(wave_square_total(acc), K, eps);
+    if (lane == 0) row_inv[m] = inv;
+  }
+  lds_barrier();
+  // (m, j): the thread's next piece; a step of THREADS pieces is dm rows and dj pieces.
+  const int total = M * npieces;
+  const int dm = THREADS / npieces, dj = THREADS - dm * npieces;
+  int m = (int)threadIdx.x / npieces;
+  int j = (int)threadIdx.x - m * npieces;
+  for (int q0 = threadIdx.x; q0 < total; q0 += kStagedScalePieces * THREADS) {
+    u32x4_t t[kStagedScalePieces];
+    int off[kStagedScalePieces];
+    float inv[kStagedScalePieces];
+#pragma unroll
+    for (int p = 0; p < kStagedScalePieces; ++p) {
+      const bool in = q0 + p * THREADS < total;
+      const int mm = in ? m : M - 1;
+      off[p] = mm * pitch + (in ? j : 0) * 16;
+      t[p] = *reinterpret_cast<const u32x4_t*>(smem + off[p]);
+      inv[p] = row_inv[mm];
+      m += dm;
+      j += dj;
+      if (j >= npieces) j -= npieces, ++m;
+    }
+#pragma unroll
+    for (int p = 0; p < kStagedScalePieces; ++p)
+      if (q0 + p * THREADS < total) *reinterpret_cast<u32x4_t*>(smem + off[p]) = scale_piece(t[p], inv[p]);
   }
   lds_barrier();
 }
@@ -495,16 +562,19 @@ __global__ void __launch_bounds__(kWave) argmax_slots_kernel(uint64_t* slots, in
 // Occupancy floor of the MFMA kernel.  One-tile, DEPTH-4 wavefronts fit in 80 VGPRs (the compiler's
 // own choice is 84-92), which allows 6 wavefronts per SIMD instead of 5: three 8-wavefront workgroups
 // per CU where the x slice leaves LDS for three (gate_up 34816x5120 at M = 5, 1088 workgroups, then
-// runs in 1.4 rounds instead of 2.1: 33.05 -> 32.43 us, results unchanged).  Other shapes keep the
-// compiler's allocation: forcing them to 6 wavefronts makes them spill.
-template <int NT, int DEPTH, int WAVES>
+// runs in 1.4 rounds instead of 2.1: 33.05 -> 32.43 us, results unchanged).  The normalising builds
+// (NORM) take a floor of 5 (96 VGPRs), room for the staged rows' loads in flight beside the ring; the
+// shapes that select them run at most 2.5 wavefronts a SIMD (qkv 10240x5120: 160 workgroups of 8
+// wavefronts at M = 5, 640 of 4 at M = 1).  Other shapes keep the compiler's allocation: forcing them
+// to 6 wavefronts makes them spill.
+template <int NT, int DEPTH, int WAVES, bool NORM = false>
 struct MfmaMinWaves {
-  static constexpr int value = (NT == 1 && DEPTH == 4) ? 6 : (WAVES >= 8 ? 2 : 1);
+  static constexpr int value = (NT == 1 && DEPTH == 4) ? (NORM ? 5 : 6) : (WAVES >= 8 ? 2 : 1);
 };
 
 template <int LAYOUT, int NT, int WN, int WK, int DEPTH, bool NTH, bool XRING, bool NORM = false>
 __global__ void __launch_bounds__(WN * WK * kWave)
-    __attribute__((amdgpu_waves_per_eu(MfmaMinWaves<NT, DEPTH, WN * WK>::value, 8)))
+    __attribute__((amdgpu_waves_per_eu(MfmaMinWaves<NT, DEPTH, WN * WK, NORM>::value, 8)))
     w8a16_mfma_kernel(const GemmArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ int last_arrival;
@@ -2939,7 +3009,12 @@ int launch(KernelFn fn, dim3 grid, dim3 block, size_t smem, hipStream_t stream, 
     std::lock_guard<std::mutex> lock(g_lds_mutex);
     const void* key = reinterpret_cast<const void*>(fn);
     if (g_lds_raised.find(key) == g_lds_raised.end()) {
-      if (hipFuncSetAttribute(key, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds) != hipSuccess)
+      // The limit is what the kernel's own static LDS leaves of the workgroup's 160 KiB.
+      hipFuncAttributes attr;
+      if (hipFuncGetAttributes(&attr, key) != hipSuccess) return QF_ERR_HIP;
+      const size_t room = kLdsPerWorkgroup - attr.sharedSizeBytes;
+      if (smem > room) return QF_ERR_UNSUPPORTED;
+      if (hipFuncSetAttribute(key, hipFuncAttributeMaxDynamicSharedMemorySize, (int)room) != hipSuccess)
         return QF_ERR_HIP;
       g_lds_raised.insert(key);
     }

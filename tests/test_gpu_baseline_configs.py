@@ -220,6 +220,9 @@ def test_rms_norm_rows(M, N):
     (16, 4096, 2048, (2, 1, 1, 8, 4, 1, 1, 0)),   # 8 x 1
     (7, 1000, 4096, (2, 1, 1, 8, 4, 1, 4, 0)),    # 2 x 4, ragged N
     (5, 2000, 17408, None),                       # a K split: the two calls instead
+    (16, 100, 64, (2, 1, 1, 8, 4, 1, 1, 0)),      # 8 x 1, one k-step: a thread's scaled pieces span several rows
+    (9, 300, 256, (2, 1, 1, 4, 4, 1, 4, 0)),      # 1 x 4: 9 rows' sums on 4 wavefronts
+    (8, 34816, 5120, None),                       # the stream kernel at its widest x-in-LDS row count
 ])
 def test_gemm_rmsnorm_bitwise(M, N, K, cfg):
     """qf_w8a16_gemm_rmsnorm (the staged rows normalised inside the GEMM) equals qf_rms_norm_rows_bf16 followed by
