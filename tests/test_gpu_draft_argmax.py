@@ -153,3 +153,36 @@ def test_signed_zero_tie_and_negative_logits(oracle, layout):
     assert np.array_equal(ref2.cpu().numpy(), _ref_ids(y2b, N, 3, oracle))
     ids2 = qf.w8a16_mm_argmax(x, wl2, s2, N, 3, None, layout)
     assert torch.equal(ids2, ref2)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 151936, 5120), (16, 151936, 5120), (7, 1000, 4096), (5, 5000, 1024)])
+def test_caller_workspace_prefix_back_at_zero(M, N, K):
+    """Through the C ABI with a caller workspace: after every call the counter prefix (the per-token slots) is all
+    zero again, and bytes past the prefix (split-K partials of earlier calls on a shared workspace) do not matter;
+    grids of more and fewer workgroups than slots."""
+    import ctypes
+    from qwen_fastpath import _lib as L
+    lib = L.load()
+    w, s = _head(N, K, seed=M + N)
+    wl = qf.to_tiled(w.t())
+    g = torch.Generator(device=DEV)
+    g.manual_seed(K)
+    x = torch.randn(M, K, device=DEV, generator=g).to(torch.bfloat16)
+    n_valid = N - 64
+    ref = qf.top_tokens(qf.w8a16_mm(x, wl, s, None, torch.bfloat16, qf.TILED), 64, 11)
+    cfg = L.Config.from_seq((0,) * 8)
+    need = int(lib.qf_w8a16_argmax_workspace_bytes(M, N, K, qf.TILED, ctypes.byref(cfg)))
+    assert need == L.COUNTER_BYTES
+    ws = torch.full((need + (1 << 20),), 0xA5, dtype=torch.uint8, device=DEV)
+    ws[:L.COUNTER_BYTES].zero_()
+    stream = torch.cuda.current_stream().cuda_stream
+    print(f"argmax workspace M={M} N={N} K={K}", flush=True)
+    for rep in range(3):
+        ids = torch.full((M,), -1, dtype=torch.int64, device=DEV)
+        rc = lib.qf_w8a16_gemm_argmax(x.data_ptr(), K, wl.data_ptr(), K, qf.TILED, s.data_ptr(), None, N,
+                                      L.DTYPE_BF16, M, N, K, n_valid, 11, ids.data_ptr(), ctypes.byref(cfg),
+                                      ws.data_ptr(), ws.numel(), stream)
+        assert rc == L.OK, rc
+        torch.cuda.synchronize()
+        assert torch.equal(ids, ref), (rep, ids.tolist(), ref.tolist())
+        assert int(torch.count_nonzero(ws[:L.COUNTER_BYTES])) == 0, rep
