@@ -364,9 +364,9 @@ __device__ __forceinline__ void normalise_staged_rows(uint8_t* smem, int pitch, 
   __shared__ float row_inv[QF_W8A16_MAX_M];
   constexpr int THREADS = WAVES * kWave;
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // uniform: the row fold needs every lane
   const int npieces = K / 8;
-  for (int m = wave; m < M; m += WAVES) {  // uniform over the wavefront
+  for (int m = wave; m < M; m += WAVES) {
     const uint8_t* row = smem + m * pitch;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     add_row_squares<kStagedSumPieces>(acc, 0, npieces, lane,
