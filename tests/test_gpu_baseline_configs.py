@@ -186,7 +186,7 @@ def test_stack64_graph_replay_and_sampled_layers(oracle):
 
 
 @pytest.mark.parametrize("M,N", [(5, 5120), (1, 8), (7, 8192), (16, 4096), (3, 17408 // 8 * 8 // 4), (5, 17408),
-                                 (2, 34816)])
+                                 (2, 34816), (64, 5120), (200, 1024)])
 def test_rms_norm_rows(M, N):
     """The stack's glue (qf_rms_norm_rows_bf16) against torch's fp32 restatement and torch's rms_norm (eps 2^-23,
     torch's default for bf16 inputs), also with eps 2^-7: at most one bf16 ulp apart; reproducible; in place equal
